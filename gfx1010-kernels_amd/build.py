@@ -1,0 +1,139 @@
+"""Build the MI355X residual LayerNorm native code in-tree.
+
+Produces, inside ``gfx1010_kernels/``:
+
+* ``librln_gfx950.so`` - the HIP kernels for gfx950 and the C ABI declared in
+  ``include/rln.h`` (hipcc, device code for gfx950 only);
+* ``_C<EXT_SUFFIX>`` - the PyTorch glue module (g++, host code only), linked
+  against ``librln_gfx950.so`` with an ``$ORIGIN`` run path.
+
+Run ``python gfx1010-kernels_amd/build.py`` or call :func:`build`.
+"""
+
+from __future__ import annotations
+
+import os
+import shlex
+import subprocess
+import sys
+import sysconfig
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+REPO = ROOT.parent
+PACKAGE = ROOT / "gfx1010_kernels"
+INCLUDE = REPO / "include"
+CSRC = ROOT / "csrc"
+ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+ARCH = "gfx950"
+LIBRARY = PACKAGE / f"librln_{ARCH}.so"
+GLUE = PACKAGE / f"_C{sysconfig.get_config_var('EXT_SUFFIX')}"
+
+# Device-code flags. Packed fp32 instructions are disabled (the compiler may
+# otherwise form v_pk_{add,mul,fma}_f32 from float code); FP contraction is
+# off so that the bit-exact residual update is never fused into an FMA.
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-ffp-contract=off",
+    "-mcode-object-version=5",
+    "-Xclang",
+    "-target-feature",
+    "-Xclang",
+    "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def _run(command: list[str]) -> None:
+    printable = " ".join(shlex.quote(part) for part in command)
+    result = subprocess.run(command, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(
+            f"build step failed ({result.returncode}): {printable}\n"
+            f"{result.stdout}\n{result.stderr}"
+        )
+
+
+def build_library() -> Path:
+    """Compile the gfx950 kernels and C ABI into librln_gfx950.so."""
+    hipcc = str(ROCM / "bin" / "hipcc")
+    temporary = LIBRARY.with_name(LIBRARY.name + ".tmp")
+    _run(
+        [hipcc, *HIP_FLAGS, f"-I{INCLUDE}", str(CSRC / "rln_kernels.hip"),
+         f"-Wl,-soname,{LIBRARY.name}", "-o", str(temporary)]
+    )
+    os.replace(temporary, LIBRARY)
+    return LIBRARY
+
+
+def _torch_paths() -> tuple[list[str], Path, bool]:
+    import torch
+    from torch.utils import cpp_extension
+
+    return (
+        cpp_extension.include_paths(),
+        Path(torch.__file__).resolve().parent / "lib",
+        bool(torch.compiled_with_cxx11_abi()),
+    )
+
+
+def build_glue() -> Path:
+    """Compile the torch glue module linked against librln_gfx950.so."""
+    includes, torch_lib, cxx11_abi = _torch_paths()
+    python_include = sysconfig.get_paths()["include"]
+    temporary = GLUE.with_name(GLUE.name + ".tmp")
+    command = [
+        "g++",
+        "-O2",
+        "-std=c++17",
+        "-fPIC",
+        "-shared",
+        "-Wall",
+        "-Wno-unused-function",
+        "-D__HIP_PLATFORM_AMD__=1",
+        "-DUSE_ROCM=1",
+        "-DTORCH_API_INCLUDE_EXTENSION_H",
+        "-DTORCH_EXTENSION_NAME=_C",
+        f"-D_GLIBCXX_USE_CXX11_ABI={1 if cxx11_abi else 0}",
+        f"-I{INCLUDE}",
+        *[f"-I{path}" for path in includes],
+        f"-I{python_include}",
+        f"-I{ROCM / 'include'}",
+        str(CSRC / "rln_torch.cpp"),
+        f"-L{torch_lib}",
+        f"-L{PACKAGE}",
+        "-lc10",
+        "-lc10_hip",
+        "-ltorch",
+        "-ltorch_cpu",
+        "-ltorch_hip",
+        "-ltorch_python",
+        f"-l:{LIBRARY.name}",
+        "-Wl,-rpath,$ORIGIN",
+        "-o",
+        str(temporary),
+    ]
+    _run(command)
+    os.replace(temporary, GLUE)
+    return GLUE
+
+
+def build() -> tuple[Path, Path]:
+    """Build both artefacts (the library first: the glue links against it)."""
+    PACKAGE.mkdir(parents=True, exist_ok=True)
+    with ThreadPoolExecutor(max_workers=1) as pool:
+        library = pool.submit(build_library).result()
+    glue = build_glue()
+    return library, glue
+
+
+if __name__ == "__main__":
+    for artefact in build():
+        print(artefact.relative_to(REPO))
+    sys.exit(0)

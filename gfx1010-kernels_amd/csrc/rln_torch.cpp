@@ -1,0 +1,464 @@
+// PyTorch glue for the MI355X residual LayerNorm C ABI (include/rln.h).
+//
+// Module `gfx1010_kernels._C`, with the three entry points of the reference's
+// binding (csrc/residual_layer_norm_bindings.cpp:131-141):
+//   residual_layer_norm(...)           autograd op returning [updated, normalized]
+//   residual_layer_norm_forward(...)   (updated, normalized, mean, rstd, mask)
+//   residual_layer_norm_backward(...)  [grad_x, grad_branch, grad_w, grad_b]
+// Argument order, return layout and error messages follow
+// csrc/residual_layer_norm.h:10-42 and the input checks at
+// csrc/residual_layer_norm_kernel.hip:26-166. The reference's launch hints
+// (threads, block_rows, parameter_threads, parameter_groups) are validated
+// with the reference's messages and otherwise ignored: the MI355X library
+// picks its own launch shape.
+//
+// This file owns what the C ABI leaves to the caller: tensor allocation on
+// the caching allocator, the device guard, the current HIP stream, the
+// deterministic-algorithms switch and the Philox (seed, offset) reservation
+// from the default HIP generator under its mutex.
+
+#include <torch/extension.h>
+#include <torch/csrc/autograd/custom_function.h>
+
+#include <ATen/Context.h>
+#include <ATen/core/Generator.h>
+#include <ATen/hip/HIPGeneratorImpl.h>
+#include <c10/hip/HIPGuard.h>
+#include <c10/hip/HIPStream.h>
+
+#include <mutex>
+#include <optional>
+#include <tuple>
+#include <vector>
+
+#include "rln.h"
+
+namespace {
+
+bool native_hidden(int64_t hidden) {
+    return rln_hidden_supported(hidden) != 0;
+}
+
+void check_status(int status) {
+    TORCH_CHECK(status == RLN_OK, rln_last_error());
+}
+
+void check_forward_inputs(
+    const at::Tensor& x,
+    const at::Tensor& branch,
+    const at::Tensor& weight,
+    const at::Tensor& bias,
+    double dropout_p,
+    double eps,
+    int64_t threads) {
+    TORCH_CHECK(x.is_cuda(), "x must be a HIP tensor");
+    TORCH_CHECK(
+        branch.is_cuda() && weight.is_cuda() && bias.is_cuda(),
+        "branch, weight and bias must be HIP tensors");
+    TORCH_CHECK(
+        x.device() == branch.device() && x.device() == weight.device()
+            && x.device() == bias.device(),
+        "all tensors must be on the same HIP device");
+    TORCH_CHECK(x.scalar_type() == at::kFloat, "x must use float32");
+    TORCH_CHECK(
+        branch.scalar_type() == at::kHalf || branch.scalar_type() == at::kFloat,
+        "branch must use float16 or float32");
+    TORCH_CHECK(
+        weight.scalar_type() == at::kFloat && bias.scalar_type() == at::kFloat,
+        "weight and bias must use float32");
+    TORCH_CHECK(x.dim() >= 2, "x must have at least two dimensions");
+    TORCH_CHECK(branch.sizes() == x.sizes(), "branch must match x");
+    const int64_t hidden = x.size(-1);
+    TORCH_CHECK(
+        weight.sizes() == at::IntArrayRef({hidden}) && bias.sizes() == at::IntArrayRef({hidden}),
+        "weight and bias must match the hidden size");
+    TORCH_CHECK(
+        x.is_contiguous() && branch.is_contiguous() && weight.is_contiguous()
+            && bias.is_contiguous(),
+        "all tensors must be contiguous");
+    TORCH_CHECK(x.numel() > 0, "empty tensors are unsupported");
+    TORCH_CHECK(native_hidden(hidden), "unsupported native hidden size: ", hidden);
+    TORCH_CHECK(
+        threads == 128 || threads == 192 || threads == 256,
+        "threads must be 128, 192 or 256");
+    TORCH_CHECK(dropout_p >= 0.0 && dropout_p < 1.0, "dropout_p must be in [0, 1)");
+    TORCH_CHECK(eps > 0.0, "eps must be positive");
+}
+
+void check_backward_inputs(
+    const std::optional<at::Tensor>& grad_updated,
+    const std::optional<at::Tensor>& grad_normalized,
+    const at::Tensor& updated,
+    const at::Tensor& weight,
+    const at::Tensor& mean,
+    const at::Tensor& rstd,
+    const at::Tensor& dropout_mask,
+    double dropout_p,
+    bool training,
+    int64_t threads,
+    int64_t block_rows,
+    int64_t parameter_threads,
+    int64_t parameter_groups) {
+    TORCH_CHECK(updated.is_cuda(), "updated must be a HIP tensor");
+    const auto device = updated.device();
+    const bool same_device = (!grad_updated || grad_updated->device() == device)
+        && (!grad_normalized || grad_normalized->device() == device)
+        && weight.device() == device && mean.device() == device && rstd.device() == device;
+    TORCH_CHECK(same_device, "all backward tensors must be on the same HIP device");
+    const bool float32 = (!grad_updated || grad_updated->scalar_type() == at::kFloat)
+        && (!grad_normalized || grad_normalized->scalar_type() == at::kFloat)
+        && updated.scalar_type() == at::kFloat && weight.scalar_type() == at::kFloat
+        && mean.scalar_type() == at::kFloat && rstd.scalar_type() == at::kFloat;
+    TORCH_CHECK(float32, "all backward tensors must use float32");
+    TORCH_CHECK(updated.dim() >= 2, "updated must have at least two dimensions");
+    TORCH_CHECK(updated.numel() > 0, "empty tensors are unsupported");
+    TORCH_CHECK(
+        (!grad_updated || grad_updated->sizes() == updated.sizes())
+            && (!grad_normalized || grad_normalized->sizes() == updated.sizes()),
+        "output gradients must match updated");
+    const int64_t hidden = updated.size(-1);
+    TORCH_CHECK(native_hidden(hidden), "unsupported native hidden size: ", hidden);
+    const int64_t rows = updated.numel() / hidden;
+    TORCH_CHECK(weight.sizes() == at::IntArrayRef({hidden}), "weight must match the hidden size");
+    TORCH_CHECK(
+        mean.numel() == rows && rstd.numel() == rows,
+        "mean and rstd must match the row count");
+    TORCH_CHECK(
+        (!grad_updated || grad_updated->is_contiguous())
+            && (!grad_normalized || grad_normalized->is_contiguous())
+            && updated.is_contiguous() && weight.is_contiguous() && mean.is_contiguous()
+            && rstd.is_contiguous(),
+        "all backward tensors must be contiguous");
+    TORCH_CHECK(
+        threads == 128 || threads == 192 || threads == 256,
+        "threads must be 128, 192 or 256");
+    TORCH_CHECK(
+        block_rows == 16 || block_rows == 32 || block_rows == 64 || block_rows == 128,
+        "block_rows must be 16, 32, 64 or 128");
+    TORCH_CHECK(
+        parameter_threads == 64 || parameter_threads == 128 || parameter_threads == 256,
+        "parameter_threads must be 64, 128 or 256");
+    TORCH_CHECK(
+        parameter_groups > 0 && parameter_groups <= rows,
+        "parameter_groups must be in [1, row_count]");
+    TORCH_CHECK(dropout_p >= 0.0 && dropout_p < 1.0, "dropout_p must be in [0, 1)");
+    if (training && dropout_p > 0.0) {
+        TORCH_CHECK(
+            dropout_mask.is_cuda() && dropout_mask.device() == device,
+            "dropout_mask must be on the same HIP device");
+        TORCH_CHECK(
+            dropout_mask.scalar_type() == at::kInt && dropout_mask.is_contiguous(),
+            "dropout_mask must be a contiguous int32 tensor");
+        TORCH_CHECK(
+            dropout_mask.numel() == rln_mask_words(rows, hidden),
+            "dropout_mask has the wrong size");
+    }
+}
+
+// Reserves rln_philox_increment() offset units from the device's default
+// generator (the reference does the same at
+// csrc/residual_layer_norm_kernel.hip:1762-1779). Under HIP graph capture the
+// generator hands out device pointers that the kernel reads at replay time,
+// so captured graphs draw fresh masks on every replay.
+rln_philox_t reserve_philox(const at::Tensor& x, int64_t hidden) {
+    auto generator = at::cuda::detail::getDefaultCUDAGenerator(x.device().index());
+    at::PhiloxCudaState state;
+    {
+        std::lock_guard<std::mutex> lock(generator.mutex());
+        state = generator.get<at::CUDAGeneratorImpl>()->philox_cuda_state(
+            rln_philox_increment(hidden));
+    }
+    rln_philox_t philox{};
+    if (state.captured_) {
+        philox.seed_ptr = state.seed_.ptr;
+        philox.offset_ptr = state.offset_.ptr;
+        philox.offset = state.offset_intragraph_;
+    } else {
+        philox.seed = state.seed_.val;
+        philox.offset = state.offset_.val;
+    }
+    return philox;
+}
+
+int branch_dtype_of(at::ScalarType type) {
+    return type == at::kHalf ? RLN_DTYPE_F16 : RLN_DTYPE_F32;
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> forward_impl(
+    const at::Tensor& x,
+    const at::Tensor& branch,
+    const at::Tensor& weight,
+    const at::Tensor& bias,
+    double dropout_p,
+    double eps,
+    bool training,
+    int64_t threads) {
+    check_forward_inputs(x, branch, weight, bias, dropout_p, eps, threads);
+    c10::hip::HIPGuard guard(x.device());
+    const int64_t hidden = x.size(-1);
+    const int64_t rows = x.numel() / hidden;
+    const bool dropout = training && dropout_p > 0.0;
+    auto updated = at::empty_like(x);
+    auto normalized = at::empty_like(x);
+    auto mean = at::empty({rows}, x.options());
+    auto rstd = at::empty({rows}, x.options());
+    auto mask = at::empty({dropout ? rln_mask_words(rows, hidden) : 0}, x.options().dtype(at::kInt));
+    rln_philox_t philox{};
+    if (dropout) {
+        philox = reserve_philox(x, hidden);
+    }
+    const auto stream = c10::hip::getCurrentHIPStream(x.device().index()).stream();
+    check_status(rln_forward(
+        x.data_ptr<float>(),
+        branch.data_ptr(),
+        branch_dtype_of(branch.scalar_type()),
+        weight.data_ptr<float>(),
+        bias.data_ptr<float>(),
+        updated.data_ptr<float>(),
+        normalized.data_ptr<float>(),
+        mean.data_ptr<float>(),
+        rstd.data_ptr<float>(),
+        dropout ? reinterpret_cast<uint32_t*>(mask.data_ptr<int32_t>()) : nullptr,
+        rows,
+        hidden,
+        dropout_p,
+        eps,
+        training ? 1 : 0,
+        dropout ? &philox : nullptr,
+        stream));
+    return {updated, normalized, mean, rstd, mask};
+}
+
+std::vector<at::Tensor> backward_impl(
+    const std::optional<at::Tensor>& grad_updated_in,
+    const std::optional<at::Tensor>& grad_normalized_in,
+    const at::Tensor& updated,
+    const at::Tensor& weight,
+    const at::Tensor& mean,
+    const at::Tensor& rstd,
+    const at::Tensor& dropout_mask,
+    double dropout_p,
+    bool training,
+    bool branch_is_half,
+    int64_t threads,
+    int64_t block_rows,
+    int64_t parameter_threads,
+    int64_t parameter_groups,
+    bool compute_parameter_gradients) {
+    // Undefined tensors arrive from autograd as nullopt-equivalents.
+    std::optional<at::Tensor> grad_updated;
+    std::optional<at::Tensor> grad_normalized;
+    if (grad_updated_in && grad_updated_in->defined()) {
+        grad_updated = grad_updated_in;
+    }
+    if (grad_normalized_in && grad_normalized_in->defined()) {
+        grad_normalized = grad_normalized_in;
+    }
+    check_backward_inputs(
+        grad_updated,
+        grad_normalized,
+        updated,
+        weight,
+        mean,
+        rstd,
+        dropout_mask,
+        dropout_p,
+        training,
+        threads,
+        block_rows,
+        parameter_threads,
+        parameter_groups);
+    c10::hip::HIPGuard guard(updated.device());
+    const int64_t hidden = updated.size(-1);
+    const int64_t rows = updated.numel() / hidden;
+    const bool dropout = training && dropout_p > 0.0;
+    const bool deterministic = at::globalContext().deterministicAlgorithms();
+    auto grad_x = at::empty_like(updated);
+    auto grad_branch = at::empty(
+        updated.sizes(),
+        updated.options().dtype(branch_is_half ? at::kHalf : at::kFloat));
+    at::Tensor grad_weight;
+    at::Tensor grad_bias;
+    at::Tensor workspace;
+    const bool launch_parameters = compute_parameter_gradients && grad_normalized.has_value();
+    if (compute_parameter_gradients) {
+        // Without grad_normalized the parameter gradients are exactly zero.
+        auto parameters = launch_parameters
+            ? at::empty({2, hidden}, updated.options())
+            : at::zeros({2, hidden}, updated.options());
+        grad_weight = parameters.select(0, 0);
+        grad_bias = parameters.select(0, 1);
+    }
+    if (launch_parameters) {
+        const size_t bytes = rln_backward_workspace_bytes(rows, hidden, deterministic ? 1 : 0);
+        if (bytes > 0) {
+            workspace = at::empty(
+                {static_cast<int64_t>(bytes / sizeof(float))},
+                updated.options());
+        }
+    }
+    const auto stream = c10::hip::getCurrentHIPStream(updated.device().index()).stream();
+    check_status(rln_backward(
+        grad_updated ? grad_updated->data_ptr<float>() : nullptr,
+        grad_normalized ? grad_normalized->data_ptr<float>() : nullptr,
+        updated.data_ptr<float>(),
+        weight.data_ptr<float>(),
+        mean.data_ptr<float>(),
+        rstd.data_ptr<float>(),
+        dropout ? reinterpret_cast<const uint32_t*>(dropout_mask.data_ptr<int32_t>()) : nullptr,
+        grad_x.data_ptr<float>(),
+        grad_branch.data_ptr(),
+        branch_is_half ? RLN_DTYPE_F16 : RLN_DTYPE_F32,
+        launch_parameters ? grad_weight.data_ptr<float>() : nullptr,
+        launch_parameters ? grad_bias.data_ptr<float>() : nullptr,
+        rows,
+        hidden,
+        dropout_p,
+        training ? 1 : 0,
+        deterministic ? 1 : 0,
+        0,
+        workspace.defined() ? workspace.data_ptr() : nullptr,
+        workspace.defined() ? static_cast<size_t>(workspace.numel()) * sizeof(float) : 0,
+        stream));
+    return {grad_x, grad_branch, grad_weight, grad_bias};
+}
+
+// Autograd contract of csrc/residual_layer_norm_bindings.cpp:10-98: saves
+// (updated, weight, mean, rstd, mask), does not materialize missing output
+// gradients, and returns weight/bias gradients only when `normalized` received
+// a gradient. Missing gradients are passed to the kernel as null pointers
+// instead of materialized zeros.
+class ResidualLayerNormFunction : public torch::autograd::Function<ResidualLayerNormFunction> {
+ public:
+    static torch::autograd::variable_list forward(
+        torch::autograd::AutogradContext* ctx,
+        torch::autograd::Variable x,
+        torch::autograd::Variable branch,
+        torch::autograd::Variable weight,
+        torch::autograd::Variable bias,
+        double dropout_p,
+        double eps,
+        bool training,
+        int64_t threads,
+        int64_t block_rows,
+        int64_t parameter_threads,
+        int64_t parameter_groups) {
+        auto result = forward_impl(x, branch, weight, bias, dropout_p, eps, training, threads);
+        auto updated = std::get<0>(result);
+        auto normalized = std::get<1>(result);
+        ctx->save_for_backward(
+            {updated, weight, std::get<2>(result), std::get<3>(result), std::get<4>(result)});
+        ctx->set_materialize_grads(false);
+        ctx->saved_data["dropout_p"] = dropout_p;
+        ctx->saved_data["training"] = training;
+        ctx->saved_data["branch_is_half"] = branch.scalar_type() == at::kHalf;
+        ctx->saved_data["threads"] = threads;
+        ctx->saved_data["block_rows"] = block_rows;
+        ctx->saved_data["parameter_threads"] = parameter_threads;
+        ctx->saved_data["parameter_groups"] = parameter_groups;
+        return {updated, normalized};
+    }
+
+    static torch::autograd::variable_list backward(
+        torch::autograd::AutogradContext* ctx,
+        torch::autograd::variable_list grad_outputs) {
+        auto saved = ctx->get_saved_variables();
+        std::optional<at::Tensor> grad_updated;
+        std::optional<at::Tensor> grad_normalized;
+        if (grad_outputs[0].defined()) {
+            grad_updated = grad_outputs[0].contiguous();
+        }
+        if (grad_outputs[1].defined()) {
+            grad_normalized = grad_outputs[1].contiguous();
+        }
+        const bool has_grad_normalized = grad_normalized.has_value();
+        if (!grad_updated && !has_grad_normalized) {
+            return {
+                at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor(),
+                at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor()};
+        }
+        auto gradients = backward_impl(
+            grad_updated,
+            grad_normalized,
+            saved[0],
+            saved[1],
+            saved[2],
+            saved[3],
+            saved[4],
+            ctx->saved_data["dropout_p"].toDouble(),
+            ctx->saved_data["training"].toBool(),
+            ctx->saved_data["branch_is_half"].toBool(),
+            ctx->saved_data["threads"].toInt(),
+            ctx->saved_data["block_rows"].toInt(),
+            ctx->saved_data["parameter_threads"].toInt(),
+            ctx->saved_data["parameter_groups"].toInt(),
+            has_grad_normalized);
+        return {
+            gradients[0],
+            gradients[1],
+            has_grad_normalized ? gradients[2] : at::Tensor(),
+            has_grad_normalized ? gradients[3] : at::Tensor(),
+            at::Tensor(),
+            at::Tensor(),
+            at::Tensor(),
+            at::Tensor(),
+            at::Tensor(),
+            at::Tensor(),
+            at::Tensor(),
+        };
+    }
+};
+
+torch::autograd::variable_list residual_layer_norm_autograd(
+    const at::Tensor& x,
+    const at::Tensor& branch,
+    const at::Tensor& weight,
+    const at::Tensor& bias,
+    double dropout_p,
+    double eps,
+    bool training,
+    int64_t threads,
+    int64_t block_rows,
+    int64_t parameter_threads,
+    int64_t parameter_groups) {
+    return ResidualLayerNormFunction::apply(
+        x,
+        branch,
+        weight,
+        bias,
+        dropout_p,
+        eps,
+        training,
+        threads,
+        block_rows,
+        parameter_threads,
+        parameter_groups);
+}
+
+}  // namespace
+
+PYBIND11_MODULE(_C, module) {
+    module.doc() = "MI355X (gfx950) fused residual + dropout + LayerNorm";
+    module.def("residual_layer_norm", &residual_layer_norm_autograd);
+    module.def("residual_layer_norm_forward", &forward_impl);
+    module.def(
+        "residual_layer_norm_backward",
+        &backward_impl,
+        pybind11::arg("grad_updated"),
+        pybind11::arg("grad_normalized"),
+        pybind11::arg("updated"),
+        pybind11::arg("weight"),
+        pybind11::arg("mean"),
+        pybind11::arg("rstd"),
+        pybind11::arg("dropout_mask"),
+        pybind11::arg("dropout_p"),
+        pybind11::arg("training"),
+        pybind11::arg("branch_is_half"),
+        pybind11::arg("threads"),
+        pybind11::arg("block_rows"),
+        pybind11::arg("parameter_threads"),
+        pybind11::arg("parameter_groups"),
+        pybind11::arg("compute_parameter_gradients"));
+    module.def("target_arch", []() { return std::string(rln_target_arch()); });
+    module.def("library_version", []() { return std::string(rln_version()); });
+}

@@ -1,0 +1,74 @@
+"""Native glue: loads the gfx950 extension and calls its autograd op.
+
+Mirrors gfx1010_kernels/_normalization_native.py of the reference (lazy ``_C``
+import :57-63, ``native_extension_status`` :66-68, ``native_residual_layer_norm``
+:71-99). The reference chooses gfx1010-tuned launch hints here (:5-54); the
+MI355X library chooses its own launch shape from (rows, hidden), so this
+module forwards fixed, valid hint values that the extension range-checks and
+otherwise ignores.
+"""
+
+from __future__ import annotations
+
+from functools import lru_cache
+
+# torch must be imported before _C: _C resolves libtorch and torch's bundled
+# HIP runtime (libamdhip64.so.7) from the already-loaded copies.
+import torch  # noqa: F401
+
+NATIVE_HIDDEN_SIZES = (128, 256, 384, 512, 768, 1024)
+TARGET_ARCHITECTURE = "gfx950"
+
+# Interface-compatibility launch hints (threads, block_rows, parameter_threads,
+# parameter_groups); parameter_groups=1 is valid for every row count.
+_LAUNCH_HINTS = (128, 64, 64, 1)
+
+
+@lru_cache(maxsize=1)
+def _extension():
+    try:
+        from . import _C
+    except ImportError as error:
+        return None, str(error)
+    return _C, ""
+
+
+def native_extension_status():
+    extension, reason = _extension()
+    return extension is not None, reason
+
+
+def native_residual_layer_norm(
+    x,
+    branch,
+    weight,
+    bias,
+    dropout_p,
+    eps,
+    training,
+):
+    extension, reason = _extension()
+    if extension is None:
+        raise RuntimeError(
+            f"{TARGET_ARCHITECTURE} native extension is unavailable: {reason}"
+        )
+    return tuple(
+        extension.residual_layer_norm(
+            x,
+            branch,
+            weight,
+            bias,
+            float(dropout_p),
+            float(eps),
+            bool(training),
+            *_LAUNCH_HINTS,
+        )
+    )
+
+
+__all__ = [
+    "NATIVE_HIDDEN_SIZES",
+    "TARGET_ARCHITECTURE",
+    "native_extension_status",
+    "native_residual_layer_norm",
+]

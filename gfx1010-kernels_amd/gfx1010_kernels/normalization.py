@@ -1,0 +1,228 @@
+"""Public residual-add + dropout + LayerNorm API and its dispatch.
+
+Drop-in for the reference's gfx1010_kernels/normalization.py:
+
+* ``residual_layer_norm`` (reference :149-298) returns ``(updated, normalized)``;
+  ``implementation`` is one of ``"auto"``, ``"gfx950"`` (strict native),
+  ``"gfx1010"`` (accepted alias of the strict native mode, so callers written
+  for the reference keep working), ``"torch"`` and ``"triton"``.
+* ``can_use_residual_layer_norm`` (reference :135-146) and
+  ``residual_layer_norm_status`` (reference :75-94) keep their signatures and
+  return types.
+
+Dispatch rules (same order and messages as the reference):
+
+* strict native modes check only ``x.is_cuda``, ``x.ndim`` and the hidden
+  size in Python, then the backend status, and leave every other check to the
+  native extension (reference :174-207);
+* ``auto`` validates inputs (``_input_reason``, reference :97-132) and falls
+  back to the PyTorch decomposition with a ``RuntimeWarning`` when they are not
+  eligible (reference :229-242, :266-285). One difference: on a gfx950 device
+  whose native extension cannot be loaded, ``auto`` raises instead of falling
+  back, so a broken install on the target hardware is never silently served by
+  the slow path;
+* ``"triton"`` is not part of this build and raises ``RuntimeError``.
+"""
+
+from __future__ import annotations
+
+from functools import lru_cache
+import warnings
+
+import torch
+from torch.nn import functional as F
+
+from ._normalization_native import NATIVE_HIDDEN_SIZES, TARGET_ARCHITECTURE
+from ._status import BackendStatus
+
+MIN_HIDDEN_SIZE = 128
+MAX_HIDDEN_SIZE = 1024
+
+IMPLEMENTATIONS = ("auto", TARGET_ARCHITECTURE, "gfx1010", "triton", "torch")
+_STRICT_NATIVE = frozenset({TARGET_ARCHITECTURE, "gfx1010"})
+_UNAVAILABLE = f"{TARGET_ARCHITECTURE} native residual LayerNorm is unavailable"
+
+
+def _torch_residual_layer_norm(x, branch, weight, bias, dropout_p, eps, training):
+    """PyTorch decomposition (reference normalization.py:15-33)."""
+    dropped = F.dropout(branch, dropout_p, training) if training else branch
+    updated = x + dropped
+    normalized = F.layer_norm(updated, (updated.shape[-1],), weight, bias, eps)
+    return updated, normalized
+
+
+def _architecture_of(properties):
+    name = getattr(properties, "gcnArchName", None)
+    if name is None:
+        name = getattr(properties, "gcn_arch_name", "") or ""
+    return name.split(":", 1)[0]
+
+
+@lru_cache(maxsize=None)
+def _native_status(device_index):
+    if not torch.cuda.is_available():
+        return BackendStatus(False, None, None, "PyTorch CUDA/HIP is unavailable")
+    if torch.version.hip is None:
+        return BackendStatus(
+            False,
+            torch.cuda.get_device_name(device_index),
+            None,
+            "PyTorch was not built with ROCm",
+        )
+    properties = torch.cuda.get_device_properties(device_index)
+    architecture = _architecture_of(properties)
+    if architecture != TARGET_ARCHITECTURE:
+        return BackendStatus(
+            False,
+            properties.name,
+            architecture,
+            f"the native extension targets {TARGET_ARCHITECTURE}",
+        )
+    from ._normalization_native import native_extension_status
+
+    available, reason = native_extension_status()
+    return BackendStatus(
+        available,
+        properties.name,
+        architecture,
+        f"{TARGET_ARCHITECTURE} native normalization backend is ready"
+        if available
+        else reason,
+    )
+
+
+def residual_layer_norm_status(device=None):
+    """Return the cached ``BackendStatus`` of the native backend on ``device``."""
+    if not torch.cuda.is_available():
+        return BackendStatus(False, None, None, "PyTorch CUDA/HIP is unavailable")
+    if device is None:
+        device_index = torch.cuda.current_device()
+    else:
+        resolved = torch.device(device)
+        if resolved.type != "cuda":
+            return BackendStatus(False, str(resolved), None, "the device must be a HIP GPU")
+        device_index = (
+            torch.cuda.current_device() if resolved.index is None else resolved.index
+        )
+    return _native_status(device_index)
+
+
+def _input_reason(x, branch, weight, bias, dropout_p, eps):
+    """Why the fused path cannot serve these inputs, or None if it can."""
+    if not x.is_cuda:
+        return "x must be a HIP tensor"
+    if not branch.is_cuda or not weight.is_cuda or not bias.is_cuda:
+        return "x, branch, weight and bias must be HIP tensors"
+    if not (x.device == branch.device == weight.device == bias.device):
+        return "x, branch, weight and bias must be on the same device"
+    if x.ndim < 2 or branch.shape != x.shape:
+        return "x and branch must have the same shape with at least two dimensions"
+    hidden_size = x.shape[-1]
+    if not MIN_HIDDEN_SIZE <= hidden_size <= MAX_HIDDEN_SIZE:
+        return f"hidden size must be between {MIN_HIDDEN_SIZE} and {MAX_HIDDEN_SIZE}"
+    if hidden_size % 8 != 0:
+        return "hidden size must be divisible by 8"
+    if weight.shape != (hidden_size,) or bias.shape != (hidden_size,):
+        return "weight and bias must match the final tensor dimension"
+    if x.dtype != torch.float32:
+        return "the optimized residual stream requires float32 x"
+    if branch.dtype not in (torch.float16, torch.float32):
+        return "branch must use float16 or float32"
+    if weight.dtype != torch.float32 or bias.dtype != torch.float32:
+        return "weight and bias must use float32"
+    if not all(tensor.is_contiguous() for tensor in (x, branch, weight, bias)):
+        return "x, branch, weight and bias must be contiguous"
+    if not 0.0 <= dropout_p < 1.0:
+        return "dropout_p must be in [0, 1)"
+    if eps <= 0.0:
+        return "eps must be positive"
+    if x.numel() == 0:
+        return "empty tensors use the PyTorch fallback"
+    return None
+
+
+def can_use_residual_layer_norm(x, branch, weight, bias, dropout_p=0.0, eps=1e-5):
+    """True when ``residual_layer_norm(..., implementation="auto")`` runs natively."""
+    reason = _input_reason(x, branch, weight, bias, dropout_p, eps)
+    if reason is not None or x.shape[-1] not in NATIVE_HIDDEN_SIZES:
+        return False
+    return residual_layer_norm_status(x.device).available
+
+
+def _strict_native(x, branch, weight, bias, dropout_p, eps, training):
+    if not x.is_cuda:
+        raise RuntimeError(f"{_UNAVAILABLE}: x must be a HIP tensor")
+    if x.ndim == 0:
+        raise RuntimeError(f"{_UNAVAILABLE}: x must have at least two dimensions")
+    if x.shape[-1] not in NATIVE_HIDDEN_SIZES:
+        raise RuntimeError(
+            f"{_UNAVAILABLE}: native hidden size must be one of {NATIVE_HIDDEN_SIZES}"
+        )
+    status = residual_layer_norm_status(x.device)
+    if not status.available:
+        raise RuntimeError(f"{_UNAVAILABLE}: {status.reason}")
+    from ._normalization_native import native_residual_layer_norm
+
+    return native_residual_layer_norm(
+        x, branch, weight, bias, float(dropout_p), float(eps), bool(training)
+    )
+
+
+def _fall_back(reason, x, branch, weight, bias, dropout_p, eps, training):
+    warnings.warn(
+        f"{TARGET_ARCHITECTURE} native residual LayerNorm was not used: {reason}",
+        RuntimeWarning,
+        stacklevel=3,
+    )
+    return _torch_residual_layer_norm(x, branch, weight, bias, dropout_p, eps, training)
+
+
+def residual_layer_norm(
+    x,
+    branch,
+    weight,
+    bias,
+    dropout_p=0.0,
+    eps=1e-5,
+    training=True,
+    *,
+    implementation="auto",
+):
+    """Fused ``dropout(branch) -> x + . -> LayerNorm``; returns ``(updated, normalized)``.
+
+    ``updated`` is the new fp32 residual stream and ``normalized`` its
+    LayerNorm with ``weight``/``bias``. Supports first-order autograd.
+    """
+    if implementation not in IMPLEMENTATIONS:
+        raise ValueError(
+            "implementation must be 'auto', 'gfx950', 'gfx1010', 'triton' or 'torch'"
+        )
+    if implementation == "torch":
+        return _torch_residual_layer_norm(x, branch, weight, bias, dropout_p, eps, training)
+    if implementation in _STRICT_NATIVE:
+        return _strict_native(x, branch, weight, bias, dropout_p, eps, training)
+
+    reason = _input_reason(x, branch, weight, bias, dropout_p, eps)
+    if implementation == "triton":
+        raise RuntimeError(
+            f"{TARGET_ARCHITECTURE} residual LayerNorm is unavailable: "
+            + (reason or "the Triton backend is not part of the MI355X build")
+        )
+    if reason is not None:
+        return _fall_back(reason, x, branch, weight, bias, dropout_p, eps, training)
+    if x.shape[-1] not in NATIVE_HIDDEN_SIZES:
+        return _fall_back(
+            f"native hidden size must be one of {NATIVE_HIDDEN_SIZES}",
+            x, branch, weight, bias, dropout_p, eps, training,
+        )
+    status = residual_layer_norm_status(x.device)
+    if not status.available:
+        if status.architecture == TARGET_ARCHITECTURE:
+            raise RuntimeError(f"{_UNAVAILABLE}: {status.reason}")
+        return _fall_back(status.reason, x, branch, weight, bias, dropout_p, eps, training)
+    from ._normalization_native import native_residual_layer_norm
+
+    with torch.cuda.device(x.device):
+        return native_residual_layer_norm(
+            x, branch, weight, bias, float(dropout_p), float(eps), bool(training)
+        )

@@ -1,0 +1,174 @@
+/*
+ * rln.h - C ABI of the MI355X (gfx950) fused residual-add + dropout + LayerNorm
+ * library, librln_gfx950.so.
+ *
+ * The operator, per row of `hidden` elements (H):
+ *
+ *   d = branch                                   (eval, or dropout_p == 0)
+ *   d = round_to_branch_dtype(float(branch) * keep * 1/(1-p))   (training, p > 0)
+ *   updated    = x + d                           (fp32)
+ *   mean       = sum(updated) / H
+ *   rstd       = 1 / sqrt(sum((updated - mean)^2) / H + eps)
+ *   normalized = (updated - mean) * rstd * weight + bias
+ *
+ * and its first-order backward. This is the contract of the reference's
+ * native entry points csrc/residual_layer_norm.h:10-42 and
+ * csrc/residual_layer_norm_kernel.hip:425-545 (forward), :548-618 (input
+ * gradients), :727-869 (weight/bias gradients).
+ *
+ * Conventions shared by every entry point:
+ *  - All pointers are device pointers on the calling thread's current HIP
+ *    device, except `philox` (host pointer to a descriptor).
+ *  - Tensors are dense row-major [rows, hidden]; mean/rstd are [rows].
+ *  - The dropout mask is `rows * hidden / 32` uint32 words: keep(r, c) is
+ *    bit (c % 32) of word r * hidden / 32 + c / 32 - the reference's layout
+ *    (csrc/residual_layer_norm_kernel.hip:500-511, :162-164).
+ *  - `stream` is a hipStream_t (NULL = the legacy default stream). Work is
+ *    enqueued asynchronously; nothing synchronizes the host.
+ *  - No entry point allocates device memory.
+ *  - Return value: RLN_OK, or an RLN_ERR_* code with a message available
+ *    from rln_last_error() (thread-local, valid until the next call on the
+ *    same thread).
+ */
+#ifndef RLN_H
+#define RLN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum rln_dtype {
+    RLN_DTYPE_F32 = 0,
+    RLN_DTYPE_F16 = 1
+};
+
+enum rln_status {
+    RLN_OK = 0,
+    RLN_ERR_INVALID = 1,     /* bad argument: shape, range, null pointer */
+    RLN_ERR_UNSUPPORTED = 2, /* valid request this build does not serve */
+    RLN_ERR_HIP = 3          /* HIP runtime reported an error at launch */
+};
+
+/*
+ * Philox4x32-10 stream selection for dropout. Mirrors torch's
+ * at::PhiloxCudaState: outside graph capture the values are given directly;
+ * under HIP graph capture the seed and base offset live in device memory and
+ * are read when the kernel runs (effective offset = *offset_ptr + offset).
+ * Replaces the seed/offset reservation at
+ * csrc/residual_layer_norm_kernel.hip:1755-1780.
+ */
+typedef struct rln_philox {
+    uint64_t seed;             /* used when seed_ptr == NULL            */
+    uint64_t offset;           /* absolute offset, or intra-graph delta */
+    const int64_t* seed_ptr;   /* device pointer or NULL                */
+    const int64_t* offset_ptr; /* device pointer or NULL                */
+} rln_philox_t;
+
+/*
+ * Forward. Replaces residual_layer_norm_forward_hip
+ * (csrc/residual_layer_norm.h:10-24; csrc/residual_layer_norm_kernel.hip:1720-1827).
+ *
+ * x, updated, normalized: fp32 [rows, hidden]; branch: [rows, hidden] in
+ * `branch_dtype`; weight, bias: fp32 [hidden]; mean, rstd: fp32 [rows].
+ * dropout_mask: rln_mask_words(rows, hidden) uint32 words, written only when
+ * training && dropout_p > 0 (may be NULL otherwise). `philox` is read only in
+ * that case (may be NULL otherwise). The call consumes
+ * rln_philox_increment(hidden) offset units of the Philox stream.
+ */
+int rln_forward(
+    const float* x,
+    const void* branch,
+    int branch_dtype,
+    const float* weight,
+    const float* bias,
+    float* updated,
+    float* normalized,
+    float* mean,
+    float* rstd,
+    uint32_t* dropout_mask,
+    int64_t rows,
+    int64_t hidden,
+    double dropout_p,
+    double eps,
+    int training,
+    const rln_philox_t* philox,
+    void* stream);
+
+/*
+ * Backward. Replaces residual_layer_norm_backward_hip
+ * (csrc/residual_layer_norm.h:27-42; csrc/residual_layer_norm_kernel.hip:1830-2036).
+ *
+ * grad_updated, grad_normalized: fp32 [rows, hidden] upstream gradients; either
+ * may be NULL, meaning zero (the reference materializes zeros instead,
+ * csrc/residual_layer_norm_bindings.cpp:62-67).
+ * grad_x: fp32 [rows, hidden]; grad_branch: [rows, hidden] in branch_dtype.
+ * grad_weight, grad_bias: fp32 [hidden], both NULL to skip the parameter
+ * gradients (they are skipped as well when grad_normalized is NULL; the
+ * outputs are then left untouched).
+ * deterministic != 0 selects the fixed-order two-stage reduction of the
+ * parameter gradients (bitwise reproducible); 0 selects grouped fp32 atomics.
+ * accumulate_parameters != 0 adds the parameter gradients to the values
+ * already in grad_weight / grad_bias (gradient accumulation across calls, one
+ * kernel launch in atomic mode); 0 overwrites them.
+ * workspace: device scratch of at least
+ * rln_backward_workspace_bytes(rows, hidden, deterministic) bytes, 256-byte
+ * aligned (may be NULL when that size is 0).
+ */
+int rln_backward(
+    const float* grad_updated,
+    const float* grad_normalized,
+    const float* updated,
+    const float* weight,
+    const float* mean,
+    const float* rstd,
+    const uint32_t* dropout_mask,
+    float* grad_x,
+    void* grad_branch,
+    int branch_dtype,
+    float* grad_weight,
+    float* grad_bias,
+    int64_t rows,
+    int64_t hidden,
+    double dropout_p,
+    int training,
+    int deterministic,
+    int accumulate_parameters,
+    void* workspace,
+    size_t workspace_bytes,
+    void* stream);
+
+/* Workspace bytes rln_backward needs (0 in atomic mode). */
+size_t rln_backward_workspace_bytes(
+    int64_t rows,
+    int64_t hidden,
+    int deterministic);
+
+/* Philox offset units one dropout forward consumes (torch's `increment`). */
+uint64_t rln_philox_increment(int64_t hidden);
+
+/* Number of uint32 dropout-mask words for [rows, hidden]. */
+int64_t rln_mask_words(int64_t rows, int64_t hidden);
+
+/* 1 if `hidden` has a compiled specialization, else 0. */
+int rln_hidden_supported(int64_t hidden);
+
+/* Writes up to `capacity` supported hidden sizes; returns how many exist. */
+int rln_supported_hidden_sizes(int64_t* out, int capacity);
+
+/* Thread-local message for the last failed call on this thread. */
+const char* rln_last_error(void);
+
+/* GPU architecture the device code was built for ("gfx950"). */
+const char* rln_target_arch(void);
+
+/* Library version string. */
+const char* rln_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RLN_H */

@@ -1,0 +1,141 @@
+"""Shared helpers for the GPU parity tests: inputs, oracle replay, tolerances.
+
+Tolerances (written here once, used by every parity test):
+
+* bit-exact: ``updated`` (always), the dropout mask, deterministic replays,
+  the misaligned (element access) path against the aligned path;
+* ``normalized``, ``mean``, ``rstd``, ``grad_x`` and fp32 ``grad_branch``:
+  normwise relative error ``max|a - b| / max|b|`` <= 1e-5 against the fp64
+  oracle;
+* fp16 ``grad_branch``: within one fp16 ulp of the fp64 oracle value, plus
+  1e-5 of the largest magnitude (the kernel rounds its fp32 result once);
+* ``grad_weight`` / ``grad_bias``: normwise relative error <= 1e-4.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from oracle import rln_oracle as oracle
+
+NATIVE_HIDDEN_SIZES = (128, 256, 384, 512, 768, 1024)
+TOL_FORWARD = 1e-5
+TOL_INPUT_GRAD = 1e-5
+TOL_PARAMETER_GRAD = 1e-4
+
+DEVICE = torch.device("cuda", 0)
+
+
+def normwise(actual, expected) -> float:
+    actual = np.asarray(actual, dtype=np.float64)
+    expected = np.asarray(expected, dtype=np.float64)
+    scale = max(float(np.max(np.abs(expected))), 1e-30)
+    return float(np.max(np.abs(actual - expected)) / scale)
+
+
+def assert_normwise(actual, expected, tolerance, what=""):
+    error = normwise(actual, expected)
+    assert error <= tolerance, f"{what}: normwise error {error:.3e} > {tolerance:.1e}"
+
+
+def assert_fp16_close(actual_f16, expected_f64, what=""):
+    actual = np.asarray(actual_f16, dtype=np.float64)
+    expected = np.asarray(expected_f64, dtype=np.float64)
+    ulp = np.spacing(np.abs(expected).astype(np.float16)).astype(np.float64)
+    bound = ulp + 1e-5 * float(np.max(np.abs(expected)))
+    excess = np.abs(actual - expected) - bound
+    assert np.all(excess <= 0), f"{what}: fp16 error exceeds one ulp by {excess.max():.3e}"
+
+
+def assert_bitwise(actual, expected, what=""):
+    a = np.ascontiguousarray(actual)
+    b = np.ascontiguousarray(expected)
+    assert a.shape == b.shape and a.dtype == b.dtype, what
+    if a.dtype.itemsize == 4:
+        a, b = a.view(np.uint32), b.view(np.uint32)
+    elif a.dtype.itemsize == 2:
+        a, b = a.view(np.uint16), b.view(np.uint16)
+    mismatches = int(np.count_nonzero(a != b))
+    assert mismatches == 0, f"{what}: {mismatches} of {a.size} values differ bitwise"
+
+
+def host(tensor: torch.Tensor) -> np.ndarray:
+    return tensor.detach().cpu().numpy()
+
+
+def make_inputs(shape, branch_dtype, seed, x_mean=0.0, x_std=1.0, branch_std=1.0,
+                device=DEVICE):
+    """Seeded CPU inputs copied to the device (CPU and GPU see identical values)."""
+    generator = torch.Generator().manual_seed(seed)
+    hidden = shape[-1]
+    x = torch.randn(shape, generator=generator) * x_std + x_mean
+    branch = (torch.randn(shape, generator=generator) * branch_std).to(branch_dtype)
+    weight = 1.0 + 0.02 * torch.randn(hidden, generator=generator)
+    bias = 0.02 * torch.randn(hidden, generator=generator)
+    return tuple(t.contiguous().to(device) for t in (x, branch, weight, bias))
+
+
+def make_grads(shape, seed, device=DEVICE):
+    generator = torch.Generator().manual_seed(seed)
+    return tuple(torch.randn(shape, generator=generator).to(device) for _ in range(2))
+
+
+def generator_state(device=DEVICE):
+    """(seed, offset) the next native dropout call will use."""
+    generator = torch.cuda.default_generators[device.index or 0]
+    return generator.initial_seed(), generator.get_offset()
+
+
+def oracle_keep(rows, hidden, dropout_p, training, seed, offset):
+    active, scale, threshold = oracle.dropout_constants(dropout_p, training)
+    if not active:
+        return None, scale, None
+    words = oracle.dropout_mask_words(rows, hidden, seed, offset, threshold)
+    return oracle.decode_mask(words, rows, hidden), scale, words
+
+
+def check_forward(outputs, inputs, dropout_p, training, eps, seed, offset, what=""):
+    """Compare raw forward outputs (updated, normalized, mean, rstd, mask) to the oracle."""
+    updated, normalized, mean, rstd, mask = outputs
+    x, branch, weight, bias = (host(t) for t in inputs)
+    hidden = x.shape[-1]
+    rows = x.size // hidden
+    keep, scale, words = oracle_keep(rows, hidden, dropout_p, training, seed, offset)
+    if words is not None:
+        assert_bitwise(host(mask).view(np.uint32), words, f"{what} mask")
+    else:
+        assert mask.numel() == 0
+    x2 = x.reshape(rows, hidden)
+    b2 = branch.reshape(rows, hidden)
+    expected = oracle.forward(x2, b2, weight, bias, eps, keep=keep, scale=scale)
+    assert_bitwise(host(updated).reshape(rows, hidden), expected["updated"], f"{what} updated")
+    assert_normwise(host(normalized).reshape(rows, hidden), expected["normalized"], TOL_FORWARD,
+                    f"{what} normalized")
+    assert_normwise(host(mean), expected["mean"], TOL_FORWARD, f"{what} mean")
+    assert_normwise(host(rstd), expected["rstd"], TOL_FORWARD, f"{what} rstd")
+    return keep, scale
+
+
+def check_backward(gradients, grad_updated, grad_normalized, updated, weight, eps, keep, scale,
+                   what="", parameters=True):
+    grad_x, grad_branch, grad_weight, grad_bias = gradients
+    u = host(updated)
+    hidden = u.shape[-1]
+    u = u.reshape(-1, hidden)
+    gu = None if grad_updated is None else host(grad_updated).reshape(-1, hidden)
+    gy = None if grad_normalized is None else host(grad_normalized).reshape(-1, hidden)
+    expected = oracle.backward(gu, gy, u, host(weight), eps, keep=keep, scale=scale)
+    assert_normwise(host(grad_x).reshape(-1, hidden), expected["grad_x"], TOL_INPUT_GRAD,
+                    f"{what} grad_x")
+    gb = host(grad_branch).reshape(-1, hidden)
+    if gb.dtype == np.float16:
+        assert_fp16_close(gb, expected["grad_branch"], f"{what} grad_branch")
+    else:
+        assert_normwise(gb, expected["grad_branch"], TOL_INPUT_GRAD, f"{what} grad_branch")
+    if parameters:
+        assert_normwise(host(grad_weight), expected["grad_weight"], TOL_PARAMETER_GRAD,
+                        f"{what} grad_weight")
+        assert_normwise(host(grad_bias), expected["grad_bias"], TOL_PARAMETER_GRAD,
+                        f"{what} grad_bias")
+    return expected

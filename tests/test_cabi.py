@@ -1,0 +1,139 @@
+"""The C ABI library loads, exports every declared symbol and validates inputs.
+
+No test here launches GPU work: every call below fails argument validation,
+which happens before any HIP call.
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch  # noqa: F401  (binds the library to torch's HIP runtime)
+
+from gfx1010_kernels import _cabi
+from gfx1010_kernels._normalization_native import NATIVE_HIDDEN_SIZES
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "rln.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:[\w\s\*]+?)\b(rln_\w+)\s*\(", text, re.MULTILINE)))
+
+
+def test_header_declares_the_expected_entry_points():
+    assert _declared_functions() == sorted(_cabi.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    library = _cabi.library()
+    for name in _declared_functions():
+        assert hasattr(library, name), name
+
+
+def test_library_metadata():
+    library = _cabi.library()
+    assert library.rln_target_arch() == b"gfx950"
+    assert re.fullmatch(rb"\d+\.\d+\.\d+", library.rln_version())
+    assert _cabi.supported_hidden_sizes() == NATIVE_HIDDEN_SIZES
+    for hidden in NATIVE_HIDDEN_SIZES:
+        assert library.rln_hidden_supported(hidden) == 1
+    for hidden in (0, 64, 160, 2048):
+        assert library.rln_hidden_supported(hidden) == 0
+
+
+def test_philox_struct_layout():
+    assert ctypes.sizeof(_cabi.RlnPhilox) == 32
+
+
+def test_size_queries():
+    assert _cabi.philox_increment(768) == 4
+    assert _cabi.mask_words(8192, 768) == 8192 * 24
+    assert _cabi.mask_words(0, 768) == 0
+    assert _cabi.backward_workspace_bytes(8192, 768, False) == 0
+    assert _cabi.backward_workspace_bytes(0, 768, True) == 0
+    # One partial [2, H] per block; 4 waves per block, one row per wave (two at H=128/384).
+    assert _cabi.backward_workspace_bytes(8192, 768, True) == 2048 * 2 * 768 * 4
+    assert _cabi.backward_workspace_bytes(37, 128, True) == 5 * 2 * 128 * 4
+    assert _cabi.backward_workspace_bytes(1 << 20, 1024, True) == 2048 * 2 * 1024 * 4
+
+
+FAKE = 1 << 20  # a non-null address; validation fails before it is touched
+
+
+def _forward(**overrides):
+    args = dict(
+        x=FAKE, branch=FAKE, branch_dtype=_cabi.RLN_DTYPE_F16, weight=FAKE, bias=FAKE,
+        updated=FAKE, normalized=FAKE, mean=FAKE, rstd=FAKE, mask=FAKE, rows=4, hidden=768,
+        dropout_p=0.1, eps=1e-5, training=True, philox=_cabi.RlnPhilox(1, 0, None, None),
+    )
+    args.update(overrides)
+    _cabi.forward(**args)
+
+
+@pytest.mark.parametrize(
+    "overrides,status,message",
+    [
+        (dict(rows=0), _cabi.RLN_ERR_INVALID, "empty tensors are unsupported"),
+        (dict(hidden=160), _cabi.RLN_ERR_UNSUPPORTED, "unsupported native hidden size: 160"),
+        (dict(branch_dtype=7), _cabi.RLN_ERR_INVALID, "branch must use float16 or float32"),
+        (dict(dropout_p=1.0), _cabi.RLN_ERR_INVALID, r"dropout_p must be in \[0, 1\)"),
+        (dict(dropout_p=-0.1), _cabi.RLN_ERR_INVALID, r"dropout_p must be in \[0, 1\)"),
+        (dict(dropout_p=0.999999999), _cabi.RLN_ERR_INVALID, r"dropout_p must be in \[0, 1\)"),
+        (dict(eps=0.0), _cabi.RLN_ERR_INVALID, "eps must be positive"),
+        (dict(x=None), _cabi.RLN_ERR_INVALID, "forward tensors must not be null"),
+        (dict(mask=None), _cabi.RLN_ERR_INVALID, "dropout_mask must not be null"),
+        (dict(philox=None), _cabi.RLN_ERR_INVALID, "philox must not be null"),
+        (dict(rows=1 << 62), _cabi.RLN_ERR_INVALID, "overflows"),
+    ],
+)
+def test_forward_rejects_invalid_arguments(overrides, status, message):
+    with pytest.raises(_cabi.RlnError, match=message) as error:
+        _forward(**overrides)
+    assert error.value.status == status
+
+
+def _backward(**overrides):
+    args = dict(
+        grad_updated=FAKE, grad_normalized=FAKE, updated=FAKE, weight=FAKE, mean=FAKE, rstd=FAKE,
+        mask=FAKE, grad_x=FAKE, grad_branch=FAKE, branch_dtype=_cabi.RLN_DTYPE_F16,
+        grad_weight=FAKE, grad_bias=FAKE, rows=4, hidden=768, dropout_p=0.1, training=True,
+        deterministic=True, workspace=None, workspace_bytes=0,
+    )
+    args.update(overrides)
+    _cabi.backward(**args)
+
+
+@pytest.mark.parametrize(
+    "overrides,message",
+    [
+        (dict(rows=-1), "empty tensors are unsupported"),
+        (dict(hidden=100), "unsupported native hidden size: 100"),
+        (dict(updated=None), "backward tensors must not be null"),
+        (dict(grad_bias=None), "both be given or both be null"),
+        (dict(mask=None), "dropout_mask must not be null"),
+        (dict(), "workspace too small"),
+        (dict(workspace=FAKE, workspace_bytes=16), "workspace too small"),
+        (dict(workspace=FAKE + 4, workspace_bytes=1 << 30), "16-byte aligned"),
+    ],
+)
+def test_backward_rejects_invalid_arguments(overrides, message):
+    with pytest.raises(_cabi.RlnError, match=message):
+        _backward(**overrides)
+
+
+def test_glue_module_imports_and_checks_device_first():
+    from gfx1010_kernels import _C
+
+    x = torch.zeros(2, 128)
+    with pytest.raises(RuntimeError, match="x must be a HIP tensor"):
+        _C.residual_layer_norm_forward(x, x, torch.ones(128), torch.zeros(128), 0.0, 1e-5, True, 128)
+    stats = torch.zeros(2)
+    with pytest.raises(RuntimeError, match="updated must be a HIP tensor"):
+        _C.residual_layer_norm_backward(
+            x, x, x, torch.ones(128), stats, stats, torch.empty(0, dtype=torch.int32),
+            0.0, True, True, 128, 16, 64, 1, True)
+    with pytest.raises(RuntimeError, match="x must be a HIP tensor"):
+        _C.residual_layer_norm(x, x, torch.ones(128), torch.zeros(128), 0.0, 1e-5, True, 128, 64, 64, 1)
+    assert _C.target_arch() == "gfx950"

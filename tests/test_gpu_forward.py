@@ -1,0 +1,110 @@
+"""Forward parity of the gfx950 kernels against the CPU oracle.
+
+Covers every hidden specialization, both branch dtypes, eval / train p=0 /
+train with dropout, the reference's row-count boundaries
+(tests/test_residual_layer_norm_native_matrix.py:171-181) and the misaligned
+element-access path (tests/test_residual_layer_norm_vectorized.py:96-164).
+"""
+
+import pytest
+import torch
+
+from gfx1010_kernels import _C, residual_layer_norm
+from parity import (
+    NATIVE_HIDDEN_SIZES,
+    assert_bitwise,
+    check_forward,
+    generator_state,
+    host,
+    make_inputs,
+)
+
+pytestmark = pytest.mark.gpu
+
+MODES = {
+    "eval": (0.8, False),
+    "train-p0": (0.0, True),
+    "train-p0.15": (0.15, True),
+}
+
+
+@pytest.mark.parametrize("hidden", NATIVE_HIDDEN_SIZES)
+@pytest.mark.parametrize("branch_dtype", [torch.float16, torch.float32], ids=["f16", "f32"])
+@pytest.mark.parametrize("mode", list(MODES))
+def test_forward_matches_oracle(hidden, branch_dtype, mode):
+    dropout_p, training = MODES[mode]
+    inputs = make_inputs((37, hidden), branch_dtype, seed=17 + hidden)
+    torch.cuda.manual_seed(2026 + hidden)
+    seed, offset = generator_state()
+    outputs = _C.residual_layer_norm_forward(*inputs, dropout_p, 1e-5, training, 128)
+    check_forward(outputs, inputs, dropout_p, training, 1e-5, seed, offset, f"H={hidden} {mode}")
+
+    # The public strict API runs the same computation for the same RNG state.
+    torch.cuda.manual_seed(2026 + hidden)
+    updated, normalized = residual_layer_norm(
+        *inputs, dropout_p=dropout_p, eps=1e-5, training=training, implementation="gfx950")
+    assert_bitwise(host(updated), host(outputs[0]), "public updated")
+    assert_bitwise(host(normalized), host(outputs[1]), "public normalized")
+
+
+@pytest.mark.parametrize("hidden", [128, 384, 1024])
+@pytest.mark.parametrize("rows", [1, 15, 16, 17, 511, 512, 513, 2047, 2048, 2049])
+def test_row_count_boundaries(hidden, rows):
+    inputs = make_inputs((rows, hidden), torch.float16, seed=227 + rows)
+    torch.cuda.manual_seed(rows)
+    seed, offset = generator_state()
+    outputs = _C.residual_layer_norm_forward(*inputs, 0.1, 1e-5, True, 128)
+    check_forward(outputs, inputs, 0.1, True, 1e-5, seed, offset, f"rows={rows}")
+
+
+def test_grid_stride_rows_beyond_one_launch_wave():
+    # More rows than the launch has waves: every wave walks several rows.
+    inputs = make_inputs((3 * 8192 + 5, 256), torch.float16, seed=5)
+    torch.cuda.manual_seed(6)
+    seed, offset = generator_state()
+    outputs = _C.residual_layer_norm_forward(*inputs, 0.2, 1e-5, True, 128)
+    check_forward(outputs, inputs, 0.2, True, 1e-5, seed, offset, "grid-stride")
+
+
+@pytest.mark.parametrize("branch_dtype", [torch.float16, torch.float32], ids=["f16", "f32"])
+@pytest.mark.parametrize("dropout_p", [0.0, 0.15])
+def test_misaligned_inputs_use_element_access_with_identical_results(branch_dtype, dropout_p):
+    rows, hidden = 23, 384
+    x, branch, weight, bias = make_inputs((rows, hidden), branch_dtype, seed=409)
+    storage = torch.empty(rows * hidden + 1, device=x.device)
+    misaligned_x = storage[1:].view(rows, hidden)
+    misaligned_x.copy_(x)
+    assert misaligned_x.is_contiguous() and misaligned_x.data_ptr() % 16 != 0
+
+    torch.cuda.manual_seed(11)
+    aligned = _C.residual_layer_norm_forward(x, branch, weight, bias, dropout_p, 1e-5, True, 128)
+    torch.cuda.manual_seed(11)
+    scalar = _C.residual_layer_norm_forward(
+        misaligned_x, branch, weight, bias, dropout_p, 1e-5, True, 128)
+    for name, a, b in zip(("updated", "normalized", "mean", "rstd", "mask"), aligned, scalar):
+        assert_bitwise(host(b), host(a), name)
+
+
+def test_leading_dimensions_are_flattened():
+    inputs = make_inputs((2, 3, 5, 512), torch.float16, seed=3)
+    torch.cuda.manual_seed(4)
+    seed, offset = generator_state()
+    outputs = _C.residual_layer_norm_forward(*inputs, 0.1, 1e-5, True, 128)
+    assert outputs[0].shape == (2, 3, 5, 512) and outputs[2].shape == (30,)
+    check_forward(outputs, inputs, 0.1, True, 1e-5, seed, offset, "4-d")
+
+
+def test_raw_forward_rejects_invalid_inputs_on_gpu():
+    x, branch, weight, bias = make_inputs((4, 768), torch.float16, seed=1)
+    with pytest.raises(RuntimeError, match="empty tensors are unsupported"):
+        _C.residual_layer_norm_forward(x[:0], branch[:0], weight, bias, 0.0, 1e-5, True, 128)
+    with pytest.raises(RuntimeError, match="unsupported native hidden size: 640"):
+        big = torch.zeros(4, 640, device=x.device)
+        _C.residual_layer_norm_forward(big, big, big[0], big[0], 0.0, 1e-5, True, 128)
+    with pytest.raises(RuntimeError, match="threads must be 128, 192 or 256"):
+        _C.residual_layer_norm_forward(x, branch, weight, bias, 0.0, 1e-5, True, 64)
+    with pytest.raises(RuntimeError, match="all tensors must be contiguous"):
+        strided = x.t().contiguous().t()
+        _C.residual_layer_norm_forward(strided, branch, weight, bias, 0.0, 1e-5, True, 128)
+    with pytest.raises(RuntimeError, match="x must use float32"):
+        _C.residual_layer_norm_forward(x.half(), branch, weight, bias, 0.0, 1e-5, True, 128)
