@@ -53,7 +53,10 @@ constexpr int kBlockThreads = 256;
 constexpr int kBlockWaves = kBlockThreads / kWaveSize;
 // Upper bound on blocks per launch: 2048 blocks x 4 waves = 8192 waves,
 // i.e. 32 resident waves on each of MI355X's 256 CUs.
-constexpr int64_t kMaxBlocks = 2048;
+#ifndef RLN_MAX_BLOCKS
+#define RLN_MAX_BLOCKS 2048
+#endif
+constexpr int64_t kMaxBlocks = RLN_MAX_BLOCKS;
 
 constexpr int64_t kSupportedHidden[] = {128, 256, 384, 512, 768, 1024};
 
@@ -146,15 +149,20 @@ __device__ __forceinline__ float row16_sum(float value) {
     return value;
 }
 
+// v_readlane_b32 of an fp32 value. The builtin is declared on int, so the
+// value travels as its bit pattern (a plain call would convert to int).
+__device__ __forceinline__ float readlane_f32(float value, int lane) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, value), lane));
+}
+
 // Sum over the lanes that own one row: 64 lanes, or the 32-lane half of the
 // wave that the calling lane belongs to. Must be called by all 64 lanes.
 template <int Lanes>
 __device__ __forceinline__ float row_sum(float value) {
     value = row16_sum(value);
-    const float low = __builtin_amdgcn_readlane(value, 0)
-        + __builtin_amdgcn_readlane(value, 16);
-    const float high = __builtin_amdgcn_readlane(value, 32)
-        + __builtin_amdgcn_readlane(value, 48);
+    const float low = readlane_f32(value, 0) + readlane_f32(value, 16);
+    const float high = readlane_f32(value, 32) + readlane_f32(value, 48);
     if constexpr (Lanes == 64) {
         return low + high;
     } else {
@@ -494,21 +502,38 @@ void rln_backward_kernel(
         const float mean = valid ? mean_in[row] : 0.0f;
         const float rstd = valid ? rstd_in[row] : 0.0f;
 
+        // Every global load of the row is issued before the first reduction so
+        // that the row costs one memory round trip.
         float4 xhat[V];
         float4 gy[V];
+        float4 gu[V];
+        uint32_t keep_bits[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+            const int column = (v * L + l) * 4;
+            xhat[v] = zero4();
+            gy[v] = zero4();
+            gu[v] = zero4();
+            keep_bits[v] = 0;
+            if (valid) {
+                xhat[v] = load4<Aligned>(updated + base + column);
+                if (has_gy) {
+                    gy[v] = load4<Aligned>(grad_normalized + base + column);
+                }
+                if (has_gu) {
+                    gu[v] = load4<Aligned>(grad_updated + base + column);
+                }
+                if (dropout) {
+                    keep_bits[v] = mask[row * G::kMaskWords + (v * L + l) / 8] >> (4 * (l & 7));
+                }
+            }
+        }
+
         float sum_q = 0.0f;
         float sum_qx = 0.0f;
 #pragma unroll
         for (int v = 0; v < V; ++v) {
-            const int column = (v * L + l) * 4;
-            float4 uv = zero4();
-            gy[v] = zero4();
-            if (valid) {
-                uv = load4<Aligned>(updated + base + column);
-                if (has_gy) {
-                    gy[v] = load4<Aligned>(grad_normalized + base + column);
-                }
-            }
+            const float4 uv = xhat[v];
             xhat[v] = make_float4(
                 (uv.x - mean) * rstd,
                 (uv.y - mean) * rstd,
@@ -532,7 +557,7 @@ void rln_backward_kernel(
 #pragma unroll
             for (int v = 0; v < V; ++v) {
                 const int column = (v * L + l) * 4;
-                float4 g = has_gu ? load4<Aligned>(grad_updated + base + column) : zero4();
+                float4 g = gu[v];
                 if (has_gy) {
                     const float4 q = make_float4(
                         gy[v].x * w[v].x, gy[v].y * w[v].y, gy[v].z * w[v].z, gy[v].w * w[v].w);
@@ -543,8 +568,7 @@ void rln_backward_kernel(
                 }
                 store4<Aligned>(grad_x + base + column, g);
                 if (dropout) {
-                    const uint32_t word = mask[row * G::kMaskWords + (v * L + l) / 8];
-                    const uint32_t bits = word >> (4 * (l & 7));
+                    const uint32_t bits = keep_bits[v];
                     g.x = g.x * (static_cast<float>(bits & 1u) * scale);
                     g.y = g.y * (static_cast<float>((bits >> 1) & 1u) * scale);
                     g.z = g.z * (static_cast<float>((bits >> 2) & 1u) * scale);

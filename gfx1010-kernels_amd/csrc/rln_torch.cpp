@@ -23,8 +23,8 @@
 #include <ATen/Context.h>
 #include <ATen/core/Generator.h>
 #include <ATen/hip/HIPGeneratorImpl.h>
-#include <c10/hip/HIPGuard.h>
-#include <c10/hip/HIPStream.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 
 #include <mutex>
 #include <optional>
@@ -194,7 +194,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> forward_i
     bool training,
     int64_t threads) {
     check_forward_inputs(x, branch, weight, bias, dropout_p, eps, threads);
-    c10::hip::HIPGuard guard(x.device());
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
     const int64_t hidden = x.size(-1);
     const int64_t rows = x.numel() / hidden;
     const bool dropout = training && dropout_p > 0.0;
@@ -207,7 +207,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> forward_i
     if (dropout) {
         philox = reserve_philox(x, hidden);
     }
-    const auto stream = c10::hip::getCurrentHIPStream(x.device().index()).stream();
+    const auto stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(x.device().index()).stream();
     check_status(rln_forward(
         x.data_ptr<float>(),
         branch.data_ptr(),
@@ -268,7 +268,7 @@ std::vector<at::Tensor> backward_impl(
         block_rows,
         parameter_threads,
         parameter_groups);
-    c10::hip::HIPGuard guard(updated.device());
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(updated.device());
     const int64_t hidden = updated.size(-1);
     const int64_t rows = updated.numel() / hidden;
     const bool dropout = training && dropout_p > 0.0;
@@ -297,7 +297,7 @@ std::vector<at::Tensor> backward_impl(
                 updated.options());
         }
     }
-    const auto stream = c10::hip::getCurrentHIPStream(updated.device().index()).stream();
+    const auto stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(updated.device().index()).stream();
     check_status(rln_backward(
         grad_updated ? grad_updated->data_ptr<float>() : nullptr,
         grad_normalized ? grad_normalized->data_ptr<float>() : nullptr,
