@@ -11,13 +11,17 @@ accumulation; the atomic backward is then a single kernel).
 
 Inputs are resident in HBM before the timed region. One input set moves about
 200 MB, under MI355X's 256 MB Infinity Cache, so steps rotate through
-``--sets`` independent copies (800 MB by default) and every step reads data that
-was last touched three steps earlier.
+``--sets`` independent copies (800 MB by default) and every step reads inputs
+that were last touched three steps earlier.
 
 Prints one JSON line:
-  value        fwd+bwd algorithmic HBM bytes / wall time per step (GB/s)
+  value        fwd+bwd algorithmic HBM bytes / wall time per step (GB/s), the
+               step = forward then backward of the same batch, back to back
   roofline     dominant kernel (backward): algorithmic bytes / its average
-               HIP-event duration, against MI355X's 8 TB/s
+               duration, from HIP events around a batch of back-to-back
+               backward launches on the launch stream, against 8 TB/s
+  cold_step    the same step with the backward lagging two batches behind,
+               so that its saved forward state is no longer cache resident
   cpu_baseline the reference's CPU decomposition (F.dropout + add +
                F.layer_norm, forward + autograd) on this host's cores
 
@@ -49,7 +53,7 @@ ROWS = BATCH * SEQUENCE
 DROPOUT_P = 0.1
 EPS = 1e-5
 BRANCH_BYTES = 2
-TRAFFIC_FILE = REPO / "profiles" / "rln_backward_kernel_c1_traffic.json"
+TRAFFIC_FILE = REPO / "profiles" / "rln_backward_c1_traffic.json"
 
 
 def forward_bytes(rows: int = ROWS, hidden: int = HIDDEN) -> int:
@@ -190,6 +194,19 @@ def main() -> int:
         if status_code:
             raise RuntimeError(_cabi.last_error())
 
+    def timed(body, count: int) -> float:
+        """Milliseconds per iteration of `body` over `count` iterations, from
+        HIP events recorded on the launch stream around the whole batch."""
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record(stream)
+        for index in range(count):
+            body(index)
+        end.record(stream)
+        end.synchronize()
+        return start.elapsed_time(end) / count
+
     torch.cuda.synchronize()
     with torch.cuda.stream(stream):
         if args.calibrate_copy_mib:
@@ -207,40 +224,42 @@ def main() -> int:
         stream.synchronize()
         print(f"[bench] warmup {args.warmup} steps done", flush=True)
 
-        # Whole-step wall time.
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        start.record(stream)
-        for step in range(args.warmup, args.warmup + args.steps):
-            launch_forward(step)
-            launch_backward(step)
-        end.record(stream)
-        end.synchronize()
-        ms_per_step = start.elapsed_time(end) / args.steps
+        # Timed region: K whole steps, forward then backward of the same batch.
+        base = args.warmup
+
+        def step_body(index):
+            launch_forward(base + index)
+            launch_backward(base + index)
+
+        ms_per_step = timed(step_body, args.steps)
         print(f"[bench] timed {args.steps} steps: {ms_per_step * 1e3:.2f} us/step", flush=True)
 
-        # Per-kernel durations: HIP events on the launch stream around each call.
-        events = []
-        base = args.warmup + args.steps
-        for step in range(base, base + args.steps):
-            marks = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
-            marks[0].record(stream)
-            launch_forward(step)
-            marks[1].record(stream)
-            launch_backward(step)
-            marks[2].record(stream)
-            events.append(marks)
-        stream.synchronize()
-    forward_ms = statistics.mean(m[0].elapsed_time(m[1]) for m in events)
-    backward_ms = statistics.mean(m[1].elapsed_time(m[2]) for m in events)
-    print(f"[bench] kernel averages: forward {forward_ms * 1e3:.2f} us, "
-          f"backward {backward_ms * 1e3:.2f} us", flush=True)
+        # Per-kernel averages: each kernel alone, back to back over the sets.
+        base += args.steps
+        forward_ms = timed(lambda index: launch_forward(base + index), args.steps)
+        base += args.steps
+        # Every set now holds the saved state of a forward; re-running the
+        # backward on it is the same work as the step's backward.
+        backward_ms = timed(lambda index: launch_backward(base + index), args.steps)
+        base += args.steps
+        print(f"[bench] kernel averages: forward {forward_ms * 1e3:.2f} us, "
+              f"backward {backward_ms * 1e3:.2f} us", flush=True)
+
+        # Cold step: the backward runs on the batch forwarded two steps earlier.
+        sets_count = len(sets)
+
+        def cold_body(index):
+            launch_forward(base + index)
+            launch_backward(base + index - 2 + sets_count)
+
+        cold_ms = timed(cold_body, args.steps)
+        print(f"[bench] cold step: {cold_ms * 1e3:.2f} us/step", flush=True)
 
     total_bytes = forward_bytes() + backward_bytes()
     value = total_bytes / (ms_per_step * 1e-3) / 1e9
     backward_gbps = backward_bytes() / (backward_ms * 1e-3) / 1e9
     forward_gbps = forward_bytes() / (forward_ms * 1e-3) / 1e9
+    cold_gbps = total_bytes / (cold_ms * 1e-3) / 1e9
 
     traffic = None
     if TRAFFIC_FILE.exists():
@@ -274,6 +293,11 @@ def main() -> int:
         "fwd_pct_of_peak": round(100.0 * forward_gbps / HBM_PEAK_GBPS, 2),
         "fwd_us": round(forward_ms * 1e3, 3),
         "bwd_us": round(backward_ms * 1e3, 3),
+        "cold_step": {
+            "us_per_step": round(cold_ms * 1e3, 3),
+            "gbps": round(cold_gbps, 2),
+            "pct_of_peak": round(100.0 * cold_gbps / HBM_PEAK_GBPS, 2),
+        },
         "algorithmic_bytes_per_step": total_bytes,
         "roofline": {
             "bound": "hbm",

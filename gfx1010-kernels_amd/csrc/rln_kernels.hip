@@ -7,12 +7,15 @@
 //
 //  * One wavefront owns one row (two rows when H/4 is not a multiple of 64,
 //    i.e. H = 128 and 384: each half-wave of 32 lanes owns a row). A lane
-//    holds kV float4 vectors of its row in registers, so both row reductions
-//    run inside the wave with DPP row operations plus v_readlane - no LDS,
-//    no barriers.
-//  * Loads and stores are 128-bit (64-bit for four fp16 values); a
-//    scalar-access variant of every kernel serves misaligned pointers with
-//    the identical arithmetic, so both variants are bitwise equal.
+//    holds kV four-element vectors of its row in registers, so both row
+//    reductions run inside the wave with DPP row operations plus
+//    v_readlane - no LDS, no barriers.
+//  * Loads and stores are 128-bit (64-bit for four fp16 values) and marked
+//    non-temporal: every byte of the op is touched exactly once per kernel,
+//    so the accesses stream through the caches instead of displacing lines
+//    other work may reuse. A scalar-access variant of every kernel serves
+//    misaligned pointers with the identical arithmetic, so both variants are
+//    bitwise equal.
 //  * Waves walk rows with a grid-stride loop over a grid that depends only on
 //    (rows, H), never on the device, so the dropout stream and the
 //    deterministic parameter-gradient order are reproducible anywhere.
@@ -24,9 +27,11 @@
 //  * The backward kernel produces grad_x and grad_branch AND accumulates
 //    the weight/bias gradients from the same registers, so g_y and updated
 //    are read once (the reference reads them a second time in its separate
-//    parameter kernels, :727-869). Per-block partial sums are combined with
-//    hardware fp32 atomics (default) or written to a workspace and reduced
-//    in a fixed order by a second kernel (deterministic mode).
+//    parameter kernels, :727-869). Each block combines its waves' sums in a
+//    fixed order in LDS and writes one [2, H] partial; a second kernel adds
+//    the partials in ascending block order (bitwise reproducible). The
+//    non-deterministic mode combines the block partials with hardware fp32
+//    atomics instead.
 //
 // Arithmetic that the tests hold bit-exact follows the reference:
 //  * dropped branch = round_to_branch_dtype(float(b) * keep * scale),
@@ -46,22 +51,49 @@
 
 #include "rln.h"
 
+// Launch-shape constants. They are part of the deterministic contract: the
+// grid is a function of (rows, H) and these values only.
+#ifndef RLN_FWD_MAX_BLOCKS
+#define RLN_FWD_MAX_BLOCKS 2048
+#endif
+#ifndef RLN_BWD_MAX_BLOCKS
+#define RLN_BWD_MAX_BLOCKS 256
+#endif
+#ifndef RLN_BWD_THREADS
+#define RLN_BWD_THREADS 512
+#endif
+#ifndef RLN_ATOMIC_PARAMETERS
+#define RLN_ATOMIC_PARAMETERS 1
+#endif
+#ifndef RLN_FWD_PREFETCH
+#define RLN_FWD_PREFETCH 1
+#endif
+#ifndef RLN_BWD_PREFETCH
+#define RLN_BWD_PREFETCH 1
+#endif
+#ifndef RLN_NT_LOADS
+#define RLN_NT_LOADS 1
+#endif
+#ifndef RLN_NT_STORES
+#define RLN_NT_STORES 1
+#endif
+
 namespace {
 
 constexpr int kWaveSize = 64;
-constexpr int kBlockThreads = 256;
-constexpr int kBlockWaves = kBlockThreads / kWaveSize;
-// Upper bound on blocks per launch: 2048 blocks x 4 waves = 8192 waves,
-// i.e. 32 resident waves on each of MI355X's 256 CUs.
-#ifndef RLN_MAX_BLOCKS
-#define RLN_MAX_BLOCKS 2048
-#endif
-constexpr int64_t kMaxBlocks = RLN_MAX_BLOCKS;
+constexpr int kForwardThreads = 256;
+constexpr int kBackwardThreads = RLN_BWD_THREADS;
+constexpr int64_t kForwardMaxBlocks = RLN_FWD_MAX_BLOCKS;
+constexpr int64_t kBackwardMaxBlocks = RLN_BWD_MAX_BLOCKS;
+constexpr bool kForwardPrefetch = RLN_FWD_PREFETCH != 0;
+constexpr bool kBackwardPrefetch = RLN_BWD_PREFETCH != 0;
+static_assert(kBackwardThreads % kWaveSize == 0 && kBackwardThreads <= 1024, "backward block");
 
 constexpr int64_t kSupportedHidden[] = {128, 256, 384, 512, 768, 1024};
 
 using half_t = _Float16;
-typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 
 // ----------------------------------------------------------------------------
 // Error reporting.
@@ -95,7 +127,7 @@ int check_launch(const char* what) {
 
 template <int H>
 struct Geometry {
-    static constexpr int kVectors = H / 4;  // float4 vectors per row
+    static constexpr int kVectors = H / 4;  // four-element vectors per row
     static constexpr int kLanes = (kVectors % kWaveSize == 0) ? 64 : 32;
     static constexpr int kV = kVectors / kLanes;  // vectors per lane
     static constexpr int kRowsPerWave = kWaveSize / kLanes;
@@ -108,12 +140,29 @@ int64_t rows_per_wave(int64_t hidden) {
     return ((hidden / 4) % kWaveSize == 0) ? 1 : 2;
 }
 
-// Blocks for a launch over `rows`: enough for one row (group) per wave, capped
-// at kMaxBlocks; a function of (rows, hidden) only.
-int64_t launch_blocks(int64_t rows, int64_t hidden) {
-    const int64_t waves = (rows + rows_per_wave(hidden) - 1) / rows_per_wave(hidden);
-    const int64_t blocks = (waves + kBlockWaves - 1) / kBlockWaves;
-    return blocks < kMaxBlocks ? blocks : kMaxBlocks;
+// Blocks for a launch over `rows`: enough for `groups_per_wave` row groups
+// per wave (a group = the rows one wave handles at once), capped; a function
+// of (rows, hidden) only.
+int64_t launch_blocks(int64_t rows, int64_t hidden, int threads, int64_t cap,
+                      int64_t groups_per_wave) {
+    const int64_t groups = (rows + rows_per_wave(hidden) - 1) / rows_per_wave(hidden);
+    const int64_t waves = (groups + groups_per_wave - 1) / groups_per_wave;
+    const int64_t waves_per_block = threads / kWaveSize;
+    const int64_t blocks = (waves + waves_per_block - 1) / waves_per_block;
+    return blocks < cap ? blocks : cap;
+}
+
+// The forward gives each wave at least two row groups so that its
+// look-ahead load overlaps a row's computation; with 256-thread blocks and
+// ~100 VGPRs per lane the cap of 2048 blocks is two waves of residency.
+int64_t forward_blocks(int64_t rows, int64_t hidden) {
+    return launch_blocks(rows, hidden, kForwardThreads, kForwardMaxBlocks, 2);
+}
+
+// The backward's grid is also the number of weight/bias partials: 256
+// blocks of 8 waves, one block per CU.
+int64_t backward_blocks(int64_t rows, int64_t hidden) {
+    return launch_blocks(rows, hidden, kBackwardThreads, kBackwardMaxBlocks, 1);
 }
 
 bool hidden_supported(int64_t hidden) {
@@ -209,68 +258,90 @@ struct PhiloxArgs {
 };
 
 // ----------------------------------------------------------------------------
-// Global memory access. Aligned = 128-bit accesses (64-bit for 4 x fp16);
-// otherwise element accesses with the same values.
+// Global memory access. Aligned = one 128-bit access (64-bit for 4 x fp16);
+// otherwise element accesses with the same values. Streaming accesses carry
+// the non-temporal hint.
+
+template <typename T>
+__device__ __forceinline__ T stream_load(const T* pointer) {
+#if RLN_NT_LOADS
+    return __builtin_nontemporal_load(pointer);
+#else
+    return *pointer;
+#endif
+}
+
+template <typename T>
+__device__ __forceinline__ void stream_store(T value, T* pointer) {
+#if RLN_NT_STORES
+    __builtin_nontemporal_store(value, pointer);
+#else
+    *pointer = value;
+#endif
+}
 
 template <bool Aligned>
-__device__ __forceinline__ float4 load4(const float* __restrict__ pointer) {
+__device__ __forceinline__ f32x4 load4(const float* __restrict__ pointer) {
     if constexpr (Aligned) {
-        return *reinterpret_cast<const float4*>(pointer);
+        return stream_load(reinterpret_cast<const f32x4*>(pointer));
     } else {
-        return make_float4(pointer[0], pointer[1], pointer[2], pointer[3]);
+        return f32x4{stream_load(pointer), stream_load(pointer + 1), stream_load(pointer + 2),
+                     stream_load(pointer + 3)};
     }
 }
 
 template <bool Aligned>
-__device__ __forceinline__ void store4(float* __restrict__ pointer, float4 value) {
+__device__ __forceinline__ void store4(float* __restrict__ pointer, f32x4 value) {
     if constexpr (Aligned) {
-        *reinterpret_cast<float4*>(pointer) = value;
+        stream_store(value, reinterpret_cast<f32x4*>(pointer));
     } else {
-        pointer[0] = value.x;
-        pointer[1] = value.y;
-        pointer[2] = value.z;
-        pointer[3] = value.w;
+        stream_store(value.x, pointer);
+        stream_store(value.y, pointer + 1);
+        stream_store(value.z, pointer + 2);
+        stream_store(value.w, pointer + 3);
+    }
+}
+
+// Parameters (weight, bias): ordinary cached loads, every wave reads them.
+template <bool Aligned>
+__device__ __forceinline__ f32x4 load_parameter4(const float* __restrict__ pointer) {
+    if constexpr (Aligned) {
+        return *reinterpret_cast<const f32x4*>(pointer);
+    } else {
+        return f32x4{pointer[0], pointer[1], pointer[2], pointer[3]};
     }
 }
 
 template <typename B, bool Aligned>
-__device__ __forceinline__ float4 load_branch4(const B* __restrict__ pointer) {
+__device__ __forceinline__ f32x4 load_branch4(const B* __restrict__ pointer) {
     if constexpr (sizeof(B) == 4) {
         return load4<Aligned>(reinterpret_cast<const float*>(pointer));
     } else if constexpr (Aligned) {
-        const half4_t packed = *reinterpret_cast<const half4_t*>(pointer);
-        return make_float4(
-            static_cast<float>(packed.x),
-            static_cast<float>(packed.y),
-            static_cast<float>(packed.z),
-            static_cast<float>(packed.w));
+        return __builtin_convertvector(
+            stream_load(reinterpret_cast<const f16x4*>(pointer)), f32x4);
     } else {
-        return make_float4(
-            static_cast<float>(pointer[0]),
-            static_cast<float>(pointer[1]),
-            static_cast<float>(pointer[2]),
-            static_cast<float>(pointer[3]));
+        return f32x4{
+            static_cast<float>(stream_load(pointer)),
+            static_cast<float>(stream_load(pointer + 1)),
+            static_cast<float>(stream_load(pointer + 2)),
+            static_cast<float>(stream_load(pointer + 3))};
     }
 }
 
 template <typename B, bool Aligned>
-__device__ __forceinline__ void store_branch4(B* __restrict__ pointer, float4 value) {
+__device__ __forceinline__ void store_branch4(B* __restrict__ pointer, f32x4 value) {
     if constexpr (sizeof(B) == 4) {
         store4<Aligned>(reinterpret_cast<float*>(pointer), value);
     } else {
         // float -> _Float16 conversions round to nearest even.
-        half4_t packed;
-        packed.x = static_cast<half_t>(value.x);
-        packed.y = static_cast<half_t>(value.y);
-        packed.z = static_cast<half_t>(value.z);
-        packed.w = static_cast<half_t>(value.w);
+        const f16x4 packed = __builtin_convertvector(value, f16x4);
         if constexpr (Aligned) {
-            *reinterpret_cast<half4_t*>(pointer) = packed;
+            stream_store(packed, reinterpret_cast<f16x4*>(pointer));
         } else {
-            pointer[0] = packed.x;
-            pointer[1] = packed.y;
-            pointer[2] = packed.z;
-            pointer[3] = packed.w;
+            stream_store(packed.x, pointer);
+            stream_store(packed.y, pointer + 1);
+            stream_store(packed.z, pointer + 2);
+            stream_store(packed.w, pointer + 3);
         }
     }
 }
@@ -285,19 +356,26 @@ __device__ __forceinline__ float round_to_branch(float value) {
     }
 }
 
-__device__ __forceinline__ float4 zero4() {
-    return make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+__device__ __forceinline__ f32x4 zero4() {
+    return f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 }
 
-__device__ __forceinline__ float sum4(float4 value) {
+__device__ __forceinline__ float sum4(f32x4 value) {
     return (value.x + value.y) + (value.z + value.w);
 }
 
 // ----------------------------------------------------------------------------
 // Forward kernel.
 
+// The global values the forward reads for one row, held in registers.
+template <int V>
+struct ForwardRow {
+    f32x4 x[V];
+    f32x4 branch[V];
+};
+
 template <int H, typename B, bool Aligned>
-__global__ __launch_bounds__(kBlockThreads)
+__global__ __launch_bounds__(kForwardThreads)
 void rln_forward_kernel(
     const float* __restrict__ x,
     const B* __restrict__ branch,
@@ -317,21 +395,21 @@ void rln_forward_kernel(
     using G = Geometry<H>;
     constexpr int L = G::kLanes;
     constexpr int V = G::kV;
+    constexpr int kWaves = kForwardThreads / kWaveSize;
     constexpr float kInvHidden = 1.0f / static_cast<float>(H);
 
     const int lane = threadIdx.x & (kWaveSize - 1);
     const int sub = lane / L;
     const int l = lane % L;
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kBlockWaves
-        + (threadIdx.x / kWaveSize);
-    const int64_t wave_count = static_cast<int64_t>(gridDim.x) * kBlockWaves;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x / kWaveSize);
+    const int64_t wave_count = static_cast<int64_t>(gridDim.x) * kWaves;
 
-    float4 w[V];
-    float4 b[V];
+    f32x4 w[V];
+    f32x4 b[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) {
-        w[v] = load4<Aligned>(weight + (v * L + l) * 4);
-        b[v] = load4<Aligned>(bias + (v * L + l) * 4);
+        w[v] = load_parameter4<Aligned>(weight + (v * L + l) * 4);
+        b[v] = load_parameter4<Aligned>(bias + (v * L + l) * 4);
     }
 
     uint32_t key0 = 0;
@@ -348,23 +426,30 @@ void rln_forward_kernel(
         position = offset / 4;
     }
 
-    for (int64_t first = wave * G::kRowsPerWave; first < rows;
-         first += wave_count * G::kRowsPerWave) {
-        const int64_t row = first + sub;
+    // Loads x and the branch of one row; rows past the end read nothing.
+    auto load_row = [&](ForwardRow<V>& r, int64_t row) {
         const bool valid = row < rows;
         const int64_t base = row * H;
-
-        float4 u[V];
-        uint32_t keep_bits[V];
 #pragma unroll
         for (int v = 0; v < V; ++v) {
             const int column = (v * L + l) * 4;
-            float4 xv = zero4();
-            float4 bv = zero4();
+            r.x[v] = zero4();
+            r.branch[v] = zero4();
             if (valid) {
-                xv = load4<Aligned>(x + base + column);
-                bv = load_branch4<B, Aligned>(branch + base + column);
+                r.x[v] = load4<Aligned>(x + base + column);
+                r.branch[v] = load_branch4<B, Aligned>(branch + base + column);
             }
+        }
+    };
+
+    auto process_row = [&](const ForwardRow<V>& r, int64_t row) {
+        const bool valid = row < rows;
+        const int64_t base = row * H;
+        f32x4 u[V];
+        uint32_t keep_bits[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+            f32x4 bv = r.branch[v];
             keep_bits[v] = 0;
             if (dropout) {
                 const uint64_t group = static_cast<uint64_t>(row) * (H / 4) + (v * L + l);
@@ -386,9 +471,9 @@ void rln_forward_kernel(
                 bv.w = round_to_branch<B>(bv.w * static_cast<float>(k3) * scale);
                 keep_bits[v] = k0 | (k1 << 1) | (k2 << 2) | (k3 << 3);
             }
-            u[v] = make_float4(xv.x + bv.x, xv.y + bv.y, xv.z + bv.z, xv.w + bv.w);
+            u[v] = r.x[v] + bv;
             if (valid) {
-                store4<Aligned>(updated + base + column, u[v]);
+                store4<Aligned>(updated + base + (v * L + l) * 4, u[v]);
             }
         }
 
@@ -397,7 +482,7 @@ void rln_forward_kernel(
             for (int v = 0; v < V; ++v) {
                 const uint32_t word = or8(keep_bits[v] << (4 * (l & 7)));
                 if (valid && (l & 7) == 0) {
-                    mask[row * G::kMaskWords + (v * L + l) / 8] = word;
+                    stream_store(word, mask + row * G::kMaskWords + (v * L + l) / 8);
                 }
             }
         }
@@ -412,7 +497,7 @@ void rln_forward_kernel(
         float square = 0.0f;
 #pragma unroll
         for (int v = 0; v < V; ++v) {
-            u[v] = make_float4(u[v].x - mean, u[v].y - mean, u[v].z - mean, u[v].w - mean);
+            u[v] = u[v] - mean;
             square += (u[v].x * u[v].x + u[v].y * u[v].y)
                 + (u[v].z * u[v].z + u[v].w * u[v].w);
         }
@@ -427,13 +512,33 @@ void rln_forward_kernel(
 #pragma unroll
             for (int v = 0; v < V; ++v) {
                 const int column = (v * L + l) * 4;
-                const float4 y = make_float4(
+                const f32x4 y = {
                     __builtin_fmaf(u[v].x * rstd, w[v].x, b[v].x),
                     __builtin_fmaf(u[v].y * rstd, w[v].y, b[v].y),
                     __builtin_fmaf(u[v].z * rstd, w[v].z, b[v].z),
-                    __builtin_fmaf(u[v].w * rstd, w[v].w, b[v].w));
+                    __builtin_fmaf(u[v].w * rstd, w[v].w, b[v].w)};
                 store4<Aligned>(normalized + base + column, y);
             }
+        }
+    };
+
+    // One row of look-ahead: the next row's loads are in flight while the
+    // current row is computed and stored.
+    const int64_t stride = wave_count * G::kRowsPerWave;
+    int64_t first = wave * G::kRowsPerWave;
+    ForwardRow<V> current;
+    if constexpr (kForwardPrefetch) {
+        load_row(current, first + sub);
+    }
+    for (; first < rows; first += stride) {
+        if constexpr (kForwardPrefetch) {
+            ForwardRow<V> next;
+            load_row(next, first + stride + sub);
+            process_row(current, first + sub);
+            current = next;
+        } else {
+            load_row(current, first + sub);
+            process_row(current, first + sub);
         }
     }
 }
@@ -441,16 +546,27 @@ void rln_forward_kernel(
 // ----------------------------------------------------------------------------
 // Backward kernel: input gradients plus per-block weight/bias partial sums.
 
+// Every global value the backward reads for one row, held in registers.
+template <int V>
+struct BackwardRow {
+    f32x4 u[V];
+    f32x4 gy[V];
+    f32x4 gu[V];
+    uint32_t keep_bits[V];
+    float mean;
+    float rstd;
+};
+
 enum BackwardFlags : int {
     kHasGradUpdated = 1,
     kHasGradNormalized = 2,
     kDropout = 4,
     kParameters = 8,
-    kDeterministic = 16,
+    kPartials = 16,  // write per-block partials (else fp32 atomics)
 };
 
 template <int H, typename B, bool Aligned>
-__global__ __launch_bounds__(kBlockThreads)
+__global__ __launch_bounds__(kBackwardThreads)
 void rln_backward_kernel(
     const float* __restrict__ grad_updated,
     const float* __restrict__ grad_normalized,
@@ -470,77 +586,72 @@ void rln_backward_kernel(
     using G = Geometry<H>;
     constexpr int L = G::kLanes;
     constexpr int V = G::kV;
+    constexpr int kWaves = kBackwardThreads / kWaveSize;
     constexpr float kInvHidden = 1.0f / static_cast<float>(H);
 
     const int lane = threadIdx.x & (kWaveSize - 1);
     const int sub = lane / L;
     const int l = lane % L;
     const int wave_in_block = threadIdx.x / kWaveSize;
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kBlockWaves + wave_in_block;
-    const int64_t wave_count = static_cast<int64_t>(gridDim.x) * kBlockWaves;
+    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWaves + wave_in_block;
+    const int64_t wave_count = static_cast<int64_t>(gridDim.x) * kWaves;
 
     const bool has_gu = flags & kHasGradUpdated;
     const bool has_gy = flags & kHasGradNormalized;
     const bool dropout = flags & kDropout;
     const bool parameters = flags & kParameters;
 
-    float4 w[V];
-    float4 acc_w[V];
-    float4 acc_b[V];
+    f32x4 w[V];
+    f32x4 acc_w[V];
+    f32x4 acc_b[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) {
-        w[v] = load4<Aligned>(weight + (v * L + l) * 4);
+        w[v] = load_parameter4<Aligned>(weight + (v * L + l) * 4);
         acc_w[v] = zero4();
         acc_b[v] = zero4();
     }
 
-    for (int64_t first = wave * G::kRowsPerWave; first < rows;
-         first += wave_count * G::kRowsPerWave) {
-        const int64_t row = first + sub;
+    // Loads every global value of one row into registers; rows past the end
+    // read nothing and hold zeros.
+    auto load_row = [&](BackwardRow<V>& r, int64_t row) {
         const bool valid = row < rows;
         const int64_t base = row * H;
-        const float mean = valid ? mean_in[row] : 0.0f;
-        const float rstd = valid ? rstd_in[row] : 0.0f;
-
-        // Every global load of the row is issued before the first reduction so
-        // that the row costs one memory round trip.
-        float4 xhat[V];
-        float4 gy[V];
-        float4 gu[V];
-        uint32_t keep_bits[V];
+        r.mean = valid ? mean_in[row] : 0.0f;
+        r.rstd = valid ? rstd_in[row] : 0.0f;
 #pragma unroll
         for (int v = 0; v < V; ++v) {
             const int column = (v * L + l) * 4;
-            xhat[v] = zero4();
-            gy[v] = zero4();
-            gu[v] = zero4();
-            keep_bits[v] = 0;
+            r.u[v] = zero4();
+            r.gy[v] = zero4();
+            r.gu[v] = zero4();
+            r.keep_bits[v] = 0;
             if (valid) {
-                xhat[v] = load4<Aligned>(updated + base + column);
+                r.u[v] = load4<Aligned>(updated + base + column);
                 if (has_gy) {
-                    gy[v] = load4<Aligned>(grad_normalized + base + column);
+                    r.gy[v] = load4<Aligned>(grad_normalized + base + column);
                 }
                 if (has_gu) {
-                    gu[v] = load4<Aligned>(grad_updated + base + column);
+                    r.gu[v] = load4<Aligned>(grad_updated + base + column);
                 }
                 if (dropout) {
-                    keep_bits[v] = mask[row * G::kMaskWords + (v * L + l) / 8] >> (4 * (l & 7));
+                    r.keep_bits[v] =
+                        mask[row * G::kMaskWords + (v * L + l) / 8] >> (4 * (l & 7));
                 }
             }
         }
+    };
 
+    // Input gradients of one row and its contribution to the parameter sums.
+    auto process_row = [&](const BackwardRow<V>& r, int64_t row) {
+        const bool valid = row < rows;
+        const int64_t base = row * H;
+        f32x4 xhat[V];
         float sum_q = 0.0f;
         float sum_qx = 0.0f;
 #pragma unroll
         for (int v = 0; v < V; ++v) {
-            const float4 uv = xhat[v];
-            xhat[v] = make_float4(
-                (uv.x - mean) * rstd,
-                (uv.y - mean) * rstd,
-                (uv.z - mean) * rstd,
-                (uv.w - mean) * rstd);
-            const float4 q = make_float4(
-                gy[v].x * w[v].x, gy[v].y * w[v].y, gy[v].z * w[v].z, gy[v].w * w[v].w);
+            xhat[v] = (r.u[v] - r.mean) * r.rstd;
+            const f32x4 q = r.gy[v] * w[v];
             sum_q += sum4(q);
             sum_qx += (q.x * xhat[v].x + q.y * xhat[v].y)
                 + (q.z * xhat[v].z + q.w * xhat[v].w);
@@ -557,18 +668,14 @@ void rln_backward_kernel(
 #pragma unroll
             for (int v = 0; v < V; ++v) {
                 const int column = (v * L + l) * 4;
-                float4 g = gu[v];
+                f32x4 g = r.gu[v];
                 if (has_gy) {
-                    const float4 q = make_float4(
-                        gy[v].x * w[v].x, gy[v].y * w[v].y, gy[v].z * w[v].z, gy[v].w * w[v].w);
-                    g.x = g.x + rstd * ((q.x - mean_q) - xhat[v].x * mean_qx);
-                    g.y = g.y + rstd * ((q.y - mean_q) - xhat[v].y * mean_qx);
-                    g.z = g.z + rstd * ((q.z - mean_q) - xhat[v].z * mean_qx);
-                    g.w = g.w + rstd * ((q.w - mean_q) - xhat[v].w * mean_qx);
+                    const f32x4 q = r.gy[v] * w[v];
+                    g = g + r.rstd * ((q - mean_q) - xhat[v] * mean_qx);
                 }
                 store4<Aligned>(grad_x + base + column, g);
                 if (dropout) {
-                    const uint32_t bits = keep_bits[v];
+                    const uint32_t bits = r.keep_bits[v];
                     g.x = g.x * (static_cast<float>(bits & 1u) * scale);
                     g.y = g.y * (static_cast<float>((bits >> 1) & 1u) * scale);
                     g.z = g.z * (static_cast<float>((bits >> 2) & 1u) * scale);
@@ -581,15 +688,32 @@ void rln_backward_kernel(
         if (parameters) {
 #pragma unroll
             for (int v = 0; v < V; ++v) {
-                acc_w[v].x = __builtin_fmaf(gy[v].x, xhat[v].x, acc_w[v].x);
-                acc_w[v].y = __builtin_fmaf(gy[v].y, xhat[v].y, acc_w[v].y);
-                acc_w[v].z = __builtin_fmaf(gy[v].z, xhat[v].z, acc_w[v].z);
-                acc_w[v].w = __builtin_fmaf(gy[v].w, xhat[v].w, acc_w[v].w);
-                acc_b[v].x += gy[v].x;
-                acc_b[v].y += gy[v].y;
-                acc_b[v].z += gy[v].z;
-                acc_b[v].w += gy[v].w;
+                acc_w[v].x = __builtin_fmaf(r.gy[v].x, xhat[v].x, acc_w[v].x);
+                acc_w[v].y = __builtin_fmaf(r.gy[v].y, xhat[v].y, acc_w[v].y);
+                acc_w[v].z = __builtin_fmaf(r.gy[v].z, xhat[v].z, acc_w[v].z);
+                acc_w[v].w = __builtin_fmaf(r.gy[v].w, xhat[v].w, acc_w[v].w);
+                acc_b[v] = acc_b[v] + r.gy[v];
             }
+        }
+    };
+
+    // Each wave walks its rows with the next row's loads in flight while the
+    // current row is reduced and stored (one row of look-ahead).
+    const int64_t stride = wave_count * G::kRowsPerWave;
+    int64_t first = wave * G::kRowsPerWave;
+    BackwardRow<V> current;
+    if constexpr (kBackwardPrefetch) {
+        load_row(current, first + sub);
+    }
+    for (; first < rows; first += stride) {
+        if constexpr (kBackwardPrefetch) {
+            BackwardRow<V> next;
+            load_row(next, first + stride + sub);
+            process_row(current, first + sub);
+            current = next;
+        } else {
+            load_row(current, first + sub);
+            process_row(current, first + sub);
         }
     }
 
@@ -597,34 +721,30 @@ void rln_backward_kernel(
         return;
     }
 
-    // Combine the block's partial sums in a fixed order: for every column,
-    // waves 0..3 and, within a wave, row slots 0..kRowsPerWave-1.
-    __shared__ float4 staging[kBlockWaves][kWaveSize][2];
-    const bool deterministic = flags & kDeterministic;
+    // Combine the block's sums in a fixed order: for every column, waves
+    // 0..kWaves-1 and, within a wave, row slots 0..kRowsPerWave-1.
+    __shared__ f32x4 staging[kWaves][kWaveSize][2];
+    const bool write_partials = flags & kPartials;
 #pragma unroll
     for (int v = 0; v < V; ++v) {
         staging[wave_in_block][lane][0] = acc_w[v];
         staging[wave_in_block][lane][1] = acc_b[v];
         __syncthreads();
-        // L lanes x 8 floats to produce; kBlockThreads threads share them.
-        for (int entry = threadIdx.x; entry < L * 8; entry += kBlockThreads) {
+        // L lanes x 8 floats to produce; the block's threads share them.
+        for (int entry = threadIdx.x; entry < L * 8; entry += kBackwardThreads) {
             const int slot = entry / 8;
             const int which = (entry / 4) & 1;  // 0 = weight, 1 = bias
             const int component = entry & 3;
             float total = 0.0f;
 #pragma unroll
-            for (int source_wave = 0; source_wave < kBlockWaves; ++source_wave) {
+            for (int source_wave = 0; source_wave < kWaves; ++source_wave) {
 #pragma unroll
                 for (int source_sub = 0; source_sub < G::kRowsPerWave; ++source_sub) {
-                    const float4 value = staging[source_wave][source_sub * L + slot][which];
-                    total += component == 0 ? value.x
-                        : component == 1 ? value.y
-                        : component == 2 ? value.z
-                        : value.w;
+                    total += staging[source_wave][source_sub * L + slot][which][component];
                 }
             }
             const int column = (v * L + slot) * 4 + component;
-            if (deterministic) {
+            if (write_partials) {
                 partials[(static_cast<int64_t>(blockIdx.x) * 2 + which) * H + column] = total;
             } else {
                 unsafeAtomicAdd((which ? grad_bias : grad_weight) + column, total);
@@ -634,7 +754,7 @@ void rln_backward_kernel(
     }
 }
 
-// Fixed-order reduction of deterministic partials [groups][2][H] into
+// Fixed-order reduction of per-block partials [groups][2][H] into
 // grad_weight / grad_bias. Block = 16 waves over 64 consecutive entries of the
 // flattened [2][H] output; wave k sums its contiguous share of the groups in
 // ascending order, then wave sums are added in ascending wave order.
@@ -713,8 +833,8 @@ struct ForwardArgs {
 
 template <int H, typename B, bool Aligned>
 int launch_forward(const ForwardArgs& a) {
-    const dim3 grid(static_cast<unsigned>(launch_blocks(a.rows, H)));
-    rln_forward_kernel<H, B, Aligned><<<grid, kBlockThreads, 0, a.stream>>>(
+    const dim3 grid(static_cast<unsigned>(forward_blocks(a.rows, H)));
+    rln_forward_kernel<H, B, Aligned><<<grid, kForwardThreads, 0, a.stream>>>(
         a.x,
         static_cast<const B*>(a.branch),
         a.weight,
@@ -762,8 +882,8 @@ struct BackwardArgs {
 
 template <int H, typename B, bool Aligned>
 int launch_backward(const BackwardArgs& a) {
-    const dim3 grid(static_cast<unsigned>(launch_blocks(a.rows, H)));
-    rln_backward_kernel<H, B, Aligned><<<grid, kBlockThreads, 0, a.stream>>>(
+    const dim3 grid(static_cast<unsigned>(backward_blocks(a.rows, H)));
+    rln_backward_kernel<H, B, Aligned><<<grid, kBackwardThreads, 0, a.stream>>>(
         a.grad_updated,
         a.grad_normalized,
         a.updated,
@@ -835,6 +955,12 @@ int check_common(int64_t rows, int64_t hidden, int branch_dtype) {
         return fail(RLN_ERR_INVALID, "rows * hidden overflows int64");
     }
     return RLN_OK;
+}
+
+// Whether the parameter gradients of this call go through per-block partials
+// (and therefore the workspace and the reduce kernel).
+bool uses_partials(int deterministic) {
+    return deterministic || !RLN_ATOMIC_PARAMETERS;
 }
 
 }  // namespace
@@ -923,10 +1049,10 @@ int rln_forward(
 }
 
 size_t rln_backward_workspace_bytes(int64_t rows, int64_t hidden, int deterministic) {
-    if (!deterministic || rows <= 0 || !hidden_supported(hidden)) {
+    if (!uses_partials(deterministic) || rows <= 0 || !hidden_supported(hidden)) {
         return 0;
     }
-    return static_cast<size_t>(launch_blocks(rows, hidden)) * 2 * static_cast<size_t>(hidden)
+    return static_cast<size_t>(backward_blocks(rows, hidden)) * 2 * static_cast<size_t>(hidden)
         * sizeof(float);
 }
 
@@ -972,7 +1098,8 @@ int rln_backward(
         return fail(RLN_ERR_INVALID, "dropout_mask must not be null when dropout is active");
     }
     const bool parameters = grad_weight != nullptr && grad_normalized != nullptr;
-    const size_t needed = parameters ? rln_backward_workspace_bytes(rows, hidden, deterministic) : 0;
+    const bool partials = parameters && uses_partials(deterministic);
+    const size_t needed = partials ? rln_backward_workspace_bytes(rows, hidden, deterministic) : 0;
     if (needed > 0) {
         if (workspace == nullptr || workspace_bytes < needed) {
             return fail(
@@ -1006,9 +1133,9 @@ int rln_backward(
         | (grad_normalized ? kHasGradNormalized : 0)
         | (drop.active ? kDropout : 0)
         | (parameters ? kParameters : 0)
-        | (parameters && deterministic ? kDeterministic : 0);
+        | (partials ? kPartials : 0);
 
-    if (parameters && !deterministic && !accumulate_parameters) {
+    if (parameters && !partials && !accumulate_parameters) {
         rln_zero_parameters_kernel<<<dim3(static_cast<unsigned>((hidden + 255) / 256)), 256, 0, a.stream>>>(
             grad_weight, grad_bias, static_cast<int>(hidden));
         status = check_launch("rln_zero_parameters_kernel");
@@ -1034,8 +1161,8 @@ int rln_backward(
     if (status != RLN_OK) {
         return status;
     }
-    if (parameters && deterministic) {
-        const int64_t groups = launch_blocks(rows, hidden);
+    if (partials) {
+        const int64_t groups = backward_blocks(rows, hidden);
         const unsigned blocks = static_cast<unsigned>((2 * hidden + kWaveSize - 1) / kWaveSize);
         rln_parameter_reduce_kernel<<<dim3(blocks), kReduceWaves * kWaveSize, 0, a.stream>>>(
             a.partials, grad_weight, grad_bias, groups, static_cast<int>(hidden),
@@ -1078,7 +1205,7 @@ const char* rln_target_arch(void) {
 }
 
 const char* rln_version(void) {
-    return "0.1.0";
+    return "0.2.0";
 }
 
 }  // extern "C"

@@ -53,10 +53,12 @@ def test_size_queries():
     assert _cabi.mask_words(0, 768) == 0
     assert _cabi.backward_workspace_bytes(8192, 768, False) == 0
     assert _cabi.backward_workspace_bytes(0, 768, True) == 0
-    # One partial [2, H] per block; 4 waves per block, one row per wave (two at H=128/384).
-    assert _cabi.backward_workspace_bytes(8192, 768, True) == 2048 * 2 * 768 * 4
-    assert _cabi.backward_workspace_bytes(37, 128, True) == 5 * 2 * 128 * 4
-    assert _cabi.backward_workspace_bytes(1 << 20, 1024, True) == 2048 * 2 * 1024 * 4
+    # One partial [2, H] per block; 8 waves per block, one row per wave (two at
+    # H=128/384), at most 256 blocks.
+    assert _cabi.backward_workspace_bytes(8192, 768, True) == 256 * 2 * 768 * 4
+    assert _cabi.backward_workspace_bytes(37, 128, True) == 3 * 2 * 128 * 4
+    assert _cabi.backward_workspace_bytes(41, 768, True) == 6 * 2 * 768 * 4
+    assert _cabi.backward_workspace_bytes(1 << 20, 1024, True) == 256 * 2 * 1024 * 4
 
 
 FAKE = 1 << 20  # a non-null address; validation fails before it is touched
