@@ -25,9 +25,14 @@ Prints one JSON line:
   cpu_baseline the reference's CPU decomposition (F.dropout + add +
                F.layer_norm, forward + autograd) on this host's cores
 
-Algorithmic bytes per row (H = 768, fp16 branch, dropout mask H/8 bytes):
-  forward  H * (4 + 2 + 4 + 4) + 8 + H/8, plus 8H once (weight, bias)
-  backward H * (4 + 4 + 4 + 4 + 2) + 8 + H/8, plus 12H once (weight; dW, db)
+``--sweep`` adds one JSON line per other BASELINE.json configuration (C0, the
+C2 hidden-size sweep, C3 deterministic, the C4 cases), each with the same
+fields for its own shape.
+
+Algorithmic bytes per row (H = hidden, bb = branch bytes, mask H/8 bytes when
+dropping):
+  forward  H * (4 + bb + 4 + 4) + 8 + H/8, plus 8H once (weight, bias)
+  backward H * (4 + 4 + 4 + 4 + bb) + 8 + H/8, plus 12H once (weight; dW, db)
 """
 
 from __future__ import annotations
@@ -39,6 +44,7 @@ import platform
 import statistics
 import sys
 import time
+from dataclasses import dataclass
 from pathlib import Path
 
 REPO = Path(__file__).resolve().parent
@@ -48,20 +54,70 @@ for _path in (REPO, REPO / "gfx1010-kernels_amd"):
 
 HBM_PEAK_GBPS = 8000.0
 METRIC = "fwd & fwd+bwd achieved HBM GB/s (% of ~8 TB/s peak), rows/s at H=768"
-BATCH, SEQUENCE, HIDDEN = 8, 1024, 768
-ROWS = BATCH * SEQUENCE
-DROPOUT_P = 0.1
 EPS = 1e-5
-BRANCH_BYTES = 2
 TRAFFIC_FILE = REPO / "profiles" / "rln_backward_c1_traffic.json"
 
 
-def forward_bytes(rows: int = ROWS, hidden: int = HIDDEN) -> int:
-    return rows * (hidden * (4 + BRANCH_BYTES + 4 + 4) + 8 + hidden // 8) + 8 * hidden
+@dataclass(frozen=True)
+class Workload:
+    name: str
+    rows: int
+    hidden: int
+    half_branch: bool
+    branch_std: float
+    dropout_p: float
+    training: bool = True
+    backward: bool = True
+    deterministic: bool = False
+    x_mean: float = 0.0
+    seed: int = 1001
+
+    @property
+    def branch_bytes(self) -> int:
+        return 2 if self.half_branch else 4
+
+    @property
+    def dropping(self) -> bool:
+        return self.training and self.dropout_p > 0.0
+
+    def forward_bytes(self) -> int:
+        mask = self.hidden // 8 if self.dropping else 0
+        per_row = self.hidden * (4 + self.branch_bytes + 4 + 4) + 8 + mask
+        return self.rows * per_row + 8 * self.hidden
+
+    def backward_bytes(self) -> int:
+        if not self.backward:
+            return 0
+        mask = self.hidden // 8 if self.dropping else 0
+        per_row = self.hidden * (4 + 4 + 4 + 4 + self.branch_bytes) + 8 + mask
+        return self.rows * per_row + 12 * self.hidden
+
+    def describe(self) -> str:
+        branch = "fp16" if self.half_branch else "fp32"
+        mode = "fwd+bwd" if self.backward else "fwd"
+        reduction = "deterministic" if self.deterministic else "atomic"
+        suffix = f", {reduction} dW/db" if self.backward else ""
+        return (f"{self.name} {mode}: x fp32 [{self.rows},{self.hidden}], branch {branch}, "
+                f"dropout_p={self.dropout_p}, training={self.training}{suffix}")
 
 
-def backward_bytes(rows: int = ROWS, hidden: int = HIDDEN) -> int:
-    return rows * (hidden * (4 + 4 + 4 + 4 + BRANCH_BYTES) + 8 + hidden // 8) + 12 * hidden
+C1 = Workload("C1", 8 * 1024, 768, True, 0.5, 0.1, seed=1001)
+
+
+def sweep_workloads() -> list[Workload]:
+    """The other BASELINE.json configurations."""
+    workloads = [Workload("C0", 4 * 1024, 768, False, 1.0, 0.0, training=False,
+                          backward=False, seed=1000)]
+    for hidden in (128, 256, 384, 512, 768, 1024):
+        workloads.append(Workload(f"C2 H={hidden}", 262144, hidden, True, 1.0, 0.15,
+                                  seed=1002 + hidden))
+    workloads.append(Workload("C3", 32 * 2048, 1024, True, 0.5, 0.15, deterministic=True,
+                              seed=1003))
+    for dropout_p in (0.0, 0.1):
+        workloads.append(Workload(f"C4 tail p={dropout_p}", 3 * 4097, 384, False, 1.0,
+                                  dropout_p, x_mean=100.0, seed=1004))
+    workloads.append(Workload("C4 large", 64 * 4096, 1024, True, 1.0, 0.1, seed=1006))
+    return workloads
 
 
 def parse_args():
@@ -73,58 +129,37 @@ def parse_args():
     parser.add_argument("--cpu-seconds", type=float, default=15.0,
                         help="time budget of the CPU baseline sample")
     parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--sweep", action="store_true",
+                        help="also print one line per other BASELINE.json configuration")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="also launch one device copy of this many MiB (PMC calibration)")
     return parser.parse_args()
 
 
-def make_set(torch, seed: int):
-    """One input/output set on the device, from a seeded CPU generator."""
-    generator = torch.Generator().manual_seed(seed)
-    shape = (ROWS, HIDDEN)
-    host = {
-        "x": torch.randn(shape, generator=generator),
-        "branch": (0.5 * torch.randn(shape, generator=generator)).half(),
-        "grad_updated": torch.randn(shape, generator=generator),
-        "grad_normalized": torch.randn(shape, generator=generator),
-    }
-    tensors = {name: value.cuda() for name, value in host.items()}
-    f32 = dict(device="cuda", dtype=torch.float32)
-    tensors.update(
-        updated=torch.empty(shape, **f32),
-        normalized=torch.empty(shape, **f32),
-        mean=torch.empty(ROWS, **f32),
-        rstd=torch.empty(ROWS, **f32),
-        mask=torch.empty(ROWS * HIDDEN // 32, device="cuda", dtype=torch.int32),
-        grad_x=torch.empty(shape, **f32),
-        grad_branch=torch.empty(shape, device="cuda", dtype=torch.float16),
-        grad_weight=torch.zeros(HIDDEN, **f32),
-        grad_bias=torch.zeros(HIDDEN, **f32),
-    )
-    return tensors
-
-
-def cpu_baseline(torch, budget_seconds: float) -> dict:
-    """The reference's CPU path on this host, on a bounded sample of C1 steps."""
+def cpu_baseline(torch, workload: Workload, budget_seconds: float) -> dict:
+    """The reference's CPU path on this host, on a bounded sample of steps."""
     from oracle.torch_path import fwd_bwd_step
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    generator = torch.Generator().manual_seed(1001)
-    shape = (ROWS, HIDDEN)
+    generator = torch.Generator().manual_seed(workload.seed)
+    shape = (workload.rows, workload.hidden)
     x = torch.randn(shape, generator=generator).requires_grad_(True)
-    branch = (0.5 * torch.randn(shape, generator=generator)).half().requires_grad_(True)
-    weight = (1.0 + 0.02 * torch.randn(HIDDEN, generator=generator)).requires_grad_(True)
-    bias = (0.02 * torch.randn(HIDDEN, generator=generator)).requires_grad_(True)
+    branch = (workload.branch_std * torch.randn(shape, generator=generator))
+    branch = (branch.half() if workload.half_branch else branch).requires_grad_(True)
+    weight = (1.0 + 0.02 * torch.randn(workload.hidden, generator=generator)).requires_grad_(True)
+    bias = (0.02 * torch.randn(workload.hidden, generator=generator)).requires_grad_(True)
     grad_updated = torch.randn(shape, generator=generator)
     grad_normalized = torch.randn(shape, generator=generator)
+    step = lambda: fwd_bwd_step(x, branch, weight, bias, grad_updated,  # noqa: E731
+                                grad_normalized, workload.dropout_p, EPS)
     for _ in range(2):
-        fwd_bwd_step(x, branch, weight, bias, grad_updated, grad_normalized, DROPOUT_P, EPS)
+        step()
     samples = []
     start = time.perf_counter()
     while len(samples) < 10 or (time.perf_counter() - start < budget_seconds and len(samples) < 1000):
         began = time.perf_counter()
-        fwd_bwd_step(x, branch, weight, bias, grad_updated, grad_normalized, DROPOUT_P, EPS)
+        step()
         samples.append(time.perf_counter() - began)
     median = statistics.median(samples)
     model = "unknown"
@@ -135,17 +170,214 @@ def cpu_baseline(torch, budget_seconds: float) -> dict:
                 break
     except OSError:
         pass
+    total = workload.forward_bytes() + workload.backward_bytes()
     return {
-        "value": round((forward_bytes() + backward_bytes()) / median / 1e9, 3),
+        "value": round(total / median / 1e9, 3),
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
-        "sample": (f"{len(samples)} fwd+bwd steps of C1 [8,1024,768] (F.dropout + add + "
-                   f"F.layer_norm, autograd.grad), median {median * 1e3:.2f} ms/step, "
+        "sample": (f"{len(samples)} fwd+bwd steps of {workload.name} "
+                   f"[{workload.rows},{workload.hidden}] (F.dropout + add + F.layer_norm, "
+                   f"autograd.grad), median {median * 1e3:.2f} ms/step, "
                    f"torch {torch.__version__} on {model}"),
-        "rows_per_s": round(ROWS / median, 1),
+        "rows_per_s": round(workload.rows / median, 1),
         "ms_per_step": round(median * 1e3, 3),
     }
+
+
+class Runner:
+    """Device buffers for one workload and the C ABI launches over them."""
+
+    def __init__(self, torch, library, cabi, workload: Workload, sets: int, stream):
+        self.torch = torch
+        self.library = library
+        self.cabi = cabi
+        self.w = workload
+        self.stream = stream
+        self.handle = stream.cuda_stream
+        generator = torch.Generator().manual_seed(workload.seed)
+        self.weight = (1.0 + 0.02 * torch.randn(workload.hidden, generator=generator)).cuda()
+        self.bias = (0.02 * torch.randn(workload.hidden, generator=generator)).cuda()
+        self.sets = [self._make_set(workload.seed + 17 * index) for index in range(sets)]
+        self.workspace = None
+        workspace_bytes = cabi.backward_workspace_bytes(
+            workload.rows, workload.hidden, workload.deterministic)
+        if workload.backward and workspace_bytes:
+            self.workspace = torch.empty(workspace_bytes, device="cuda", dtype=torch.uint8)
+        self.seed = 0x5EED_0000 + workload.seed
+
+    def _make_set(self, seed: int) -> dict:
+        torch, w = self.torch, self.w
+        generator = torch.Generator(device="cuda").manual_seed(seed)
+        shape = (w.rows, w.hidden)
+        f32 = dict(device="cuda", dtype=torch.float32)
+        branch = torch.randn(shape, generator=generator, **f32) * w.branch_std
+        tensors = {
+            "x": torch.randn(shape, generator=generator, **f32) + w.x_mean,
+            "branch": branch.half() if w.half_branch else branch,
+            "updated": torch.empty(shape, **f32),
+            "normalized": torch.empty(shape, **f32),
+            "mean": torch.empty(w.rows, **f32),
+            "rstd": torch.empty(w.rows, **f32),
+            "mask": torch.empty(max(w.rows * w.hidden // 32, 1), device="cuda",
+                                dtype=torch.int32),
+        }
+        if w.backward:
+            tensors.update(
+                grad_updated=torch.randn(shape, generator=generator, **f32),
+                grad_normalized=torch.randn(shape, generator=generator, **f32),
+                grad_x=torch.empty(shape, **f32),
+                grad_branch=torch.empty(shape, device="cuda",
+                                        dtype=torch.float16 if w.half_branch else torch.float32),
+                grad_weight=torch.zeros(w.hidden, **f32),
+                grad_bias=torch.zeros(w.hidden, **f32),
+            )
+        return tensors
+
+    @property
+    def dtype(self) -> int:
+        return self.cabi.RLN_DTYPE_F16 if self.w.half_branch else self.cabi.RLN_DTYPE_F32
+
+    def forward(self, step: int):
+        t, w = self.sets[step % len(self.sets)], self.w
+        philox = self.cabi.RlnPhilox(self.seed, 4 * step, None, None)
+        status = self.library.rln_forward(
+            t["x"].data_ptr(), t["branch"].data_ptr(), self.dtype, self.weight.data_ptr(),
+            self.bias.data_ptr(), t["updated"].data_ptr(), t["normalized"].data_ptr(),
+            t["mean"].data_ptr(), t["rstd"].data_ptr(), t["mask"].data_ptr(), w.rows, w.hidden,
+            w.dropout_p, EPS, int(w.training), philox, self.handle)
+        if status:
+            raise RuntimeError(self.cabi.last_error())
+
+    def backward(self, step: int):
+        t, w = self.sets[step % len(self.sets)], self.w
+        workspace = self.workspace
+        status = self.library.rln_backward(
+            t["grad_updated"].data_ptr(), t["grad_normalized"].data_ptr(),
+            t["updated"].data_ptr(), self.weight.data_ptr(), t["mean"].data_ptr(),
+            t["rstd"].data_ptr(), t["mask"].data_ptr(), t["grad_x"].data_ptr(),
+            t["grad_branch"].data_ptr(), self.dtype, t["grad_weight"].data_ptr(),
+            t["grad_bias"].data_ptr(), w.rows, w.hidden, w.dropout_p, int(w.training),
+            int(w.deterministic), 1,
+            workspace.data_ptr() if workspace is not None else None,
+            workspace.numel() if workspace is not None else 0, self.handle)
+        if status:
+            raise RuntimeError(self.cabi.last_error())
+
+    def step(self, index: int):
+        self.forward(index)
+        if self.w.backward:
+            self.backward(index)
+
+    def timed(self, body, count: int) -> float:
+        """Milliseconds per iteration of `body` over `count` iterations, from
+        HIP events recorded on the launch stream around the whole batch."""
+        torch = self.torch
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record(self.stream)
+        for index in range(count):
+            body(index)
+        end.record(self.stream)
+        end.synchronize()
+        return start.elapsed_time(end) / count
+
+    def measure(self, warmup: int, steps: int) -> dict:
+        w = self.w
+        for index in range(warmup):
+            self.step(index)
+        self.stream.synchronize()
+        base = warmup
+        step_ms = self.timed(lambda i: self.step(base + i), steps)
+        base += steps
+        forward_ms = self.timed(lambda i: self.forward(base + i), steps)
+        base += steps
+        result = {"step_ms": step_ms, "forward_ms": forward_ms}
+        if w.backward:
+            # Every set now holds the saved state of a forward; re-running the
+            # backward on it is the same work as the step's backward.
+            result["backward_ms"] = self.timed(lambda i: self.backward(base + i), steps)
+            base += steps
+            # Backward on the set forwarded `lag` steps earlier (two, or one
+            # when only two sets rotate).
+            lag = min(2, len(self.sets) - 1)
+
+            def cold(index):
+                self.forward(base + index)
+                self.backward(base + index - lag + len(self.sets))
+
+            result["cold_ms"] = self.timed(cold, steps)
+        return result
+
+
+def gbps(nbytes: int, ms: float) -> float:
+    return nbytes / (ms * 1e-3) / 1e9
+
+
+def result_line(torch, workload: Workload, timing: dict, steps: int, warmup: int,
+                sets: int, traffic) -> dict:
+    total = workload.forward_bytes() + workload.backward_bytes()
+    value = gbps(total, timing["step_ms"])
+    forward_gbps = gbps(workload.forward_bytes(), timing["forward_ms"])
+    if workload.backward:
+        dominant, dominant_ms = "rln_backward_kernel", timing["backward_ms"]
+        dominant_bytes = workload.backward_bytes()
+    else:
+        dominant, dominant_ms = "rln_forward_kernel", timing["forward_ms"]
+        dominant_bytes = workload.forward_bytes()
+    branch_type = "_Float16" if workload.half_branch else "float"
+    dominant_gbps = gbps(dominant_bytes, dominant_ms)
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(timing["step_ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded torch.randn, BASELINE.json distributions)",
+        "config": {
+            "workload": workload.describe() + f", {sets} rotated input sets",
+            "rows": workload.rows,
+            "hidden": workload.hidden,
+            "dropout_p": workload.dropout_p,
+            "branch_dtype": "float16" if workload.half_branch else "float32",
+            "parallelism": "single GPU",
+        },
+        "pct_of_peak": round(100.0 * value / HBM_PEAK_GBPS, 2),
+        "rows_per_s": round(workload.rows / (timing["step_ms"] * 1e-3), 1),
+        "fwd_gbps": round(forward_gbps, 2),
+        "fwd_pct_of_peak": round(100.0 * forward_gbps / HBM_PEAK_GBPS, 2),
+        "fwd_us": round(timing["forward_ms"] * 1e3, 3),
+        "algorithmic_bytes_per_step": total,
+        "roofline": {
+            "bound": "hbm",
+            "kernel": f"{dominant}<{workload.hidden}, {branch_type}, true>",
+            "achieved": round(dominant_gbps, 2),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(dominant_gbps / HBM_PEAK_GBPS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes_per_launch": dominant_bytes,
+        },
+        "cpu_baseline": None,
+        "device": torch.cuda.get_device_name(0),
+        "host": platform.node(),
+    }
+    if workload.backward:
+        cold = gbps(total, timing["cold_ms"])
+        line["bwd_us"] = round(timing["backward_ms"] * 1e3, 3)
+        line["cold_step"] = {
+            "us_per_step": round(timing["cold_ms"] * 1e3, 3),
+            "gbps": round(cold, 2),
+            "pct_of_peak": round(100.0 * cold / HBM_PEAK_GBPS, 2),
+        }
+    return line
 
 
 def main() -> int:
@@ -163,51 +395,12 @@ def main() -> int:
     if not status.available:
         raise RuntimeError(f"native backend unavailable: {status.reason}")
     library = _cabi.library()
-
-    generator = torch.Generator().manual_seed(1001)
-    weight = (1.0 + 0.02 * torch.randn(HIDDEN, generator=generator)).cuda()
-    bias = (0.02 * torch.randn(HIDDEN, generator=generator)).cuda()
-    sets = [make_set(torch, 1001 + index) for index in range(args.sets)]
     stream = torch.cuda.Stream()
-    handle = stream.cuda_stream
-    seed = 0x5EED_1001
 
-    def launch_forward(step: int):
-        t = sets[step % len(sets)]
-        philox = _cabi.RlnPhilox(seed, 4 * step, None, None)
-        status_code = library.rln_forward(
-            t["x"].data_ptr(), t["branch"].data_ptr(), _cabi.RLN_DTYPE_F16, weight.data_ptr(),
-            bias.data_ptr(), t["updated"].data_ptr(), t["normalized"].data_ptr(),
-            t["mean"].data_ptr(), t["rstd"].data_ptr(), t["mask"].data_ptr(), ROWS, HIDDEN,
-            DROPOUT_P, EPS, 1, philox, handle)
-        if status_code:
-            raise RuntimeError(_cabi.last_error())
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
 
-    def launch_backward(step: int):
-        t = sets[step % len(sets)]
-        status_code = library.rln_backward(
-            t["grad_updated"].data_ptr(), t["grad_normalized"].data_ptr(), t["updated"].data_ptr(),
-            weight.data_ptr(), t["mean"].data_ptr(), t["rstd"].data_ptr(), t["mask"].data_ptr(),
-            t["grad_x"].data_ptr(), t["grad_branch"].data_ptr(), _cabi.RLN_DTYPE_F16,
-            t["grad_weight"].data_ptr(), t["grad_bias"].data_ptr(), ROWS, HIDDEN, DROPOUT_P,
-            1, 0, 1, None, 0, handle)
-        if status_code:
-            raise RuntimeError(_cabi.last_error())
-
-    def timed(body, count: int) -> float:
-        """Milliseconds per iteration of `body` over `count` iterations, from
-        HIP events recorded on the launch stream around the whole batch."""
-        start = torch.cuda.Event(enable_timing=True)
-        end = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        start.record(stream)
-        for index in range(count):
-            body(index)
-        end.record(stream)
-        end.synchronize()
-        return start.elapsed_time(end) / count
-
-    torch.cuda.synchronize()
     with torch.cuda.stream(stream):
         if args.calibrate_copy_mib:
             elements = args.calibrate_copy_mib * (1 << 20) // 4
@@ -218,105 +411,31 @@ def main() -> int:
             print(f"[bench] calibration copy of {args.calibrate_copy_mib} MiB done", flush=True)
             del source, destination
 
-        for step in range(args.warmup):
-            launch_forward(step)
-            launch_backward(step)
-        stream.synchronize()
-        print(f"[bench] warmup {args.warmup} steps done", flush=True)
-
-        # Timed region: K whole steps, forward then backward of the same batch.
-        base = args.warmup
-
-        def step_body(index):
-            launch_forward(base + index)
-            launch_backward(base + index)
-
-        ms_per_step = timed(step_body, args.steps)
-        print(f"[bench] timed {args.steps} steps: {ms_per_step * 1e3:.2f} us/step", flush=True)
-
-        # Per-kernel averages: each kernel alone, back to back over the sets.
-        base += args.steps
-        forward_ms = timed(lambda index: launch_forward(base + index), args.steps)
-        base += args.steps
-        # Every set now holds the saved state of a forward; re-running the
-        # backward on it is the same work as the step's backward.
-        backward_ms = timed(lambda index: launch_backward(base + index), args.steps)
-        base += args.steps
-        print(f"[bench] kernel averages: forward {forward_ms * 1e3:.2f} us, "
-              f"backward {backward_ms * 1e3:.2f} us", flush=True)
-
-        # Cold step: the backward runs on the batch forwarded two steps earlier.
-        sets_count = len(sets)
-
-        def cold_body(index):
-            launch_forward(base + index)
-            launch_backward(base + index - 2 + sets_count)
-
-        cold_ms = timed(cold_body, args.steps)
-        print(f"[bench] cold step: {cold_ms * 1e3:.2f} us/step", flush=True)
-
-    total_bytes = forward_bytes() + backward_bytes()
-    value = total_bytes / (ms_per_step * 1e-3) / 1e9
-    backward_gbps = backward_bytes() / (backward_ms * 1e-3) / 1e9
-    forward_gbps = forward_bytes() / (forward_ms * 1e-3) / 1e9
-    cold_gbps = total_bytes / (cold_ms * 1e-3) / 1e9
-
-    traffic = None
-    if TRAFFIC_FILE.exists():
-        traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
-
-    result = {
-        "metric": METRIC,
-        "value": round(value, 2),
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 5),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic (seeded torch.randn, BASELINE.json config 1 distributions)",
-        "config": {
-            "workload": "C1 fwd+bwd: x fp32 [8,1024,768], branch fp16, dropout_p=0.1, "
-                        "atomic dW/db, 4 rotated input sets",
-            "rows": ROWS,
-            "hidden": HIDDEN,
-            "dropout_p": DROPOUT_P,
-            "branch_dtype": "float16",
-            "parallelism": "single GPU",
-        },
-        "pct_of_peak": round(100.0 * value / HBM_PEAK_GBPS, 2),
-        "rows_per_s": round(ROWS / (ms_per_step * 1e-3), 1),
-        "fwd_gbps": round(forward_gbps, 2),
-        "fwd_pct_of_peak": round(100.0 * forward_gbps / HBM_PEAK_GBPS, 2),
-        "fwd_us": round(forward_ms * 1e3, 3),
-        "bwd_us": round(backward_ms * 1e3, 3),
-        "cold_step": {
-            "us_per_step": round(cold_ms * 1e3, 3),
-            "gbps": round(cold_gbps, 2),
-            "pct_of_peak": round(100.0 * cold_gbps / HBM_PEAK_GBPS, 2),
-        },
-        "algorithmic_bytes_per_step": total_bytes,
-        "roofline": {
-            "bound": "hbm",
-            "kernel": "rln_backward_kernel<768, _Float16, true>",
-            "achieved": round(backward_gbps, 2),
-            "peak": HBM_PEAK_GBPS,
-            "unit": "GB/s",
-            "frac": round(backward_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": traffic,
-            "algorithmic_bytes_per_launch": backward_bytes(),
-        },
-        "cpu_baseline": None,
-        "device": torch.cuda.get_device_name(0),
-        "host": platform.node(),
-    }
+        runner = Runner(torch, library, _cabi, C1, args.sets, stream)
+        timing = runner.measure(args.warmup, args.steps)
+        del runner
+        print(f"[bench] C1: step {timing['step_ms'] * 1e3:.2f} us, forward "
+              f"{timing['forward_ms'] * 1e3:.2f} us, backward {timing['backward_ms'] * 1e3:.2f} us, "
+              f"cold step {timing['cold_ms'] * 1e3:.2f} us", flush=True)
+    result = result_line(torch, C1, timing, args.steps, args.warmup, args.sets, traffic)
     if not args.no_cpu_baseline:
         print(f"[bench] CPU baseline (~{args.cpu_seconds:.0f} s)", flush=True)
-        result["cpu_baseline"] = cpu_baseline(torch, args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(torch, C1, args.cpu_seconds)
     print(json.dumps(result), flush=True)
+
+    if args.sweep:
+        for workload in sweep_workloads():
+            torch.cuda.empty_cache()
+            large = workload.rows * workload.hidden >= (1 << 26)
+            sets = 2 if large else args.sets
+            steps = max(args.steps // 10, 20) if large else args.steps
+            with torch.cuda.stream(stream):
+                runner = Runner(torch, library, _cabi, workload, sets, stream)
+                timing = runner.measure(min(args.warmup, 10) if large else args.warmup, steps)
+                del runner
+            line = result_line(torch, workload, timing, steps, args.warmup, sets, None)
+            line["sweep"] = True
+            print(json.dumps(line), flush=True)
     return 0
 
 
