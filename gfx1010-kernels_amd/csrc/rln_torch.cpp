@@ -283,11 +283,12 @@ std::vector<at::Tensor> backward_impl(
     const bool launch_parameters = compute_parameter_gradients && grad_normalized.has_value();
     if (compute_parameter_gradients) {
         // Without grad_normalized the parameter gradients are exactly zero.
-        auto parameters = launch_parameters
-            ? at::empty({2, hidden}, updated.options())
-            : at::zeros({2, hidden}, updated.options());
-        grad_weight = parameters.select(0, 0);
-        grad_bias = parameters.select(0, 1);
+        // Two separate tensors (not views of one), so that no two returned
+        // gradients alias each other.
+        grad_weight = launch_parameters ? at::empty({hidden}, updated.options())
+                                        : at::zeros({hidden}, updated.options());
+        grad_bias = launch_parameters ? at::empty({hidden}, updated.options())
+                                      : at::zeros({hidden}, updated.options());
     }
     if (launch_parameters) {
         const size_t bytes = rln_backward_workspace_bytes(rows, hidden, deterministic ? 1 : 0);

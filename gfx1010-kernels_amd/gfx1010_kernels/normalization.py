@@ -33,6 +33,7 @@ import torch
 from torch.nn import functional as F
 
 from ._normalization_native import NATIVE_HIDDEN_SIZES, TARGET_ARCHITECTURE
+from ._ops import residual_layer_norm_op
 from ._status import BackendStatus
 
 MIN_HIDDEN_SIZE = 128
@@ -177,6 +178,30 @@ def _fall_back(reason, x, branch, weight, bias, dropout_p, eps, training):
     return _torch_residual_layer_norm(x, branch, weight, bias, dropout_p, eps, training)
 
 
+def _traced(x, branch, weight, bias, dropout_p, eps, training, implementation):
+    """Dispatch while ``torch.compile`` traces: the native kernels run through
+    the registered custom op (``gfx1010_kernels::rln_forward``) so the graph
+    keeps them; the backend status is not queried (the op raises at run time
+    if the extension is missing) and ``auto`` falls back without a warning."""
+    native = x.is_cuda and x.ndim >= 2 and x.shape[-1] in NATIVE_HIDDEN_SIZES
+    if implementation in _STRICT_NATIVE:
+        if not x.is_cuda:
+            raise RuntimeError(f"{_UNAVAILABLE}: x must be a HIP tensor")
+        if not native:
+            raise RuntimeError(
+                f"{_UNAVAILABLE}: native hidden size must be one of {NATIVE_HIDDEN_SIZES}"
+            )
+        return residual_layer_norm_op(x, branch, weight, bias, dropout_p, eps, training)
+    if implementation == "triton":
+        raise RuntimeError(
+            f"{TARGET_ARCHITECTURE} residual LayerNorm is unavailable: "
+            "the Triton backend is not part of the MI355X build"
+        )
+    if native and _input_reason(x, branch, weight, bias, dropout_p, eps) is None:
+        return residual_layer_norm_op(x, branch, weight, bias, dropout_p, eps, training)
+    return _torch_residual_layer_norm(x, branch, weight, bias, dropout_p, eps, training)
+
+
 def residual_layer_norm(
     x,
     branch,
@@ -191,7 +216,8 @@ def residual_layer_norm(
     """Fused ``dropout(branch) -> x + . -> LayerNorm``; returns ``(updated, normalized)``.
 
     ``updated`` is the new fp32 residual stream and ``normalized`` its
-    LayerNorm with ``weight``/``bias``. Supports first-order autograd.
+    LayerNorm with ``weight``/``bias``. Supports first-order autograd, HIP
+    graph capture and ``torch.compile``.
     """
     if implementation not in IMPLEMENTATIONS:
         raise ValueError(
@@ -199,6 +225,8 @@ def residual_layer_norm(
         )
     if implementation == "torch":
         return _torch_residual_layer_norm(x, branch, weight, bias, dropout_p, eps, training)
+    if torch.compiler.is_compiling():
+        return _traced(x, branch, weight, bias, dropout_p, eps, training, implementation)
     if implementation in _STRICT_NATIVE:
         return _strict_native(x, branch, weight, bias, dropout_p, eps, training)
 

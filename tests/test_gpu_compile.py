@@ -1,0 +1,80 @@
+"""torch.compile and the registered custom ops on the GPU.
+
+The compiled graph calls ``gfx1010_kernels::rln_forward`` / ``rln_backward``
+(the same kernels as the eager autograd function), so from the same RNG state
+a compiled training step reproduces the eager step bit for bit (weight/bias
+gradients in deterministic mode). ``backend="aot_eager"`` traces with Dynamo
+and AOTAutograd without generating code for the surrounding ops.
+"""
+
+import contextlib
+
+import pytest
+import torch
+
+from gfx1010_kernels import residual_layer_norm
+from parity import assert_bitwise, host, make_grads, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+@contextlib.contextmanager
+def deterministic_algorithms():
+    previous = torch.are_deterministic_algorithms_enabled()
+    torch.use_deterministic_algorithms(True)
+    try:
+        yield
+    finally:
+        torch.use_deterministic_algorithms(previous)
+
+
+def test_opcheck_forward_and_backward():
+    inputs = make_inputs((33, 512), torch.float16, seed=3)
+    # Without dropout the op is a pure function of its inputs, as opcheck
+    # requires (it compares several executions).
+    torch.library.opcheck(torch.ops.gfx1010_kernels.rln_forward.default,
+                          (*inputs, 0.0, 1e-5, True))
+    outputs = torch.ops.gfx1010_kernels.rln_forward(*inputs, 0.0, 1e-5, True)
+    grads = make_grads((33, 512), seed=4)
+    with deterministic_algorithms():
+        torch.library.opcheck(
+            torch.ops.gfx1010_kernels.rln_backward.default,
+            (grads[0], grads[1], outputs[0], inputs[2], outputs[2], outputs[3], outputs[4],
+             0.0, True, True))
+
+
+@pytest.mark.parametrize("implementation", ["gfx950", "auto"])
+@pytest.mark.parametrize("shape,dropout_p", [((4, 64, 768), 0.1), ((3, 97, 384), 0.0)])
+def test_compiled_step_matches_eager_bitwise(implementation, shape, dropout_p):
+    inputs = make_inputs(shape, torch.float16, seed=11)
+    grads = make_grads(shape, seed=12)
+
+    def step(x, branch, weight, bias):
+        updated, normalized = residual_layer_norm(
+            x, branch, weight, bias, dropout_p=dropout_p, implementation=implementation)
+        return updated, normalized
+
+    compiled = torch.compile(step, backend="aot_eager", fullgraph=True)
+    results = []
+    with deterministic_algorithms():
+        for function in (step, compiled):
+            leaves = [t.detach().clone().requires_grad_(True) for t in inputs]
+            torch.cuda.manual_seed(2024)
+            outputs = function(*leaves)
+            torch.autograd.backward(outputs, grads)
+            torch.cuda.synchronize()
+            results.append([host(t) for t in outputs] + [host(t.grad) for t in leaves])
+    for eager, traced in zip(*results):
+        assert_bitwise(traced, eager, "compiled vs eager")
+
+
+def test_compiled_auto_falls_back_for_non_native_hidden_size():
+    inputs = make_inputs((5, 160), torch.float32, seed=2)
+
+    def step(x, branch, weight, bias):
+        return residual_layer_norm(x, branch, weight, bias, dropout_p=0.0)
+
+    compiled = torch.compile(step, backend="aot_eager", fullgraph=True)
+    expected = torch.nn.functional.layer_norm(inputs[0] + inputs[1], (160,), inputs[2],
+                                              inputs[3], 1e-5)
+    torch.testing.assert_close(compiled(*inputs)[1], expected)
