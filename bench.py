@@ -244,7 +244,8 @@ class Runner:
         status = self.library.rln_forward(
             t["x"].data_ptr(), t["branch"].data_ptr(), self.dtype, self.weight.data_ptr(),
             self.bias.data_ptr(), t["updated"].data_ptr(), t["normalized"].data_ptr(),
-            t["mean"].data_ptr(), t["rstd"].data_ptr(), t["mask"].data_ptr(), w.rows, w.hidden,
+            self.cabi.RLN_DTYPE_F32, t["mean"].data_ptr(), t["rstd"].data_ptr(),
+            t["mask"].data_ptr(), w.rows, w.hidden,
             w.dropout_p, EPS, int(w.training), philox, self.handle)
         if status:
             raise RuntimeError(self.cabi.last_error())
@@ -254,7 +255,7 @@ class Runner:
         workspace = self.workspace
         status = self.library.rln_backward(
             t["grad_updated"].data_ptr(), t["grad_normalized"].data_ptr(),
-            t["updated"].data_ptr(), self.weight.data_ptr(), t["mean"].data_ptr(),
+            self.cabi.RLN_DTYPE_F32, t["updated"].data_ptr(), self.weight.data_ptr(), t["mean"].data_ptr(),
             t["rstd"].data_ptr(), t["mask"].data_ptr(), t["grad_x"].data_ptr(),
             t["grad_branch"].data_ptr(), self.dtype, t["grad_weight"].data_ptr(),
             t["grad_bias"].data_ptr(), w.rows, w.hidden, w.dropout_p, int(w.training),

@@ -92,8 +92,10 @@ static_assert(kBackwardThreads % kWaveSize == 0 && kBackwardThreads <= 1024, "ba
 constexpr int64_t kSupportedHidden[] = {128, 256, 384, 512, 768, 1024};
 
 using half_t = _Float16;
+using bf16_t = __bf16;
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
 // ----------------------------------------------------------------------------
 // Error reporting.
@@ -312,13 +314,27 @@ __device__ __forceinline__ f32x4 load_parameter4(const float* __restrict__ point
     }
 }
 
-template <typename B, bool Aligned>
-__device__ __forceinline__ f32x4 load_branch4(const B* __restrict__ pointer) {
-    if constexpr (sizeof(B) == 4) {
-        return load4<Aligned>(reinterpret_cast<const float*>(pointer));
-    } else if constexpr (Aligned) {
+template <typename T>
+struct Vector4;
+template <>
+struct Vector4<float> {
+    using type = f32x4;
+};
+template <>
+struct Vector4<half_t> {
+    using type = f16x4;
+};
+template <>
+struct Vector4<bf16_t> {
+    using type = bf16x4;
+};
+
+// Four consecutive elements of type T (fp32, fp16 or bf16), widened to fp32.
+template <typename T, bool Aligned>
+__device__ __forceinline__ f32x4 load_convert4(const T* __restrict__ pointer) {
+    if constexpr (Aligned) {
         return __builtin_convertvector(
-            stream_load(reinterpret_cast<const f16x4*>(pointer)), f32x4);
+            stream_load(reinterpret_cast<const typename Vector4<T>::type*>(pointer)), f32x4);
     } else {
         return f32x4{
             static_cast<float>(stream_load(pointer)),
@@ -328,32 +344,51 @@ __device__ __forceinline__ f32x4 load_branch4(const B* __restrict__ pointer) {
     }
 }
 
-template <typename B, bool Aligned>
-__device__ __forceinline__ void store_branch4(B* __restrict__ pointer, f32x4 value) {
-    if constexpr (sizeof(B) == 4) {
-        store4<Aligned>(reinterpret_cast<float*>(pointer), value);
+// Stores four fp32 values as type T; narrowing rounds to nearest even.
+template <typename T, bool Aligned>
+__device__ __forceinline__ void store_convert4(T* __restrict__ pointer, f32x4 value) {
+    const typename Vector4<T>::type packed =
+        __builtin_convertvector(value, typename Vector4<T>::type);
+    if constexpr (Aligned) {
+        stream_store(packed, reinterpret_cast<typename Vector4<T>::type*>(pointer));
     } else {
-        // float -> _Float16 conversions round to nearest even.
-        const f16x4 packed = __builtin_convertvector(value, f16x4);
-        if constexpr (Aligned) {
-            stream_store(packed, reinterpret_cast<f16x4*>(pointer));
-        } else {
-            stream_store(packed.x, pointer);
-            stream_store(packed.y, pointer + 1);
-            stream_store(packed.z, pointer + 2);
-            stream_store(packed.w, pointer + 3);
-        }
+        stream_store(static_cast<T>(packed.x), pointer);
+        stream_store(static_cast<T>(packed.y), pointer + 1);
+        stream_store(static_cast<T>(packed.z), pointer + 2);
+        stream_store(static_cast<T>(packed.w), pointer + 3);
+    }
+}
+
+// The same with the element type chosen at run time (an rln_dtype value,
+// uniform across the launch).
+template <bool Aligned>
+__device__ __forceinline__ f32x4 load_any4(const void* __restrict__ base, int64_t index,
+                                           int dtype) {
+    if (dtype == RLN_DTYPE_F16) {
+        return load_convert4<half_t, Aligned>(static_cast<const half_t*>(base) + index);
+    }
+    if (dtype == RLN_DTYPE_BF16) {
+        return load_convert4<bf16_t, Aligned>(static_cast<const bf16_t*>(base) + index);
+    }
+    return load_convert4<float, Aligned>(static_cast<const float*>(base) + index);
+}
+
+template <bool Aligned>
+__device__ __forceinline__ void store_any4(void* __restrict__ base, int64_t index, f32x4 value,
+                                           int dtype) {
+    if (dtype == RLN_DTYPE_F16) {
+        store_convert4<half_t, Aligned>(static_cast<half_t*>(base) + index, value);
+    } else if (dtype == RLN_DTYPE_BF16) {
+        store_convert4<bf16_t, Aligned>(static_cast<bf16_t*>(base) + index, value);
+    } else {
+        store_convert4<float, Aligned>(static_cast<float*>(base) + index, value);
     }
 }
 
 // Rounds an fp32 value through the branch dtype (identity for fp32).
 template <typename B>
 __device__ __forceinline__ float round_to_branch(float value) {
-    if constexpr (sizeof(B) == 4) {
-        return value;
-    } else {
-        return static_cast<float>(static_cast<half_t>(value));
-    }
+    return static_cast<float>(static_cast<B>(value));
 }
 
 __device__ __forceinline__ f32x4 zero4() {
@@ -382,7 +417,8 @@ void rln_forward_kernel(
     const float* __restrict__ weight,
     const float* __restrict__ bias,
     float* __restrict__ updated,
-    float* __restrict__ normalized,
+    void* __restrict__ normalized,
+    int normalized_dtype,
     float* __restrict__ mean_out,
     float* __restrict__ rstd_out,
     uint32_t* __restrict__ mask,
@@ -437,7 +473,7 @@ void rln_forward_kernel(
             r.branch[v] = zero4();
             if (valid) {
                 r.x[v] = load4<Aligned>(x + base + column);
-                r.branch[v] = load_branch4<B, Aligned>(branch + base + column);
+                r.branch[v] = load_convert4<B, Aligned>(branch + base + column);
             }
         }
     };
@@ -517,7 +553,7 @@ void rln_forward_kernel(
                     __builtin_fmaf(u[v].y * rstd, w[v].y, b[v].y),
                     __builtin_fmaf(u[v].z * rstd, w[v].z, b[v].z),
                     __builtin_fmaf(u[v].w * rstd, w[v].w, b[v].w)};
-                store4<Aligned>(normalized + base + column, y);
+                store_any4<Aligned>(normalized, base + column, y, normalized_dtype);
             }
         }
     };
@@ -569,7 +605,8 @@ template <int H, typename B, bool Aligned>
 __global__ __launch_bounds__(kBackwardThreads)
 void rln_backward_kernel(
     const float* __restrict__ grad_updated,
-    const float* __restrict__ grad_normalized,
+    const void* __restrict__ grad_normalized,
+    int grad_normalized_dtype,
     const float* __restrict__ updated,
     const float* __restrict__ weight,
     const float* __restrict__ mean_in,
@@ -628,7 +665,7 @@ void rln_backward_kernel(
             if (valid) {
                 r.u[v] = load4<Aligned>(updated + base + column);
                 if (has_gy) {
-                    r.gy[v] = load4<Aligned>(grad_normalized + base + column);
+                    r.gy[v] = load_any4<Aligned>(grad_normalized, base + column, grad_normalized_dtype);
                 }
                 if (has_gu) {
                     r.gu[v] = load4<Aligned>(grad_updated + base + column);
@@ -681,7 +718,7 @@ void rln_backward_kernel(
                     g.z = g.z * (static_cast<float>((bits >> 2) & 1u) * scale);
                     g.w = g.w * (static_cast<float>((bits >> 3) & 1u) * scale);
                 }
-                store_branch4<B, Aligned>(grad_branch + base + column, g);
+                store_convert4<B, Aligned>(grad_branch + base + column, g);
             }
         }
 
@@ -818,7 +855,8 @@ struct ForwardArgs {
     const float* weight;
     const float* bias;
     float* updated;
-    float* normalized;
+    void* normalized;
+    int normalized_dtype;
     float* mean;
     float* rstd;
     uint32_t* mask;
@@ -841,6 +879,7 @@ int launch_forward(const ForwardArgs& a) {
         a.bias,
         a.updated,
         a.normalized,
+        a.normalized_dtype,
         a.mean,
         a.rstd,
         a.mask,
@@ -853,17 +892,26 @@ int launch_forward(const ForwardArgs& a) {
     return check_launch("rln_forward_kernel");
 }
 
+template <int H, typename B>
+int launch_forward_branch(const ForwardArgs& a, bool aligned) {
+    return aligned ? launch_forward<H, B, true>(a) : launch_forward<H, B, false>(a);
+}
+
 template <int H>
-int launch_forward_hidden(const ForwardArgs& a, bool half_branch, bool aligned) {
-    if (half_branch) {
-        return aligned ? launch_forward<H, half_t, true>(a) : launch_forward<H, half_t, false>(a);
+int launch_forward_hidden(const ForwardArgs& a, int branch_dtype, bool aligned) {
+    if (branch_dtype == RLN_DTYPE_F16) {
+        return launch_forward_branch<H, half_t>(a, aligned);
     }
-    return aligned ? launch_forward<H, float, true>(a) : launch_forward<H, float, false>(a);
+    if (branch_dtype == RLN_DTYPE_BF16) {
+        return launch_forward_branch<H, bf16_t>(a, aligned);
+    }
+    return launch_forward_branch<H, float>(a, aligned);
 }
 
 struct BackwardArgs {
     const float* grad_updated;
-    const float* grad_normalized;
+    const void* grad_normalized;
+    int grad_normalized_dtype;
     const float* updated;
     const float* weight;
     const float* mean;
@@ -886,6 +934,7 @@ int launch_backward(const BackwardArgs& a) {
     rln_backward_kernel<H, B, Aligned><<<grid, kBackwardThreads, 0, a.stream>>>(
         a.grad_updated,
         a.grad_normalized,
+        a.grad_normalized_dtype,
         a.updated,
         a.weight,
         a.mean,
@@ -902,12 +951,20 @@ int launch_backward(const BackwardArgs& a) {
     return check_launch("rln_backward_kernel");
 }
 
+template <int H, typename B>
+int launch_backward_branch(const BackwardArgs& a, bool aligned) {
+    return aligned ? launch_backward<H, B, true>(a) : launch_backward<H, B, false>(a);
+}
+
 template <int H>
-int launch_backward_hidden(const BackwardArgs& a, bool half_branch, bool aligned) {
-    if (half_branch) {
-        return aligned ? launch_backward<H, half_t, true>(a) : launch_backward<H, half_t, false>(a);
+int launch_backward_hidden(const BackwardArgs& a, int branch_dtype, bool aligned) {
+    if (branch_dtype == RLN_DTYPE_F16) {
+        return launch_backward_branch<H, half_t>(a, aligned);
     }
-    return aligned ? launch_backward<H, float, true>(a) : launch_backward<H, float, false>(a);
+    if (branch_dtype == RLN_DTYPE_BF16) {
+        return launch_backward_branch<H, bf16_t>(a, aligned);
+    }
+    return launch_backward_branch<H, float>(a, aligned);
 }
 
 bool aligned_to(const void* pointer, uintptr_t alignment) {
@@ -938,6 +995,15 @@ int dropout_constants(double dropout_p, int training, DropoutConstants* out) {
     return RLN_OK;
 }
 
+bool valid_dtype(int dtype) {
+    return dtype == RLN_DTYPE_F32 || dtype == RLN_DTYPE_F16 || dtype == RLN_DTYPE_BF16;
+}
+
+// Alignment of one four-element vector of `dtype`.
+uintptr_t vector_alignment(int dtype) {
+    return dtype == RLN_DTYPE_F32 ? 16 : 8;
+}
+
 int check_common(int64_t rows, int64_t hidden, int branch_dtype) {
     if (rows <= 0) {
         return fail(RLN_ERR_INVALID, "empty tensors are unsupported");
@@ -948,8 +1014,8 @@ int check_common(int64_t rows, int64_t hidden, int branch_dtype) {
             "unsupported native hidden size: %lld",
             static_cast<long long>(hidden));
     }
-    if (branch_dtype != RLN_DTYPE_F32 && branch_dtype != RLN_DTYPE_F16) {
-        return fail(RLN_ERR_INVALID, "branch must use float16 or float32");
+    if (!valid_dtype(branch_dtype)) {
+        return fail(RLN_ERR_INVALID, "branch must use float16, bfloat16 or float32");
     }
     if (rows > (INT64_MAX / hidden)) {
         return fail(RLN_ERR_INVALID, "rows * hidden overflows int64");
@@ -977,7 +1043,8 @@ int rln_forward(
     const float* weight,
     const float* bias,
     float* updated,
-    float* normalized,
+    void* normalized,
+    int normalized_dtype,
     float* mean,
     float* rstd,
     uint32_t* dropout_mask,
@@ -992,6 +1059,9 @@ int rln_forward(
     int status = check_common(rows, hidden, branch_dtype);
     if (status != RLN_OK) {
         return status;
+    }
+    if (!valid_dtype(normalized_dtype)) {
+        return fail(RLN_ERR_INVALID, "normalized must use float16, bfloat16 or float32");
     }
     if (!x || !branch || !weight || !bias || !updated || !normalized || !mean || !rstd) {
         return fail(RLN_ERR_INVALID, "forward tensors must not be null");
@@ -1011,6 +1081,7 @@ int rln_forward(
     a.bias = bias;
     a.updated = updated;
     a.normalized = normalized;
+    a.normalized_dtype = normalized_dtype;
     a.mean = mean;
     a.rstd = rstd;
     a.mask = dropout_mask;
@@ -1032,17 +1103,17 @@ int rln_forward(
         a.philox.seed_ptr = philox->seed_ptr;
         a.philox.offset_ptr = philox->offset_ptr;
     }
-    const bool half_branch = branch_dtype == RLN_DTYPE_F16;
     const bool aligned = aligned_to(x, 16) && aligned_to(weight, 16) && aligned_to(bias, 16)
-        && aligned_to(updated, 16) && aligned_to(normalized, 16)
-        && aligned_to(branch, half_branch ? 8 : 16);
+        && aligned_to(updated, 16)
+        && aligned_to(normalized, vector_alignment(normalized_dtype))
+        && aligned_to(branch, vector_alignment(branch_dtype));
     switch (hidden) {
-        case 128: return launch_forward_hidden<128>(a, half_branch, aligned);
-        case 256: return launch_forward_hidden<256>(a, half_branch, aligned);
-        case 384: return launch_forward_hidden<384>(a, half_branch, aligned);
-        case 512: return launch_forward_hidden<512>(a, half_branch, aligned);
-        case 768: return launch_forward_hidden<768>(a, half_branch, aligned);
-        case 1024: return launch_forward_hidden<1024>(a, half_branch, aligned);
+        case 128: return launch_forward_hidden<128>(a, branch_dtype, aligned);
+        case 256: return launch_forward_hidden<256>(a, branch_dtype, aligned);
+        case 384: return launch_forward_hidden<384>(a, branch_dtype, aligned);
+        case 512: return launch_forward_hidden<512>(a, branch_dtype, aligned);
+        case 768: return launch_forward_hidden<768>(a, branch_dtype, aligned);
+        case 1024: return launch_forward_hidden<1024>(a, branch_dtype, aligned);
         default: break;
     }
     return fail(RLN_ERR_UNSUPPORTED, "unsupported native hidden size: %lld", static_cast<long long>(hidden));
@@ -1058,7 +1129,8 @@ size_t rln_backward_workspace_bytes(int64_t rows, int64_t hidden, int determinis
 
 int rln_backward(
     const float* grad_updated,
-    const float* grad_normalized,
+    const void* grad_normalized,
+    int grad_normalized_dtype,
     const float* updated,
     const float* weight,
     const float* mean,
@@ -1085,6 +1157,9 @@ int rln_backward(
     }
     if (!updated || !weight || !mean || !rstd || !grad_x || !grad_branch) {
         return fail(RLN_ERR_INVALID, "backward tensors must not be null");
+    }
+    if (!valid_dtype(grad_normalized_dtype)) {
+        return fail(RLN_ERR_INVALID, "grad_normalized must use float16, bfloat16 or float32");
     }
     if ((grad_weight == nullptr) != (grad_bias == nullptr)) {
         return fail(RLN_ERR_INVALID, "grad_weight and grad_bias must both be given or both be null");
@@ -1116,6 +1191,7 @@ int rln_backward(
     BackwardArgs a{};
     a.grad_updated = grad_updated;
     a.grad_normalized = grad_normalized;
+    a.grad_normalized_dtype = grad_normalized_dtype;
     a.updated = updated;
     a.weight = weight;
     a.mean = mean;
@@ -1144,17 +1220,17 @@ int rln_backward(
         }
     }
 
-    const bool half_branch = branch_dtype == RLN_DTYPE_F16;
-    const bool aligned = aligned_to(grad_updated, 16) && aligned_to(grad_normalized, 16)
+    const bool aligned = aligned_to(grad_updated, 16)
+        && aligned_to(grad_normalized, vector_alignment(grad_normalized_dtype))
         && aligned_to(updated, 16) && aligned_to(weight, 16) && aligned_to(grad_x, 16)
-        && aligned_to(grad_branch, half_branch ? 8 : 16);
+        && aligned_to(grad_branch, vector_alignment(branch_dtype));
     switch (hidden) {
-        case 128: status = launch_backward_hidden<128>(a, half_branch, aligned); break;
-        case 256: status = launch_backward_hidden<256>(a, half_branch, aligned); break;
-        case 384: status = launch_backward_hidden<384>(a, half_branch, aligned); break;
-        case 512: status = launch_backward_hidden<512>(a, half_branch, aligned); break;
-        case 768: status = launch_backward_hidden<768>(a, half_branch, aligned); break;
-        case 1024: status = launch_backward_hidden<1024>(a, half_branch, aligned); break;
+        case 128: status = launch_backward_hidden<128>(a, branch_dtype, aligned); break;
+        case 256: status = launch_backward_hidden<256>(a, branch_dtype, aligned); break;
+        case 384: status = launch_backward_hidden<384>(a, branch_dtype, aligned); break;
+        case 512: status = launch_backward_hidden<512>(a, branch_dtype, aligned); break;
+        case 768: status = launch_backward_hidden<768>(a, branch_dtype, aligned); break;
+        case 1024: status = launch_backward_hidden<1024>(a, branch_dtype, aligned); break;
         default:
             return fail(RLN_ERR_UNSUPPORTED, "unsupported native hidden size: %lld", static_cast<long long>(hidden));
     }

@@ -7,7 +7,10 @@
 //   residual_layer_norm_backward(...)  [grad_x, grad_branch, grad_w, grad_b]
 // Argument order, return layout and error messages follow
 // csrc/residual_layer_norm.h:10-42 and the input checks at
-// csrc/residual_layer_norm_kernel.hip:26-166. The reference's launch hints
+// csrc/residual_layer_norm_kernel.hip:26-166. Two optional trailing keyword
+// arguments extend them: `normalized_dtype` (forward; float32, float16 or
+// bfloat16 normalized output) and `branch_dtype` (backward; names a bfloat16
+// branch, which the reference's `branch_is_half` flag cannot express). The reference's launch hints
 // (threads, block_rows, parameter_threads, parameter_groups) are validated
 // with the reference's messages and otherwise ignored: the MI355X library
 // picks its own launch shape.
@@ -39,6 +42,10 @@ bool native_hidden(int64_t hidden) {
     return rln_hidden_supported(hidden) != 0;
 }
 
+bool supported_dtype(at::ScalarType type) {
+    return type == at::kFloat || type == at::kHalf || type == at::kBFloat16;
+}
+
 void check_status(int status) {
     TORCH_CHECK(status == RLN_OK, rln_last_error());
 }
@@ -61,8 +68,9 @@ void check_forward_inputs(
         "all tensors must be on the same HIP device");
     TORCH_CHECK(x.scalar_type() == at::kFloat, "x must use float32");
     TORCH_CHECK(
-        branch.scalar_type() == at::kHalf || branch.scalar_type() == at::kFloat,
-        "branch must use float16 or float32");
+        branch.scalar_type() == at::kHalf || branch.scalar_type() == at::kBFloat16
+            || branch.scalar_type() == at::kFloat,
+        "branch must use float16, bfloat16 or float32");
     TORCH_CHECK(
         weight.scalar_type() == at::kFloat && bias.scalar_type() == at::kFloat,
         "weight and bias must use float32");
@@ -106,10 +114,12 @@ void check_backward_inputs(
         && weight.device() == device && mean.device() == device && rstd.device() == device;
     TORCH_CHECK(same_device, "all backward tensors must be on the same HIP device");
     const bool float32 = (!grad_updated || grad_updated->scalar_type() == at::kFloat)
-        && (!grad_normalized || grad_normalized->scalar_type() == at::kFloat)
         && updated.scalar_type() == at::kFloat && weight.scalar_type() == at::kFloat
         && mean.scalar_type() == at::kFloat && rstd.scalar_type() == at::kFloat;
     TORCH_CHECK(float32, "all backward tensors must use float32");
+    TORCH_CHECK(
+        !grad_normalized || supported_dtype(grad_normalized->scalar_type()),
+        "grad_normalized must use float32, float16 or bfloat16");
     TORCH_CHECK(updated.dim() >= 2, "updated must have at least two dimensions");
     TORCH_CHECK(updated.numel() > 0, "empty tensors are unsupported");
     TORCH_CHECK(
@@ -180,8 +190,14 @@ rln_philox_t reserve_philox(const at::Tensor& x, int64_t hidden) {
     return philox;
 }
 
-int branch_dtype_of(at::ScalarType type) {
-    return type == at::kHalf ? RLN_DTYPE_F16 : RLN_DTYPE_F32;
+int dtype_of(at::ScalarType type) {
+    if (type == at::kHalf) {
+        return RLN_DTYPE_F16;
+    }
+    if (type == at::kBFloat16) {
+        return RLN_DTYPE_BF16;
+    }
+    return RLN_DTYPE_F32;
 }
 
 std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> forward_impl(
@@ -192,14 +208,18 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> forward_i
     double dropout_p,
     double eps,
     bool training,
-    int64_t threads) {
+    int64_t threads,
+    std::optional<at::ScalarType> normalized_dtype) {
     check_forward_inputs(x, branch, weight, bias, dropout_p, eps, threads);
+    const at::ScalarType output_type = normalized_dtype.value_or(at::kFloat);
+    TORCH_CHECK(supported_dtype(output_type),
+                "normalized_dtype must be float32, float16 or bfloat16");
     c10::hip::HIPGuardMasqueradingAsCUDA guard(x.device());
     const int64_t hidden = x.size(-1);
     const int64_t rows = x.numel() / hidden;
     const bool dropout = training && dropout_p > 0.0;
     auto updated = at::empty_like(x);
-    auto normalized = at::empty_like(x);
+    auto normalized = at::empty_like(x, x.options().dtype(output_type));
     auto mean = at::empty({rows}, x.options());
     auto rstd = at::empty({rows}, x.options());
     auto mask = at::empty({dropout ? rln_mask_words(rows, hidden) : 0}, x.options().dtype(at::kInt));
@@ -211,11 +231,12 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> forward_i
     check_status(rln_forward(
         x.data_ptr<float>(),
         branch.data_ptr(),
-        branch_dtype_of(branch.scalar_type()),
+        dtype_of(branch.scalar_type()),
         weight.data_ptr<float>(),
         bias.data_ptr<float>(),
         updated.data_ptr<float>(),
-        normalized.data_ptr<float>(),
+        normalized.data_ptr(),
+        dtype_of(output_type),
         mean.data_ptr<float>(),
         rstd.data_ptr<float>(),
         dropout ? reinterpret_cast<uint32_t*>(mask.data_ptr<int32_t>()) : nullptr,
@@ -244,7 +265,8 @@ std::vector<at::Tensor> backward_impl(
     int64_t block_rows,
     int64_t parameter_threads,
     int64_t parameter_groups,
-    bool compute_parameter_gradients) {
+    bool compute_parameter_gradients,
+    std::optional<at::ScalarType> branch_dtype) {
     // Undefined tensors arrive from autograd as nullopt-equivalents.
     std::optional<at::Tensor> grad_updated;
     std::optional<at::Tensor> grad_normalized;
@@ -273,10 +295,13 @@ std::vector<at::Tensor> backward_impl(
     const int64_t rows = updated.numel() / hidden;
     const bool dropout = training && dropout_p > 0.0;
     const bool deterministic = at::globalContext().deterministicAlgorithms();
+    // The reference passes only `branch_is_half`; `branch_dtype`, when given,
+    // names the branch type exactly (bfloat16 included).
+    const at::ScalarType branch_type =
+        branch_dtype.value_or(branch_is_half ? at::kHalf : at::kFloat);
+    TORCH_CHECK(supported_dtype(branch_type), "branch_dtype must be float32, float16 or bfloat16");
     auto grad_x = at::empty_like(updated);
-    auto grad_branch = at::empty(
-        updated.sizes(),
-        updated.options().dtype(branch_is_half ? at::kHalf : at::kFloat));
+    auto grad_branch = at::empty(updated.sizes(), updated.options().dtype(branch_type));
     at::Tensor grad_weight;
     at::Tensor grad_bias;
     at::Tensor workspace;
@@ -301,7 +326,8 @@ std::vector<at::Tensor> backward_impl(
     const auto stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(updated.device().index()).stream();
     check_status(rln_backward(
         grad_updated ? grad_updated->data_ptr<float>() : nullptr,
-        grad_normalized ? grad_normalized->data_ptr<float>() : nullptr,
+        grad_normalized ? grad_normalized->data_ptr() : nullptr,
+        grad_normalized ? dtype_of(grad_normalized->scalar_type()) : RLN_DTYPE_F32,
         updated.data_ptr<float>(),
         weight.data_ptr<float>(),
         mean.data_ptr<float>(),
@@ -309,7 +335,7 @@ std::vector<at::Tensor> backward_impl(
         dropout ? reinterpret_cast<const uint32_t*>(dropout_mask.data_ptr<int32_t>()) : nullptr,
         grad_x.data_ptr<float>(),
         grad_branch.data_ptr(),
-        branch_is_half ? RLN_DTYPE_F16 : RLN_DTYPE_F32,
+        dtype_of(branch_type),
         launch_parameters ? grad_weight.data_ptr<float>() : nullptr,
         launch_parameters ? grad_bias.data_ptr<float>() : nullptr,
         rows,
@@ -343,8 +369,10 @@ class ResidualLayerNormFunction : public torch::autograd::Function<ResidualLayer
         int64_t threads,
         int64_t block_rows,
         int64_t parameter_threads,
-        int64_t parameter_groups) {
-        auto result = forward_impl(x, branch, weight, bias, dropout_p, eps, training, threads);
+        int64_t parameter_groups,
+        std::optional<at::ScalarType> normalized_dtype) {
+        auto result = forward_impl(
+            x, branch, weight, bias, dropout_p, eps, training, threads, normalized_dtype);
         auto updated = std::get<0>(result);
         auto normalized = std::get<1>(result);
         ctx->save_for_backward(
@@ -353,6 +381,7 @@ class ResidualLayerNormFunction : public torch::autograd::Function<ResidualLayer
         ctx->saved_data["dropout_p"] = dropout_p;
         ctx->saved_data["training"] = training;
         ctx->saved_data["branch_is_half"] = branch.scalar_type() == at::kHalf;
+        ctx->saved_data["branch_dtype"] = static_cast<int64_t>(branch.scalar_type());
         ctx->saved_data["threads"] = threads;
         ctx->saved_data["block_rows"] = block_rows;
         ctx->saved_data["parameter_threads"] = parameter_threads;
@@ -376,7 +405,7 @@ class ResidualLayerNormFunction : public torch::autograd::Function<ResidualLayer
         if (!grad_updated && !has_grad_normalized) {
             return {
                 at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor(),
-                at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor()};
+                at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor()};
         }
         auto gradients = backward_impl(
             grad_updated,
@@ -393,12 +422,14 @@ class ResidualLayerNormFunction : public torch::autograd::Function<ResidualLayer
             ctx->saved_data["block_rows"].toInt(),
             ctx->saved_data["parameter_threads"].toInt(),
             ctx->saved_data["parameter_groups"].toInt(),
-            has_grad_normalized);
+            has_grad_normalized,
+            static_cast<at::ScalarType>(ctx->saved_data["branch_dtype"].toInt()));
         return {
             gradients[0],
             gradients[1],
             has_grad_normalized ? gradients[2] : at::Tensor(),
             has_grad_normalized ? gradients[3] : at::Tensor(),
+            at::Tensor(),
             at::Tensor(),
             at::Tensor(),
             at::Tensor(),
@@ -421,7 +452,8 @@ torch::autograd::variable_list residual_layer_norm_autograd(
     int64_t threads,
     int64_t block_rows,
     int64_t parameter_threads,
-    int64_t parameter_groups) {
+    int64_t parameter_groups,
+    std::optional<at::ScalarType> normalized_dtype) {
     return ResidualLayerNormFunction::apply(
         x,
         branch,
@@ -433,15 +465,41 @@ torch::autograd::variable_list residual_layer_norm_autograd(
         threads,
         block_rows,
         parameter_threads,
-        parameter_groups);
+        parameter_groups,
+        normalized_dtype);
 }
 
 }  // namespace
 
 PYBIND11_MODULE(_C, module) {
     module.doc() = "MI355X (gfx950) fused residual + dropout + LayerNorm";
-    module.def("residual_layer_norm", &residual_layer_norm_autograd);
-    module.def("residual_layer_norm_forward", &forward_impl);
+    module.def(
+        "residual_layer_norm",
+        &residual_layer_norm_autograd,
+        pybind11::arg("x"),
+        pybind11::arg("branch"),
+        pybind11::arg("weight"),
+        pybind11::arg("bias"),
+        pybind11::arg("dropout_p"),
+        pybind11::arg("eps"),
+        pybind11::arg("training"),
+        pybind11::arg("threads"),
+        pybind11::arg("block_rows"),
+        pybind11::arg("parameter_threads"),
+        pybind11::arg("parameter_groups"),
+        pybind11::arg("normalized_dtype") = pybind11::none());
+    module.def(
+        "residual_layer_norm_forward",
+        &forward_impl,
+        pybind11::arg("x"),
+        pybind11::arg("branch"),
+        pybind11::arg("weight"),
+        pybind11::arg("bias"),
+        pybind11::arg("dropout_p"),
+        pybind11::arg("eps"),
+        pybind11::arg("training"),
+        pybind11::arg("threads"),
+        pybind11::arg("normalized_dtype") = pybind11::none());
     module.def(
         "residual_layer_norm_backward",
         &backward_impl,
@@ -459,7 +517,8 @@ PYBIND11_MODULE(_C, module) {
         pybind11::arg("block_rows"),
         pybind11::arg("parameter_threads"),
         pybind11::arg("parameter_groups"),
-        pybind11::arg("compute_parameter_gradients"));
+        pybind11::arg("compute_parameter_gradients"),
+        pybind11::arg("branch_dtype") = pybind11::none());
     module.def("target_arch", []() { return std::string(rln_target_arch()); });
     module.def("library_version", []() { return std::string(rln_version()); });
 }

@@ -20,6 +20,7 @@ LIBRARY_PATH = Path(__file__).resolve().parent / "librln_gfx950.so"
 
 RLN_DTYPE_F32 = 0
 RLN_DTYPE_F16 = 1
+RLN_DTYPE_BF16 = 2
 
 RLN_OK = 0
 RLN_ERR_INVALID = 1
@@ -51,12 +52,12 @@ _I64 = ctypes.c_int64
 SIGNATURES = {
     "rln_forward": (
         ctypes.c_int,
-        [_P, _P, ctypes.c_int, _P, _P, _P, _P, _P, _P, _P, _I64, _I64,
+        [_P, _P, ctypes.c_int, _P, _P, _P, _P, ctypes.c_int, _P, _P, _P, _I64, _I64,
          ctypes.c_double, ctypes.c_double, ctypes.c_int, ctypes.POINTER(RlnPhilox), _P],
     ),
     "rln_backward": (
         ctypes.c_int,
-        [_P, _P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_int, _P, _P, _I64, _I64,
+        [_P, _P, ctypes.c_int, _P, _P, _P, _P, _P, _P, _P, ctypes.c_int, _P, _P, _I64, _I64,
          ctypes.c_double, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P, ctypes.c_size_t, _P],
     ),
     "rln_backward_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, ctypes.c_int]),
@@ -105,13 +106,15 @@ def supported_hidden_sizes() -> tuple[int, ...]:
 def forward(
     x, branch, branch_dtype, weight, bias, updated, normalized, mean, rstd, mask,
     rows, hidden, dropout_p, eps, training, philox=None, stream=None,
+    normalized_dtype=RLN_DTYPE_F32,
 ):
     """Call ``rln_forward`` with integer device addresses; raises RlnError."""
     pointer = ctypes.byref(philox) if philox is not None else None
     _check(
         library().rln_forward(
-            x, branch, branch_dtype, weight, bias, updated, normalized, mean, rstd,
-            mask, rows, hidden, dropout_p, eps, int(bool(training)), pointer, stream,
+            x, branch, branch_dtype, weight, bias, updated, normalized, normalized_dtype,
+            mean, rstd, mask, rows, hidden, dropout_p, eps, int(bool(training)), pointer,
+            stream,
         )
     )
 
@@ -120,15 +123,15 @@ def backward(
     grad_updated, grad_normalized, updated, weight, mean, rstd, mask, grad_x,
     grad_branch, branch_dtype, grad_weight, grad_bias, rows, hidden, dropout_p,
     training, deterministic, workspace=None, workspace_bytes=0, stream=None,
-    accumulate_parameters=False,
+    accumulate_parameters=False, grad_normalized_dtype=RLN_DTYPE_F32,
 ):
     """Call ``rln_backward`` with integer device addresses; raises RlnError."""
     _check(
         library().rln_backward(
-            grad_updated, grad_normalized, updated, weight, mean, rstd, mask, grad_x,
-            grad_branch, branch_dtype, grad_weight, grad_bias, rows, hidden, dropout_p,
-            int(bool(training)), int(bool(deterministic)), int(bool(accumulate_parameters)),
-            workspace, workspace_bytes, stream,
+            grad_updated, grad_normalized, grad_normalized_dtype, updated, weight, mean,
+            rstd, mask, grad_x, grad_branch, branch_dtype, grad_weight, grad_bias, rows,
+            hidden, dropout_p, int(bool(training)), int(bool(deterministic)),
+            int(bool(accumulate_parameters)), workspace, workspace_bytes, stream,
         )
     )
 

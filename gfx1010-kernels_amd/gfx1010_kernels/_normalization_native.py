@@ -46,6 +46,7 @@ def native_residual_layer_norm(
     dropout_p,
     eps,
     training,
+    normalized_dtype=None,
 ):
     extension, reason = _extension()
     if extension is None:
@@ -62,6 +63,7 @@ def native_residual_layer_norm(
             float(eps),
             bool(training),
             *_LAUNCH_HINTS,
+            normalized_dtype=normalized_dtype,
         )
     )
 

@@ -8,14 +8,14 @@ shape inference and an autograd formula, so that a compiled graph keeps the
 fused op instead of breaking around it (the reference does not support
 ``torch.compile``; docs/residual_layer_norm.md:301-302).
 
-* ``gfx1010_kernels::rln_forward(x, branch, weight, bias, dropout_p, eps, training)
-  -> (updated, normalized, mean, rstd, mask)`` runs
+* ``gfx1010_kernels::rln_forward(x, branch, weight, bias, dropout_p, eps, training,
+  normalized_dtype) -> (updated, normalized, mean, rstd, mask)`` runs
   ``_C.residual_layer_norm_forward``; with dropout it reserves its Philox
   offsets from the device's default generator when it executes, exactly as
   the eager path does, so compiled and eager runs draw the same masks from the
   same RNG state.
 * ``gfx1010_kernels::rln_backward(grad_updated, grad_normalized, updated, weight,
-  mean, rstd, mask, dropout_p, training, branch_is_half)
+  mean, rstd, mask, dropout_p, training, branch_dtype)
   -> (grad_x, grad_branch, grad_weight, grad_bias)`` runs
   ``_C.residual_layer_norm_backward``; a missing upstream gradient counts as
   zero, and the weight/bias gradients are zero when ``grad_normalized`` is.
@@ -54,22 +54,25 @@ def rln_forward(
     dropout_p: float,
     eps: float,
     training: bool,
+    normalized_dtype: Optional[torch.dtype] = None,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     return tuple(
         _native().residual_layer_norm_forward(
-            x, branch, weight, bias, float(dropout_p), float(eps), bool(training), _THREADS
+            x, branch, weight, bias, float(dropout_p), float(eps), bool(training), _THREADS,
+            normalized_dtype=normalized_dtype,
         )
     )
 
 
 @rln_forward.register_fake
-def _rln_forward_fake(x, branch, weight, bias, dropout_p, eps, training):
+def _rln_forward_fake(x, branch, weight, bias, dropout_p, eps, training, normalized_dtype=None):
     hidden = x.shape[-1]
     rows = x.numel() // hidden
     mask_words = rows * (hidden // 32) if (training and dropout_p > 0.0) else 0
     return (
         torch.empty_like(x, memory_format=torch.contiguous_format),
-        torch.empty_like(x, memory_format=torch.contiguous_format),
+        torch.empty_like(x, dtype=normalized_dtype or torch.float32,
+                         memory_format=torch.contiguous_format),
         x.new_empty((rows,)),
         x.new_empty((rows,)),
         x.new_empty((mask_words,), dtype=torch.int32),
@@ -87,20 +90,20 @@ def rln_backward(
     mask: Tensor,
     dropout_p: float,
     training: bool,
-    branch_is_half: bool,
+    branch_dtype: torch.dtype,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     grad_x, grad_branch, grad_weight, grad_bias = _native().residual_layer_norm_backward(
         grad_updated, grad_normalized, updated, weight, mean, rstd, mask, float(dropout_p),
-        bool(training), bool(branch_is_half), *_BACKWARD_HINTS, True,
+        bool(training), branch_dtype == torch.float16, *_BACKWARD_HINTS, True,
+        branch_dtype=branch_dtype,
     )
     return grad_x, grad_branch, grad_weight, grad_bias
 
 
 @rln_backward.register_fake
 def _rln_backward_fake(grad_updated, grad_normalized, updated, weight, mean, rstd, mask,
-                       dropout_p, training, branch_is_half):
+                       dropout_p, training, branch_dtype):
     hidden = updated.shape[-1]
-    branch_dtype = torch.float16 if branch_is_half else torch.float32
     return (
         torch.empty_like(updated, memory_format=torch.contiguous_format),
         torch.empty_like(updated, dtype=branch_dtype, memory_format=torch.contiguous_format),
@@ -110,19 +113,19 @@ def _rln_backward_fake(grad_updated, grad_normalized, updated, weight, mean, rst
 
 
 def _setup_context(ctx, inputs, output):
-    _, branch, weight, _, dropout_p, _, training = inputs
+    _, branch, weight, _, dropout_p, _, training, _ = inputs
     updated, _, mean, rstd, mask = output
     ctx.save_for_backward(updated, weight, mean, rstd, mask)
     ctx.dropout_p = dropout_p
     ctx.training = training
-    ctx.branch_is_half = branch.dtype == torch.float16
+    ctx.branch_dtype = branch.dtype
     ctx.mark_non_differentiable(mean, rstd, mask)
     ctx.set_materialize_grads(False)
 
 
 def _backward(ctx, grad_updated, grad_normalized, _grad_mean, _grad_rstd, _grad_mask):
     if grad_updated is None and grad_normalized is None:
-        return None, None, None, None, None, None, None
+        return None, None, None, None, None, None, None, None
     updated, weight, mean, rstd, mask = ctx.saved_tensors
     if grad_updated is not None:
         grad_updated = grad_updated.contiguous()
@@ -130,20 +133,21 @@ def _backward(ctx, grad_updated, grad_normalized, _grad_mean, _grad_rstd, _grad_
         grad_normalized = grad_normalized.contiguous()
     grad_x, grad_branch, grad_weight, grad_bias = rln_backward(
         grad_updated, grad_normalized, updated, weight, mean, rstd, mask, ctx.dropout_p,
-        ctx.training, ctx.branch_is_half,
+        ctx.training, ctx.branch_dtype,
     )
     if grad_normalized is None:
         grad_weight = grad_bias = None
-    return grad_x, grad_branch, grad_weight, grad_bias, None, None, None
+    return grad_x, grad_branch, grad_weight, grad_bias, None, None, None, None
 
 
 rln_forward.register_autograd(_backward, setup_context=_setup_context)
 
 
-def residual_layer_norm_op(x, branch, weight, bias, dropout_p, eps, training):
+def residual_layer_norm_op(x, branch, weight, bias, dropout_p, eps, training,
+                           normalized_dtype=None):
     """``(updated, normalized)`` through the registered custom op."""
     updated, normalized, _, _, _ = rln_forward(
-        x, branch, weight, bias, float(dropout_p), float(eps), bool(training)
+        x, branch, weight, bias, float(dropout_p), float(eps), bool(training), normalized_dtype
     )
     return updated, normalized
 

@@ -40,15 +40,21 @@ MIN_HIDDEN_SIZE = 128
 MAX_HIDDEN_SIZE = 1024
 
 IMPLEMENTATIONS = ("auto", TARGET_ARCHITECTURE, "gfx1010", "triton", "torch")
+BRANCH_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
+NORMALIZED_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
 _STRICT_NATIVE = frozenset({TARGET_ARCHITECTURE, "gfx1010"})
 _UNAVAILABLE = f"{TARGET_ARCHITECTURE} native residual LayerNorm is unavailable"
 
 
-def _torch_residual_layer_norm(x, branch, weight, bias, dropout_p, eps, training):
-    """PyTorch decomposition (reference normalization.py:15-33)."""
+def _torch_residual_layer_norm(x, branch, weight, bias, dropout_p, eps, training,
+                               normalized_dtype=None):
+    """PyTorch decomposition (reference normalization.py:15-33); a requested
+    ``normalized_dtype`` casts the LayerNorm output."""
     dropped = F.dropout(branch, dropout_p, training) if training else branch
     updated = x + dropped
     normalized = F.layer_norm(updated, (updated.shape[-1],), weight, bias, eps)
+    if normalized_dtype is not None:
+        normalized = normalized.to(normalized_dtype)
     return updated, normalized
 
 
@@ -127,8 +133,8 @@ def _input_reason(x, branch, weight, bias, dropout_p, eps):
         return "weight and bias must match the final tensor dimension"
     if x.dtype != torch.float32:
         return "the optimized residual stream requires float32 x"
-    if branch.dtype not in (torch.float16, torch.float32):
-        return "branch must use float16 or float32"
+    if branch.dtype not in BRANCH_DTYPES:
+        return "branch must use float16, bfloat16 or float32"
     if weight.dtype != torch.float32 or bias.dtype != torch.float32:
         return "weight and bias must use float32"
     if not all(tensor.is_contiguous() for tensor in (x, branch, weight, bias)):
@@ -150,7 +156,7 @@ def can_use_residual_layer_norm(x, branch, weight, bias, dropout_p=0.0, eps=1e-5
     return residual_layer_norm_status(x.device).available
 
 
-def _strict_native(x, branch, weight, bias, dropout_p, eps, training):
+def _strict_native(x, branch, weight, bias, dropout_p, eps, training, normalized_dtype):
     if not x.is_cuda:
         raise RuntimeError(f"{_UNAVAILABLE}: x must be a HIP tensor")
     if x.ndim == 0:
@@ -165,25 +171,29 @@ def _strict_native(x, branch, weight, bias, dropout_p, eps, training):
     from ._normalization_native import native_residual_layer_norm
 
     return native_residual_layer_norm(
-        x, branch, weight, bias, float(dropout_p), float(eps), bool(training)
+        x, branch, weight, bias, float(dropout_p), float(eps), bool(training),
+        normalized_dtype=normalized_dtype,
     )
 
 
-def _fall_back(reason, x, branch, weight, bias, dropout_p, eps, training):
+def _fall_back(reason, x, branch, weight, bias, dropout_p, eps, training, normalized_dtype):
     warnings.warn(
         f"{TARGET_ARCHITECTURE} native residual LayerNorm was not used: {reason}",
         RuntimeWarning,
         stacklevel=3,
     )
-    return _torch_residual_layer_norm(x, branch, weight, bias, dropout_p, eps, training)
+    return _torch_residual_layer_norm(
+        x, branch, weight, bias, dropout_p, eps, training, normalized_dtype)
 
 
-def _traced(x, branch, weight, bias, dropout_p, eps, training, implementation):
+def _traced(x, branch, weight, bias, dropout_p, eps, training, normalized_dtype,
+            implementation):
     """Dispatch while ``torch.compile`` traces: the native kernels run through
     the registered custom op (``gfx1010_kernels::rln_forward``) so the graph
     keeps them; the backend status is not queried (the op raises at run time
     if the extension is missing) and ``auto`` falls back without a warning."""
     native = x.is_cuda and x.ndim >= 2 and x.shape[-1] in NATIVE_HIDDEN_SIZES
+    args = (x, branch, weight, bias, dropout_p, eps, training, normalized_dtype)
     if implementation in _STRICT_NATIVE:
         if not x.is_cuda:
             raise RuntimeError(f"{_UNAVAILABLE}: x must be a HIP tensor")
@@ -191,15 +201,15 @@ def _traced(x, branch, weight, bias, dropout_p, eps, training, implementation):
             raise RuntimeError(
                 f"{_UNAVAILABLE}: native hidden size must be one of {NATIVE_HIDDEN_SIZES}"
             )
-        return residual_layer_norm_op(x, branch, weight, bias, dropout_p, eps, training)
+        return residual_layer_norm_op(*args)
     if implementation == "triton":
         raise RuntimeError(
             f"{TARGET_ARCHITECTURE} residual LayerNorm is unavailable: "
             "the Triton backend is not part of the MI355X build"
         )
     if native and _input_reason(x, branch, weight, bias, dropout_p, eps) is None:
-        return residual_layer_norm_op(x, branch, weight, bias, dropout_p, eps, training)
-    return _torch_residual_layer_norm(x, branch, weight, bias, dropout_p, eps, training)
+        return residual_layer_norm_op(*args)
+    return _torch_residual_layer_norm(*args)
 
 
 def residual_layer_norm(
@@ -212,23 +222,31 @@ def residual_layer_norm(
     training=True,
     *,
     implementation="auto",
+    normalized_dtype=None,
 ):
     """Fused ``dropout(branch) -> x + . -> LayerNorm``; returns ``(updated, normalized)``.
 
     ``updated`` is the new fp32 residual stream and ``normalized`` its
-    LayerNorm with ``weight``/``bias``. Supports first-order autograd, HIP
-    graph capture and ``torch.compile``.
+    LayerNorm with ``weight``/``bias``, in fp32 or, when ``normalized_dtype``
+    is ``torch.float16`` / ``torch.bfloat16``, rounded to that type for a
+    half-precision consumer (the reference always returns fp32). ``branch``
+    may be fp32, fp16 or bf16. Supports first-order autograd, HIP graph
+    capture and ``torch.compile``.
     """
     if implementation not in IMPLEMENTATIONS:
         raise ValueError(
             "implementation must be 'auto', 'gfx950', 'gfx1010', 'triton' or 'torch'"
         )
+    if normalized_dtype is not None and normalized_dtype not in NORMALIZED_DTYPES:
+        raise ValueError("normalized_dtype must be None, torch.float32, torch.float16 "
+                         "or torch.bfloat16")
+    args = (x, branch, weight, bias, dropout_p, eps, training, normalized_dtype)
     if implementation == "torch":
-        return _torch_residual_layer_norm(x, branch, weight, bias, dropout_p, eps, training)
+        return _torch_residual_layer_norm(*args)
     if torch.compiler.is_compiling():
-        return _traced(x, branch, weight, bias, dropout_p, eps, training, implementation)
+        return _traced(*args, implementation)
     if implementation in _STRICT_NATIVE:
-        return _strict_native(x, branch, weight, bias, dropout_p, eps, training)
+        return _strict_native(*args)
 
     reason = _input_reason(x, branch, weight, bias, dropout_p, eps)
     if implementation == "triton":
@@ -237,20 +255,18 @@ def residual_layer_norm(
             + (reason or "the Triton backend is not part of the MI355X build")
         )
     if reason is not None:
-        return _fall_back(reason, x, branch, weight, bias, dropout_p, eps, training)
+        return _fall_back(reason, *args)
     if x.shape[-1] not in NATIVE_HIDDEN_SIZES:
-        return _fall_back(
-            f"native hidden size must be one of {NATIVE_HIDDEN_SIZES}",
-            x, branch, weight, bias, dropout_p, eps, training,
-        )
+        return _fall_back(f"native hidden size must be one of {NATIVE_HIDDEN_SIZES}", *args)
     status = residual_layer_norm_status(x.device)
     if not status.available:
         if status.architecture == TARGET_ARCHITECTURE:
             raise RuntimeError(f"{_UNAVAILABLE}: {status.reason}")
-        return _fall_back(status.reason, x, branch, weight, bias, dropout_p, eps, training)
+        return _fall_back(status.reason, *args)
     from ._normalization_native import native_residual_layer_norm
 
     with torch.cuda.device(x.device):
         return native_residual_layer_norm(
-            x, branch, weight, bias, float(dropout_p), float(eps), bool(training)
+            x, branch, weight, bias, float(dropout_p), float(eps), bool(training),
+            normalized_dtype=normalized_dtype,
         )

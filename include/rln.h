@@ -40,9 +40,12 @@
 extern "C" {
 #endif
 
+/* Element types of the branch, grad_branch, normalized and grad_normalized
+ * tensors (x, updated, mean, rstd and the other gradients are always fp32). */
 enum rln_dtype {
     RLN_DTYPE_F32 = 0,
-    RLN_DTYPE_F16 = 1
+    RLN_DTYPE_F16 = 1,
+    RLN_DTYPE_BF16 = 2
 };
 
 enum rln_status {
@@ -71,8 +74,10 @@ typedef struct rln_philox {
  * Forward. Replaces residual_layer_norm_forward_hip
  * (csrc/residual_layer_norm.h:10-24; csrc/residual_layer_norm_kernel.hip:1720-1827).
  *
- * x, updated, normalized: fp32 [rows, hidden]; branch: [rows, hidden] in
- * `branch_dtype`; weight, bias: fp32 [hidden]; mean, rstd: fp32 [rows].
+ * x, updated: fp32 [rows, hidden]; branch: [rows, hidden] in `branch_dtype`;
+ * normalized: [rows, hidden] in `normalized_dtype` (fp32 in the reference;
+ * fp16/bf16 round the fp32 result to nearest even for a consumer that reads
+ * half precision); weight, bias: fp32 [hidden]; mean, rstd: fp32 [rows].
  * dropout_mask: rln_mask_words(rows, hidden) uint32 words, written only when
  * training && dropout_p > 0 (may be NULL otherwise). `philox` is read only in
  * that case (may be NULL otherwise). The call consumes
@@ -85,7 +90,8 @@ int rln_forward(
     const float* weight,
     const float* bias,
     float* updated,
-    float* normalized,
+    void* normalized,
+    int normalized_dtype,
     float* mean,
     float* rstd,
     uint32_t* dropout_mask,
@@ -101,9 +107,10 @@ int rln_forward(
  * Backward. Replaces residual_layer_norm_backward_hip
  * (csrc/residual_layer_norm.h:27-42; csrc/residual_layer_norm_kernel.hip:1830-2036).
  *
- * grad_updated, grad_normalized: fp32 [rows, hidden] upstream gradients; either
- * may be NULL, meaning zero (the reference materializes zeros instead,
- * csrc/residual_layer_norm_bindings.cpp:62-67).
+ * grad_updated: fp32 [rows, hidden]; grad_normalized: [rows, hidden] in
+ * `grad_normalized_dtype` (the dtype of the forward's normalized output);
+ * either upstream gradient may be NULL, meaning zero (the reference
+ * materializes zeros instead, csrc/residual_layer_norm_bindings.cpp:62-67).
  * grad_x: fp32 [rows, hidden]; grad_branch: [rows, hidden] in branch_dtype.
  * grad_weight, grad_bias: fp32 [hidden], both NULL to skip the parameter
  * gradients (they are skipped as well when grad_normalized is NULL; the
@@ -119,7 +126,8 @@ int rln_forward(
  */
 int rln_backward(
     const float* grad_updated,
-    const float* grad_normalized,
+    const void* grad_normalized,
+    int grad_normalized_dtype,
     const float* updated,
     const float* weight,
     const float* mean,

@@ -12,6 +12,8 @@ Restatement of the reference's algorithm, in numpy:
 * ``dropped_branch`` / ``updated``: d = round_to_branch_dtype(float(b) * keep *
   scale) with fp32 products, then one fp32 add u = x + d
   (csrc/residual_layer_norm_kernel.hip:488-498). Bit-exact by construction.
+  The reference has fp16 and fp32 branches; bfloat16 (this build's addition)
+  rounds with ``round_to_bfloat16``.
 * ``layer_norm_forward``: two-pass mean / centred variance / rsqrt / affine in
   fp64 (csrc/residual_layer_norm_kernel.hip:516-544;
   docs/residual_layer_norm.md:85-109).
@@ -30,6 +32,8 @@ How each function is pinned (tests/test_oracle.py):
 * dropout constants: closed forms (p = 0.5, 0.25, 0.75 give exact powers of
   two) and the reference's probability conversion for p = 0.1.
 * updated: torch's own fp32 add for p = 0; hand-computed fp16 products.
+* round_to_bfloat16 / round_to_float16: torch's CPU conversions on ties,
+  subnormals, overflow, infinities and NaN.
 * forward / backward / parameter gradients: golden vectors written by
   tests/golden/make_golden.py from PyTorch's float64 ``F.layer_norm`` and
   autograd (the reference's fallback decomposition,
@@ -142,21 +146,59 @@ def encode_mask(keep: np.ndarray) -> np.ndarray:
     return packed.view("<u4").astype(np.uint32)
 
 
-def dropped_branch(branch: np.ndarray, keep: np.ndarray | None, scale) -> np.ndarray:
-    """round_to_branch_dtype(float(b) * keep * scale), as fp32."""
+def round_to_bfloat16(values) -> np.ndarray:
+    """fp32 -> bfloat16 -> fp32, rounding to nearest even (NaN stays NaN).
+
+    bfloat16 is the upper half of an fp32 word: add 0x7FFF plus the lowest
+    kept bit, then clear the low 16 bits (the IEEE round-to-nearest-even rule
+    on the dropped half; overflow carries into the exponent and gives inf)."""
+    values = np.asarray(values, dtype=np.float32)
+    bits = values.view(np.uint32).astype(np.uint64)
+    rounded = ((bits + 0x7FFF + ((bits >> 16) & 1)) >> 16) << 16
+    out = (rounded & 0xFFFFFFFF).astype(np.uint32).view(np.float32)
+    return np.where(np.isnan(values), np.float32(np.nan), out).astype(np.float32)
+
+
+def round_to_float16(values) -> np.ndarray:
+    """fp32 -> float16 -> fp32 (numpy's conversion rounds to nearest even;
+    values beyond the float16 range become infinities)."""
+    with np.errstate(over="ignore"):
+        return np.asarray(values, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
+def round_to(values, dtype: str) -> np.ndarray:
+    """Round fp32 values through "f32" (identity), "f16" or "bf16"."""
+    if dtype == "f16":
+        return round_to_float16(values)
+    if dtype == "bf16":
+        return round_to_bfloat16(values)
+    return np.asarray(values, dtype=np.float32)
+
+
+def _branch_type(branch: np.ndarray, branch_type: str | None) -> str:
+    if branch_type is not None:
+        return branch_type
+    return "f16" if branch.dtype == np.float16 else "f32"
+
+
+def dropped_branch(branch: np.ndarray, keep: np.ndarray | None, scale,
+                   branch_type: str | None = None) -> np.ndarray:
+    """round_to_branch_dtype(float(b) * keep * scale), as fp32.
+
+    ``branch_type`` ("f32", "f16", "bf16") defaults to the numpy dtype; a
+    bfloat16 branch is passed as its exact fp32 values with "bf16"."""
     b32 = branch.astype(np.float32)
     if keep is None:
         return b32
     product = (b32 * keep.astype(np.float32)) * np.float32(scale)
-    if branch.dtype == np.float16:
-        product = product.astype(np.float16).astype(np.float32)
-    return product
+    return round_to(product, _branch_type(branch, branch_type))
 
 
-def updated(x: np.ndarray, branch: np.ndarray, keep=None, scale=1.0) -> np.ndarray:
+def updated(x: np.ndarray, branch: np.ndarray, keep=None, scale=1.0,
+            branch_type: str | None = None) -> np.ndarray:
     """The residual update x + dropped branch, one fp32 add (bit-exact)."""
     assert x.dtype == np.float32
-    return x + dropped_branch(branch, keep, scale)
+    return x + dropped_branch(branch, keep, scale, branch_type)
 
 
 # ---------------------------------------------------------------------------
@@ -175,9 +217,9 @@ def layer_norm_forward(updated_values: np.ndarray, weight, bias, eps: float):
     return mean, rstd, normalized
 
 
-def forward(x, branch, weight, bias, eps, keep=None, scale=1.0) -> dict:
+def forward(x, branch, weight, bias, eps, keep=None, scale=1.0, branch_type=None) -> dict:
     """Forward outputs: ``updated`` (fp32, bit-exact) and fp64 statistics."""
-    upd = updated(x, branch, keep, scale)
+    upd = updated(x, branch, keep, scale, branch_type)
     mean, rstd, normalized = layer_norm_forward(upd, weight, bias, eps)
     return {"updated": upd, "normalized": normalized, "mean": mean, "rstd": rstd}
 

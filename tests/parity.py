@@ -7,8 +7,9 @@ Tolerances (written here once, used by every parity test):
 * ``normalized``, ``mean``, ``rstd``, ``grad_x`` and fp32 ``grad_branch``:
   normwise relative error ``max|a - b| / max|b|`` <= 1e-5 against the fp64
   oracle;
-* fp16 ``grad_branch``: within one fp16 ulp of the fp64 oracle value, plus
-  1e-5 of the largest magnitude (the kernel rounds its fp32 result once);
+* fp16 / bf16 ``grad_branch`` and a fp16 / bf16 ``normalized``: within one ulp
+  of that type at the fp64 oracle value, plus 1e-5 of the largest magnitude
+  (the kernel rounds its fp32 result once);
 * ``grad_weight`` / ``grad_bias``: normwise relative error <= 1e-4.
 """
 
@@ -39,13 +40,27 @@ def assert_normwise(actual, expected, tolerance, what=""):
     assert error <= tolerance, f"{what}: normwise error {error:.3e} > {tolerance:.1e}"
 
 
-def assert_fp16_close(actual_f16, expected_f64, what=""):
-    actual = np.asarray(actual_f16, dtype=np.float64)
+def half_ulp(values, kind):
+    """Spacing of fp16 ("f16") or bfloat16 ("bf16") numbers at |values|."""
+    magnitude = np.abs(np.asarray(values, dtype=np.float64))
+    if kind == "f16":
+        return np.spacing(magnitude.astype(np.float16)).astype(np.float64)
+    # bfloat16 keeps 8 significand bits: spacing 2^(e - 7), at least 2^-133.
+    exponent = np.floor(np.log2(np.maximum(magnitude, 2.0 ** -126)))
+    return np.exp2(exponent - 7)
+
+
+def assert_rounded_close(actual, expected_f64, kind, what=""):
+    """A value rounded once to fp16/bf16 lies within one ulp of the exact one."""
+    actual = np.asarray(actual, dtype=np.float64)
     expected = np.asarray(expected_f64, dtype=np.float64)
-    ulp = np.spacing(np.abs(expected).astype(np.float16)).astype(np.float64)
-    bound = ulp + 1e-5 * float(np.max(np.abs(expected)))
+    bound = half_ulp(expected, kind) + 1e-5 * float(np.max(np.abs(expected)))
     excess = np.abs(actual - expected) - bound
-    assert np.all(excess <= 0), f"{what}: fp16 error exceeds one ulp by {excess.max():.3e}"
+    assert np.all(excess <= 0), f"{what}: {kind} error exceeds one ulp by {excess.max():.3e}"
+
+
+def assert_fp16_close(actual_f16, expected_f64, what=""):
+    assert_rounded_close(actual_f16, expected_f64, "f16", what)
 
 
 def assert_bitwise(actual, expected, what=""):
@@ -60,8 +75,19 @@ def assert_bitwise(actual, expected, what=""):
     assert mismatches == 0, f"{what}: {mismatches} of {a.size} values differ bitwise"
 
 
+KIND = {torch.float32: "f32", torch.float16: "f16", torch.bfloat16: "bf16"}
+
+
 def host(tensor: torch.Tensor) -> np.ndarray:
-    return tensor.detach().cpu().numpy()
+    """Host copy; bfloat16 (which numpy lacks) comes back as its exact fp32 values."""
+    tensor = tensor.detach()
+    if tensor.dtype == torch.bfloat16:
+        tensor = tensor.float()
+    return tensor.cpu().numpy()
+
+
+def kind(tensor: torch.Tensor) -> str:
+    return KIND[tensor.dtype]
 
 
 def make_inputs(shape, branch_dtype, seed, x_mean=0.0, x_std=1.0, branch_std=1.0,
@@ -98,6 +124,7 @@ def oracle_keep(rows, hidden, dropout_p, training, seed, offset):
 def check_forward(outputs, inputs, dropout_p, training, eps, seed, offset, what=""):
     """Compare raw forward outputs (updated, normalized, mean, rstd, mask) to the oracle."""
     updated, normalized, mean, rstd, mask = outputs
+    branch_kind = kind(inputs[1])
     x, branch, weight, bias = (host(t) for t in inputs)
     hidden = x.shape[-1]
     rows = x.size // hidden
@@ -108,10 +135,15 @@ def check_forward(outputs, inputs, dropout_p, training, eps, seed, offset, what=
         assert mask.numel() == 0
     x2 = x.reshape(rows, hidden)
     b2 = branch.reshape(rows, hidden)
-    expected = oracle.forward(x2, b2, weight, bias, eps, keep=keep, scale=scale)
+    expected = oracle.forward(x2, b2, weight, bias, eps, keep=keep, scale=scale,
+                              branch_type=branch_kind)
     assert_bitwise(host(updated).reshape(rows, hidden), expected["updated"], f"{what} updated")
-    assert_normwise(host(normalized).reshape(rows, hidden), expected["normalized"], TOL_FORWARD,
-                    f"{what} normalized")
+    if normalized.dtype == torch.float32:
+        assert_normwise(host(normalized).reshape(rows, hidden), expected["normalized"],
+                        TOL_FORWARD, f"{what} normalized")
+    else:
+        assert_rounded_close(host(normalized).reshape(rows, hidden), expected["normalized"],
+                             kind(normalized), f"{what} normalized")
     assert_normwise(host(mean), expected["mean"], TOL_FORWARD, f"{what} mean")
     assert_normwise(host(rstd), expected["rstd"], TOL_FORWARD, f"{what} rstd")
     return keep, scale
@@ -129,10 +161,11 @@ def check_backward(gradients, grad_updated, grad_normalized, updated, weight, ep
     assert_normwise(host(grad_x).reshape(-1, hidden), expected["grad_x"], TOL_INPUT_GRAD,
                     f"{what} grad_x")
     gb = host(grad_branch).reshape(-1, hidden)
-    if gb.dtype == np.float16:
-        assert_fp16_close(gb, expected["grad_branch"], f"{what} grad_branch")
-    else:
+    if grad_branch.dtype == torch.float32:
         assert_normwise(gb, expected["grad_branch"], TOL_INPUT_GRAD, f"{what} grad_branch")
+    else:
+        assert_rounded_close(gb, expected["grad_branch"], kind(grad_branch),
+                             f"{what} grad_branch")
     if parameters:
         assert_normwise(host(grad_weight), expected["grad_weight"], TOL_PARAMETER_GRAD,
                         f"{what} grad_weight")

@@ -79,7 +79,8 @@ def _forward(**overrides):
     [
         (dict(rows=0), _cabi.RLN_ERR_INVALID, "empty tensors are unsupported"),
         (dict(hidden=160), _cabi.RLN_ERR_UNSUPPORTED, "unsupported native hidden size: 160"),
-        (dict(branch_dtype=7), _cabi.RLN_ERR_INVALID, "branch must use float16 or float32"),
+        (dict(branch_dtype=7), _cabi.RLN_ERR_INVALID, "branch must use float16, bfloat16 or float32"),
+        (dict(normalized_dtype=5), _cabi.RLN_ERR_INVALID, "normalized must use"),
         (dict(dropout_p=1.0), _cabi.RLN_ERR_INVALID, r"dropout_p must be in \[0, 1\)"),
         (dict(dropout_p=-0.1), _cabi.RLN_ERR_INVALID, r"dropout_p must be in \[0, 1\)"),
         (dict(dropout_p=0.999999999), _cabi.RLN_ERR_INVALID, r"dropout_p must be in \[0, 1\)"),

@@ -161,7 +161,7 @@ def test_auto_falls_back_for_non_native_hidden_size(monkeypatch):
     "mutate,reason",
     [
         (lambda t: t.update(x=t["x"].double()), "requires float32 x"),
-        (lambda t: t.update(branch=t["branch"].to(torch.bfloat16)), "float16 or float32"),
+        (lambda t: t.update(branch=t["branch"].double()), "float16, bfloat16 or float32"),
         (lambda t: t.update(weight=t["weight"][:-8]), "match the final tensor dimension"),
         (lambda t: t.update(x=t["x"][:, :120].contiguous(), branch=t["branch"][:, :120].contiguous(),
                             weight=t["weight"][:120], bias=t["bias"][:120]), "between 128 and 1024"),

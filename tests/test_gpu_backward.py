@@ -40,13 +40,19 @@ def deterministic_algorithms(enabled):
 
 def raw_backward(grad_updated, grad_normalized, outputs, weight, dropout_p, branch_is_half,
                  training=True, parameters=True):
+    """``branch_is_half`` is the reference's flag, or a torch dtype (bf16 included)."""
+    extra = {}
+    if isinstance(branch_is_half, torch.dtype):
+        extra["branch_dtype"] = branch_is_half
+        branch_is_half = branch_is_half == torch.float16
     return _C.residual_layer_norm_backward(
         grad_updated, grad_normalized, outputs[0], weight, outputs[2], outputs[3], outputs[4],
-        dropout_p, training, branch_is_half, 128, 64, 64, 1, parameters)
+        dropout_p, training, branch_is_half, 128, 64, 64, 1, parameters, **extra)
 
 
 @pytest.mark.parametrize("hidden", NATIVE_HIDDEN_SIZES)
-@pytest.mark.parametrize("branch_dtype", [torch.float16, torch.float32], ids=["f16", "f32"])
+@pytest.mark.parametrize("branch_dtype", [torch.float16, torch.bfloat16, torch.float32],
+                         ids=["f16", "bf16", "f32"])
 @pytest.mark.parametrize("dropout_p", [0.0, 0.15])
 @pytest.mark.parametrize("deterministic", [False, True], ids=["atomic", "deterministic"])
 def test_backward_matches_oracle(hidden, branch_dtype, dropout_p, deterministic):
@@ -59,7 +65,7 @@ def test_backward_matches_oracle(hidden, branch_dtype, dropout_p, deterministic)
     keep, scale = check_forward(outputs, inputs, dropout_p, True, 1e-5, seed, offset)
     with deterministic_algorithms(deterministic):
         gradients = raw_backward(grad_updated, grad_normalized, outputs, inputs[2], dropout_p,
-                                 branch_dtype == torch.float16)
+                                 branch_dtype)
     check_backward(gradients, grad_updated, grad_normalized, outputs[0], inputs[2], 1e-5, keep,
                    scale, f"H={hidden}")
     assert gradients[1].dtype == branch_dtype

@@ -34,13 +34,15 @@ def test_opcheck_forward_and_backward():
     # requires (it compares several executions).
     torch.library.opcheck(torch.ops.gfx1010_kernels.rln_forward.default,
                           (*inputs, 0.0, 1e-5, True))
+    torch.library.opcheck(torch.ops.gfx1010_kernels.rln_forward.default,
+                          (*inputs, 0.0, 1e-5, True, torch.bfloat16))
     outputs = torch.ops.gfx1010_kernels.rln_forward(*inputs, 0.0, 1e-5, True)
     grads = make_grads((33, 512), seed=4)
     with deterministic_algorithms():
         torch.library.opcheck(
             torch.ops.gfx1010_kernels.rln_backward.default,
             (grads[0], grads[1], outputs[0], inputs[2], outputs[2], outputs[3], outputs[4],
-             0.0, True, True))
+             0.0, True, torch.float16))
 
 
 @pytest.mark.parametrize("implementation", ["gfx950", "auto"])

@@ -1,6 +1,6 @@
 """Forward parity of the gfx950 kernels against the CPU oracle.
 
-Covers every hidden specialization, both branch dtypes, eval / train p=0 /
+Covers every hidden specialization, the fp16 / bf16 / fp32 branch, eval / train p=0 /
 train with dropout, the reference's row-count boundaries
 (tests/test_residual_layer_norm_native_matrix.py:171-181) and the misaligned
 element-access path (tests/test_residual_layer_norm_vectorized.py:96-164).
@@ -29,7 +29,8 @@ MODES = {
 
 
 @pytest.mark.parametrize("hidden", NATIVE_HIDDEN_SIZES)
-@pytest.mark.parametrize("branch_dtype", [torch.float16, torch.float32], ids=["f16", "f32"])
+@pytest.mark.parametrize("branch_dtype", [torch.float16, torch.bfloat16, torch.float32],
+                         ids=["f16", "bf16", "f32"])
 @pytest.mark.parametrize("mode", list(MODES))
 def test_forward_matches_oracle(hidden, branch_dtype, mode):
     dropout_p, training = MODES[mode]

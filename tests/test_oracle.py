@@ -284,3 +284,32 @@ def test_backward_matches_finite_differences():
             flat[index] = original
             numeric = (plus - minus) / (2 * step)
             assert abs(numeric - expected.reshape(-1)[index]) < 1e-5 * max(1.0, abs(numeric)), name
+
+
+@pytest.mark.parametrize("torch_dtype,rounding", [(torch.bfloat16, oracle.round_to_bfloat16),
+                                                  (torch.float16, oracle.round_to_float16)])
+def test_half_precision_rounding_matches_torch(torch_dtype, rounding):
+    generator = torch.Generator().manual_seed(5)
+    random = torch.randn(100000, generator=generator) * torch.logspace(-40, 38, 100000)
+    info = torch.finfo(torch_dtype)
+    special = torch.tensor([
+        0.0, -0.0, 1.0, -1.0, float("inf"), float("-inf"),
+        1.0 + 2.0 ** -8, 1.0 + 3 * 2.0 ** -8, 1.0 + 2.0 ** -12, 1.0 + 3 * 2.0 ** -12,  # ties
+        info.max, float(info.max) * 1.0001, float(info.tiny) / 3, 1e-45, 3.4e38,
+    ])
+    values = torch.cat([random, special]).float()
+    expected = values.to(torch_dtype).float().numpy()
+    actual = rounding(values.numpy())
+    assert np.array_equal(actual.view(np.uint32), expected.view(np.uint32))
+    nan = rounding(np.array([np.nan], np.float32))
+    assert np.isnan(nan).all()
+
+
+def test_dropped_bfloat16_branch_rounds_fp32_product_once():
+    branch = oracle.round_to_bfloat16(np.array([1.0, 0.3, -2.7, 1e-3], np.float32))
+    keep = np.array([True, True, False, True])
+    _, scale, _ = oracle.dropout_constants(0.1)
+    product = branch * keep.astype(np.float32) * scale
+    expected = torch.from_numpy(product).to(torch.bfloat16).float().numpy()
+    got = oracle.dropped_branch(branch, keep, scale, "bf16")
+    assert np.array_equal(got, expected)
