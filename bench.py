@@ -58,12 +58,16 @@ EPS = 1e-5
 TRAFFIC_FILE = REPO / "profiles" / "rln_backward_c1_traffic.json"
 
 
+DTYPE_BYTES = {"f32": 4, "f16": 2, "bf16": 2}
+DTYPE_NAMES = {"f32": "float32", "f16": "float16", "bf16": "bfloat16"}
+
+
 @dataclass(frozen=True)
 class Workload:
     name: str
     rows: int
     hidden: int
-    half_branch: bool
+    branch: str  # "f32", "f16" or "bf16"
     branch_std: float
     dropout_p: float
     training: bool = True
@@ -71,10 +75,15 @@ class Workload:
     deterministic: bool = False
     x_mean: float = 0.0
     seed: int = 1001
+    normalized: str = "f32"  # dtype of normalized and of its upstream gradient
 
     @property
     def branch_bytes(self) -> int:
-        return 2 if self.half_branch else 4
+        return DTYPE_BYTES[self.branch]
+
+    @property
+    def normalized_bytes(self) -> int:
+        return DTYPE_BYTES[self.normalized]
 
     @property
     def dropping(self) -> bool:
@@ -82,41 +91,48 @@ class Workload:
 
     def forward_bytes(self) -> int:
         mask = self.hidden // 8 if self.dropping else 0
-        per_row = self.hidden * (4 + self.branch_bytes + 4 + 4) + 8 + mask
+        per_row = self.hidden * (4 + self.branch_bytes + 4 + self.normalized_bytes) + 8 + mask
         return self.rows * per_row + 8 * self.hidden
 
     def backward_bytes(self) -> int:
         if not self.backward:
             return 0
         mask = self.hidden // 8 if self.dropping else 0
-        per_row = self.hidden * (4 + 4 + 4 + 4 + self.branch_bytes) + 8 + mask
+        per_row = (self.hidden * (4 + self.normalized_bytes + 4 + 4 + self.branch_bytes)
+                   + 8 + mask)
         return self.rows * per_row + 12 * self.hidden
 
     def describe(self) -> str:
-        branch = "fp16" if self.half_branch else "fp32"
         mode = "fwd+bwd" if self.backward else "fwd"
         reduction = "deterministic" if self.deterministic else "atomic"
         suffix = f", {reduction} dW/db" if self.backward else ""
-        return (f"{self.name} {mode}: x fp32 [{self.rows},{self.hidden}], branch {branch}, "
-                f"dropout_p={self.dropout_p}, training={self.training}{suffix}")
+        output = "" if self.normalized == "f32" else f", normalized {self.normalized}"
+        return (f"{self.name} {mode}: x fp32 [{self.rows},{self.hidden}], branch {self.branch}"
+                f"{output}, dropout_p={self.dropout_p}, training={self.training}{suffix}")
 
 
-C1 = Workload("C1", 8 * 1024, 768, True, 0.5, 0.1, seed=1001)
+C1 = Workload("C1", 8 * 1024, 768, "f16", 0.5, 0.1, seed=1001)
 
 
 def sweep_workloads() -> list[Workload]:
     """The other BASELINE.json configurations."""
-    workloads = [Workload("C0", 4 * 1024, 768, False, 1.0, 0.0, training=False,
+    workloads = [Workload("C0", 4 * 1024, 768, "f32", 1.0, 0.0, training=False,
                           backward=False, seed=1000)]
     for hidden in (128, 256, 384, 512, 768, 1024):
-        workloads.append(Workload(f"C2 H={hidden}", 262144, hidden, True, 1.0, 0.15,
+        workloads.append(Workload(f"C2 H={hidden}", 262144, hidden, "f16", 1.0, 0.15,
                                   seed=1002 + hidden))
-    workloads.append(Workload("C3", 32 * 2048, 1024, True, 0.5, 0.15, deterministic=True,
+    workloads.append(Workload("C3", 32 * 2048, 1024, "f16", 0.5, 0.15, deterministic=True,
                               seed=1003))
     for dropout_p in (0.0, 0.1):
-        workloads.append(Workload(f"C4 tail p={dropout_p}", 3 * 4097, 384, False, 1.0,
+        workloads.append(Workload(f"C4 tail p={dropout_p}", 3 * 4097, 384, "f32", 1.0,
                                   dropout_p, x_mean=100.0, seed=1004))
-    workloads.append(Workload("C4 large", 64 * 4096, 1024, True, 1.0, 0.1, seed=1006))
+    workloads.append(Workload("C4 large", 64 * 4096, 1024, "f16", 1.0, 0.1, seed=1006))
+    # Half-precision interfaces (beyond the reference): bf16 branch, bf16
+    # normalized output and upstream gradient, at the C1 and C2 H=768 shapes.
+    workloads.append(Workload("C1 bf16-out", 8 * 1024, 768, "bf16", 0.5, 0.1, seed=1001,
+                              normalized="bf16"))
+    workloads.append(Workload("C2 H=768 bf16-out", 262144, 768, "bf16", 1.0, 0.15,
+                              seed=1770, normalized="bf16"))
     return workloads
 
 
@@ -146,7 +162,7 @@ def cpu_baseline(torch, workload: Workload, budget_seconds: float) -> dict:
     shape = (workload.rows, workload.hidden)
     x = torch.randn(shape, generator=generator).requires_grad_(True)
     branch = (workload.branch_std * torch.randn(shape, generator=generator))
-    branch = (branch.half() if workload.half_branch else branch).requires_grad_(True)
+    branch = branch.to(getattr(torch, DTYPE_NAMES[workload.branch])).requires_grad_(True)
     weight = (1.0 + 0.02 * torch.randn(workload.hidden, generator=generator)).requires_grad_(True)
     bias = (0.02 * torch.randn(workload.hidden, generator=generator)).requires_grad_(True)
     grad_updated = torch.randn(shape, generator=generator)
@@ -212,11 +228,12 @@ class Runner:
         shape = (w.rows, w.hidden)
         f32 = dict(device="cuda", dtype=torch.float32)
         branch = torch.randn(shape, generator=generator, **f32) * w.branch_std
+        normalized_type = getattr(torch, DTYPE_NAMES[w.normalized])
         tensors = {
             "x": torch.randn(shape, generator=generator, **f32) + w.x_mean,
-            "branch": branch.half() if w.half_branch else branch,
+            "branch": branch.to(getattr(torch, DTYPE_NAMES[w.branch])),
             "updated": torch.empty(shape, **f32),
-            "normalized": torch.empty(shape, **f32),
+            "normalized": torch.empty(shape, device="cuda", dtype=normalized_type),
             "mean": torch.empty(w.rows, **f32),
             "rstd": torch.empty(w.rows, **f32),
             "mask": torch.empty(max(w.rows * w.hidden // 32, 1), device="cuda",
@@ -225,26 +242,26 @@ class Runner:
         if w.backward:
             tensors.update(
                 grad_updated=torch.randn(shape, generator=generator, **f32),
-                grad_normalized=torch.randn(shape, generator=generator, **f32),
+                grad_normalized=torch.randn(shape, generator=generator, **f32).to(normalized_type),
                 grad_x=torch.empty(shape, **f32),
                 grad_branch=torch.empty(shape, device="cuda",
-                                        dtype=torch.float16 if w.half_branch else torch.float32),
+                                        dtype=getattr(torch, DTYPE_NAMES[w.branch])),
                 grad_weight=torch.zeros(w.hidden, **f32),
                 grad_bias=torch.zeros(w.hidden, **f32),
             )
         return tensors
 
-    @property
-    def dtype(self) -> int:
-        return self.cabi.RLN_DTYPE_F16 if self.w.half_branch else self.cabi.RLN_DTYPE_F32
+    def code(self, name: str) -> int:
+        return {"f32": self.cabi.RLN_DTYPE_F32, "f16": self.cabi.RLN_DTYPE_F16,
+                "bf16": self.cabi.RLN_DTYPE_BF16}[name]
 
     def forward(self, step: int):
         t, w = self.sets[step % len(self.sets)], self.w
         philox = self.cabi.RlnPhilox(self.seed, 4 * step, None, None)
         status = self.library.rln_forward(
-            t["x"].data_ptr(), t["branch"].data_ptr(), self.dtype, self.weight.data_ptr(),
+            t["x"].data_ptr(), t["branch"].data_ptr(), self.code(w.branch), self.weight.data_ptr(),
             self.bias.data_ptr(), t["updated"].data_ptr(), t["normalized"].data_ptr(),
-            self.cabi.RLN_DTYPE_F32, t["mean"].data_ptr(), t["rstd"].data_ptr(),
+            self.code(w.normalized), t["mean"].data_ptr(), t["rstd"].data_ptr(),
             t["mask"].data_ptr(), w.rows, w.hidden,
             w.dropout_p, EPS, int(w.training), philox, self.handle)
         if status:
@@ -255,9 +272,9 @@ class Runner:
         workspace = self.workspace
         status = self.library.rln_backward(
             t["grad_updated"].data_ptr(), t["grad_normalized"].data_ptr(),
-            self.cabi.RLN_DTYPE_F32, t["updated"].data_ptr(), self.weight.data_ptr(), t["mean"].data_ptr(),
+            self.code(w.normalized), t["updated"].data_ptr(), self.weight.data_ptr(), t["mean"].data_ptr(),
             t["rstd"].data_ptr(), t["mask"].data_ptr(), t["grad_x"].data_ptr(),
-            t["grad_branch"].data_ptr(), self.dtype, t["grad_weight"].data_ptr(),
+            t["grad_branch"].data_ptr(), self.code(w.branch), t["grad_weight"].data_ptr(),
             t["grad_bias"].data_ptr(), w.rows, w.hidden, w.dropout_p, int(w.training),
             int(w.deterministic), 1,
             workspace.data_ptr() if workspace is not None else None,
@@ -327,7 +344,7 @@ def result_line(torch, workload: Workload, timing: dict, steps: int, warmup: int
     else:
         dominant, dominant_ms = "rln_forward_kernel", timing["forward_ms"]
         dominant_bytes = workload.forward_bytes()
-    branch_type = "_Float16" if workload.half_branch else "float"
+    branch_type = {"f32": "float", "f16": "_Float16", "bf16": "__bf16"}[workload.branch]
     dominant_gbps = gbps(dominant_bytes, dominant_ms)
     line = {
         "metric": METRIC,
@@ -347,7 +364,8 @@ def result_line(torch, workload: Workload, timing: dict, steps: int, warmup: int
             "rows": workload.rows,
             "hidden": workload.hidden,
             "dropout_p": workload.dropout_p,
-            "branch_dtype": "float16" if workload.half_branch else "float32",
+            "branch_dtype": DTYPE_NAMES[workload.branch],
+            "normalized_dtype": DTYPE_NAMES[workload.normalized],
             "parallelism": "single GPU",
         },
         "pct_of_peak": round(100.0 * value / HBM_PEAK_GBPS, 2),

@@ -36,9 +36,8 @@ GLUE = PACKAGE / f"_C{sysconfig.get_config_var('EXT_SUFFIX')}"
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",
-    "-std=c++17",
+    "-std=c++20",
     "-fPIC",
-    "-shared",
     "-ffp-contract=off",
     "-mcode-object-version=5",
     "-Xclang",
@@ -48,6 +47,11 @@ HIP_FLAGS = [
     "-Wall",
     "-Wno-unused-command-line-argument",
 ]
+
+# One translation unit per hidden size (every dtype and alignment variant of
+# its kernels), plus the C ABI; compiled in parallel, linked into one library.
+HIDDEN_SIZES = (128, 256, 384, 512, 768, 1024)
+BUILD_DIR = ROOT / "_build"
 
 
 def _run(command: list[str]) -> None:
@@ -60,14 +64,28 @@ def _run(command: list[str]) -> None:
         )
 
 
-def build_library() -> Path:
+def _compile_object(source: Path, output: Path, defines: list[str]) -> Path:
+    hipcc = str(ROCM / "bin" / "hipcc")
+    _run([hipcc, *HIP_FLAGS, *defines, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(source),
+          "-o", str(output)])
+    return output
+
+
+def build_library(jobs: int | None = None) -> Path:
     """Compile the gfx950 kernels and C ABI into librln_gfx950.so."""
+    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+    units = [(CSRC / "rln_api.hip", BUILD_DIR / "rln_api.o", [])]
+    units += [
+        (CSRC / "rln_hidden.hip", BUILD_DIR / f"rln_hidden_{hidden}.o", [f"-DRLN_HIDDEN={hidden}"])
+        for hidden in HIDDEN_SIZES
+    ]
+    workers = jobs or min(len(units), max(1, (os.cpu_count() or 1)))
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        objects = list(pool.map(lambda unit: _compile_object(*unit), units))
     hipcc = str(ROCM / "bin" / "hipcc")
     temporary = LIBRARY.with_name(LIBRARY.name + ".tmp")
-    _run(
-        [hipcc, *HIP_FLAGS, f"-I{INCLUDE}", str(CSRC / "rln_kernels.hip"),
-         f"-Wl,-soname,{LIBRARY.name}", "-o", str(temporary)]
-    )
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects),
+          f"-Wl,-soname,{LIBRARY.name}", "-o", str(temporary)])
     os.replace(temporary, LIBRARY)
     return LIBRARY
 
@@ -127,8 +145,7 @@ def build_glue() -> Path:
 def build() -> tuple[Path, Path]:
     """Build both artefacts (the library first: the glue links against it)."""
     PACKAGE.mkdir(parents=True, exist_ok=True)
-    with ThreadPoolExecutor(max_workers=1) as pool:
-        library = pool.submit(build_library).result()
+    library = build_library()
     glue = build_glue()
     return library, glue
 

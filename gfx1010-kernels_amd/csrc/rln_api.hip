@@ -1,0 +1,419 @@
+// C ABI of the MI355X fused residual LayerNorm (include/rln.h): argument
+// checks, dropout constants, dispatch to the per-hidden-size launchers
+// (rln_device.h, instantiated in rln_hidden.hip), and the small kernels that
+// zero or reduce the weight/bias gradients.
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "rln_device.h"
+
+namespace rln {
+
+RLN_FOR_EACH_HIDDEN(RLN_DECLARE_HIDDEN)
+
+namespace {
+
+thread_local std::string t_last_error;
+
+}  // namespace
+
+int fail(int code, const char* format, ...) {
+    char buffer[512];
+    va_list args;
+    va_start(args, format);
+    vsnprintf(buffer, sizeof(buffer), format, args);
+    va_end(args);
+    t_last_error = buffer;
+    return code;
+}
+
+int check_launch(const char* what) {
+    const hipError_t status = hipGetLastError();
+    if (status != hipSuccess) {
+        return fail(
+            RLN_ERR_HIP,
+            "%s launch failed: %s",
+            what,
+            hipGetErrorString(status));
+    }
+    return RLN_OK;
+}
+
+namespace {
+
+// Fixed-order reduction of per-block partials [groups][2][H] into
+// grad_weight / grad_bias. Block = 16 waves over 64 consecutive entries of the
+// flattened [2][H] output; wave k sums its contiguous share of the groups in
+// ascending order, then wave sums are added in ascending wave order.
+constexpr int kReduceWaves = 16;
+
+__global__ __launch_bounds__(kReduceWaves * kWaveSize)
+void rln_parameter_reduce_kernel(
+    const float* __restrict__ partials,
+    float* __restrict__ grad_weight,
+    float* __restrict__ grad_bias,
+    int64_t groups,
+    int hidden,
+    int accumulate) {
+    __shared__ float wave_totals[kReduceWaves][kWaveSize];
+    const int lane = threadIdx.x & (kWaveSize - 1);
+    const int wave = threadIdx.x / kWaveSize;
+    const int entry = blockIdx.x * kWaveSize + lane;  // index into [2][H]
+    const bool active = entry < 2 * hidden;
+    const int64_t share = (groups + kReduceWaves - 1) / kReduceWaves;
+    const int64_t begin = wave * share;
+    const int64_t end = begin + share < groups ? begin + share : groups;
+    const int which = active ? entry / hidden : 0;
+    const int column = active ? entry % hidden : 0;
+    float total = 0.0f;
+    if (active) {
+        const float* source = partials + static_cast<int64_t>(which) * hidden + column;
+        const int64_t stride = 2 * static_cast<int64_t>(hidden);
+#pragma unroll 16
+        for (int64_t group = begin; group < end; ++group) {
+            total += source[group * stride];
+        }
+    }
+    wave_totals[wave][lane] = total;
+    __syncthreads();
+    if (wave == 0 && active) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int source = 0; source < kReduceWaves; ++source) {
+            sum += wave_totals[source][lane];
+        }
+        float* target = (which ? grad_bias : grad_weight) + column;
+        *target = accumulate ? *target + sum : sum;
+    }
+}
+
+__global__ __launch_bounds__(256)
+void rln_zero_parameters_kernel(float* __restrict__ grad_weight, float* __restrict__ grad_bias, int hidden) {
+    const int index = blockIdx.x * blockDim.x + threadIdx.x;
+    if (index < hidden) {
+        grad_weight[index] = 0.0f;
+        grad_bias[index] = 0.0f;
+    }
+}
+
+bool aligned_to(const void* pointer, uintptr_t alignment) {
+    return pointer == nullptr || (reinterpret_cast<uintptr_t>(pointer) & (alignment - 1)) == 0;
+}
+
+// Mirrors the reference's conversion of the double probability
+// (csrc/residual_layer_norm_kernel.hip:893-899, :1883-1886).
+struct DropoutConstants {
+    bool active;
+    float scale;
+    uint32_t threshold;
+};
+
+int dropout_constants(double dropout_p, int training, DropoutConstants* out) {
+    if (!(dropout_p >= 0.0 && dropout_p < 1.0)) {
+        return fail(RLN_ERR_INVALID, "dropout_p must be in [0, 1)");
+    }
+    const float p = static_cast<float>(dropout_p);
+    out->active = training && dropout_p > 0.0;
+    if (out->active && !(p < 1.0f)) {
+        return fail(RLN_ERR_INVALID, "dropout_p must be in [0, 1)");
+    }
+    out->scale = out->active ? 1.0f / (1.0f - p) : 1.0f;
+    out->threshold = out->active
+        ? static_cast<uint32_t>(static_cast<double>(p) * 4294967296.0)
+        : 0u;
+    return RLN_OK;
+}
+
+bool valid_dtype(int dtype) {
+    return dtype == RLN_DTYPE_F32 || dtype == RLN_DTYPE_F16 || dtype == RLN_DTYPE_BF16;
+}
+
+// Alignment of one four-element vector of `dtype`.
+uintptr_t vector_alignment(int dtype) {
+    return dtype == RLN_DTYPE_F32 ? 16 : 8;
+}
+
+int check_common(int64_t rows, int64_t hidden, int branch_dtype) {
+    if (rows <= 0) {
+        return fail(RLN_ERR_INVALID, "empty tensors are unsupported");
+    }
+    if (!hidden_supported(hidden)) {
+        return fail(
+            RLN_ERR_UNSUPPORTED,
+            "unsupported native hidden size: %lld",
+            static_cast<long long>(hidden));
+    }
+    if (!valid_dtype(branch_dtype)) {
+        return fail(RLN_ERR_INVALID, "branch must use float16, bfloat16 or float32");
+    }
+    if (rows > (INT64_MAX / hidden)) {
+        return fail(RLN_ERR_INVALID, "rows * hidden overflows int64");
+    }
+    return RLN_OK;
+}
+
+// Whether the parameter gradients of this call go through per-block partials
+// (and therefore the workspace and the reduce kernel).
+bool uses_partials(int deterministic) {
+    return deterministic || !RLN_ATOMIC_PARAMETERS;
+}
+
+}  // namespace
+}  // namespace rln
+
+using namespace rln;
+
+// ----------------------------------------------------------------------------
+// C ABI.
+
+extern "C" {
+
+int rln_forward(
+    const float* x,
+    const void* branch,
+    int branch_dtype,
+    const float* weight,
+    const float* bias,
+    float* updated,
+    void* normalized,
+    int normalized_dtype,
+    float* mean,
+    float* rstd,
+    uint32_t* dropout_mask,
+    int64_t rows,
+    int64_t hidden,
+    double dropout_p,
+    double eps,
+    int training,
+    const rln_philox_t* philox,
+    void* stream) {
+    rln::t_last_error.clear();
+    int status = check_common(rows, hidden, branch_dtype);
+    if (status != RLN_OK) {
+        return status;
+    }
+    if (!valid_dtype(normalized_dtype)) {
+        return fail(RLN_ERR_INVALID, "normalized must use float16, bfloat16 or float32");
+    }
+    if (!x || !branch || !weight || !bias || !updated || !normalized || !mean || !rstd) {
+        return fail(RLN_ERR_INVALID, "forward tensors must not be null");
+    }
+    if (!(eps > 0.0)) {
+        return fail(RLN_ERR_INVALID, "eps must be positive");
+    }
+    DropoutConstants drop{};
+    status = dropout_constants(dropout_p, training, &drop);
+    if (status != RLN_OK) {
+        return status;
+    }
+    ForwardArgs a{};
+    a.x = x;
+    a.branch = branch;
+    a.weight = weight;
+    a.bias = bias;
+    a.updated = updated;
+    a.normalized = normalized;
+    a.mean = mean;
+    a.rstd = rstd;
+    a.mask = dropout_mask;
+    a.rows = rows;
+    a.eps = static_cast<float>(eps);
+    a.dropout = drop.active ? 1 : 0;
+    a.scale = drop.scale;
+    a.threshold = drop.threshold;
+    a.stream = static_cast<hipStream_t>(stream);
+    if (drop.active) {
+        if (!dropout_mask) {
+            return fail(RLN_ERR_INVALID, "dropout_mask must not be null when dropout is active");
+        }
+        if (!philox) {
+            return fail(RLN_ERR_INVALID, "philox must not be null when dropout is active");
+        }
+        a.philox.seed = philox->seed;
+        a.philox.offset = philox->offset;
+        a.philox.seed_ptr = philox->seed_ptr;
+        a.philox.offset_ptr = philox->offset_ptr;
+    }
+    const bool aligned = aligned_to(x, 16) && aligned_to(weight, 16) && aligned_to(bias, 16)
+        && aligned_to(updated, 16)
+        && aligned_to(normalized, vector_alignment(normalized_dtype))
+        && aligned_to(branch, vector_alignment(branch_dtype));
+    switch (hidden) {
+        case 128: return launch_forward_hidden<128>(a, branch_dtype, normalized_dtype, aligned);
+        case 256: return launch_forward_hidden<256>(a, branch_dtype, normalized_dtype, aligned);
+        case 384: return launch_forward_hidden<384>(a, branch_dtype, normalized_dtype, aligned);
+        case 512: return launch_forward_hidden<512>(a, branch_dtype, normalized_dtype, aligned);
+        case 768: return launch_forward_hidden<768>(a, branch_dtype, normalized_dtype, aligned);
+        case 1024: return launch_forward_hidden<1024>(a, branch_dtype, normalized_dtype, aligned);
+        default: break;
+    }
+    return fail(RLN_ERR_UNSUPPORTED, "unsupported native hidden size: %lld", static_cast<long long>(hidden));
+}
+
+size_t rln_backward_workspace_bytes(int64_t rows, int64_t hidden, int deterministic) {
+    if (!uses_partials(deterministic) || rows <= 0 || !hidden_supported(hidden)) {
+        return 0;
+    }
+    return static_cast<size_t>(backward_blocks(rows, hidden)) * 2 * static_cast<size_t>(hidden)
+        * sizeof(float);
+}
+
+int rln_backward(
+    const float* grad_updated,
+    const void* grad_normalized,
+    int grad_normalized_dtype,
+    const float* updated,
+    const float* weight,
+    const float* mean,
+    const float* rstd,
+    const uint32_t* dropout_mask,
+    float* grad_x,
+    void* grad_branch,
+    int branch_dtype,
+    float* grad_weight,
+    float* grad_bias,
+    int64_t rows,
+    int64_t hidden,
+    double dropout_p,
+    int training,
+    int deterministic,
+    int accumulate_parameters,
+    void* workspace,
+    size_t workspace_bytes,
+    void* stream) {
+    rln::t_last_error.clear();
+    int status = check_common(rows, hidden, branch_dtype);
+    if (status != RLN_OK) {
+        return status;
+    }
+    if (!updated || !weight || !mean || !rstd || !grad_x || !grad_branch) {
+        return fail(RLN_ERR_INVALID, "backward tensors must not be null");
+    }
+    if (!valid_dtype(grad_normalized_dtype)) {
+        return fail(RLN_ERR_INVALID, "grad_normalized must use float16, bfloat16 or float32");
+    }
+    if ((grad_weight == nullptr) != (grad_bias == nullptr)) {
+        return fail(RLN_ERR_INVALID, "grad_weight and grad_bias must both be given or both be null");
+    }
+    DropoutConstants drop{};
+    status = dropout_constants(dropout_p, training, &drop);
+    if (status != RLN_OK) {
+        return status;
+    }
+    if (drop.active && !dropout_mask) {
+        return fail(RLN_ERR_INVALID, "dropout_mask must not be null when dropout is active");
+    }
+    const bool parameters = grad_weight != nullptr && grad_normalized != nullptr;
+    const bool partials = parameters && uses_partials(deterministic);
+    const size_t needed = partials ? rln_backward_workspace_bytes(rows, hidden, deterministic) : 0;
+    if (needed > 0) {
+        if (workspace == nullptr || workspace_bytes < needed) {
+            return fail(
+                RLN_ERR_INVALID,
+                "workspace too small: need %zu bytes, got %zu",
+                needed,
+                workspace == nullptr ? static_cast<size_t>(0) : workspace_bytes);
+        }
+        if (!aligned_to(workspace, 16)) {
+            return fail(RLN_ERR_INVALID, "workspace must be 16-byte aligned");
+        }
+    }
+
+    BackwardArgs a{};
+    a.grad_updated = grad_updated;
+    a.grad_normalized = grad_normalized;
+    a.updated = updated;
+    a.weight = weight;
+    a.mean = mean;
+    a.rstd = rstd;
+    a.mask = dropout_mask;
+    a.grad_x = grad_x;
+    a.grad_branch = grad_branch;
+    a.grad_weight = grad_weight;
+    a.grad_bias = grad_bias;
+    a.partials = static_cast<float*>(workspace);
+    a.rows = rows;
+    a.scale = drop.scale;
+    a.stream = static_cast<hipStream_t>(stream);
+    a.flags = (grad_updated ? kHasGradUpdated : 0)
+        | (grad_normalized ? kHasGradNormalized : 0)
+        | (drop.active ? kDropout : 0)
+        | (parameters ? kParameters : 0)
+        | (partials ? kPartials : 0);
+
+    if (parameters && !partials && !accumulate_parameters) {
+        rln_zero_parameters_kernel<<<dim3(static_cast<unsigned>((hidden + 255) / 256)), 256, 0, a.stream>>>(
+            grad_weight, grad_bias, static_cast<int>(hidden));
+        status = check_launch("rln_zero_parameters_kernel");
+        if (status != RLN_OK) {
+            return status;
+        }
+    }
+
+    const bool aligned = aligned_to(grad_updated, 16)
+        && aligned_to(grad_normalized, vector_alignment(grad_normalized_dtype))
+        && aligned_to(updated, 16) && aligned_to(weight, 16) && aligned_to(grad_x, 16)
+        && aligned_to(grad_branch, vector_alignment(branch_dtype));
+    switch (hidden) {
+        case 128: status = launch_backward_hidden<128>(a, branch_dtype, grad_normalized_dtype, aligned); break;
+        case 256: status = launch_backward_hidden<256>(a, branch_dtype, grad_normalized_dtype, aligned); break;
+        case 384: status = launch_backward_hidden<384>(a, branch_dtype, grad_normalized_dtype, aligned); break;
+        case 512: status = launch_backward_hidden<512>(a, branch_dtype, grad_normalized_dtype, aligned); break;
+        case 768: status = launch_backward_hidden<768>(a, branch_dtype, grad_normalized_dtype, aligned); break;
+        case 1024: status = launch_backward_hidden<1024>(a, branch_dtype, grad_normalized_dtype, aligned); break;
+        default:
+            return fail(RLN_ERR_UNSUPPORTED, "unsupported native hidden size: %lld", static_cast<long long>(hidden));
+    }
+    if (status != RLN_OK) {
+        return status;
+    }
+    if (partials) {
+        const int64_t groups = backward_blocks(rows, hidden);
+        const unsigned blocks = static_cast<unsigned>((2 * hidden + kWaveSize - 1) / kWaveSize);
+        rln_parameter_reduce_kernel<<<dim3(blocks), kReduceWaves * kWaveSize, 0, a.stream>>>(
+            a.partials, grad_weight, grad_bias, groups, static_cast<int>(hidden),
+            accumulate_parameters ? 1 : 0);
+        status = check_launch("rln_parameter_reduce_kernel");
+    }
+    return status;
+}
+
+uint64_t rln_philox_increment(int64_t hidden) {
+    (void)hidden;
+    return 4;
+}
+
+int64_t rln_mask_words(int64_t rows, int64_t hidden) {
+    if (rows <= 0 || hidden <= 0 || hidden % 32 != 0) {
+        return 0;
+    }
+    return rows * (hidden / 32);
+}
+
+int rln_hidden_supported(int64_t hidden) {
+    return hidden_supported(hidden) ? 1 : 0;
+}
+
+int rln_supported_hidden_sizes(int64_t* out, int capacity) {
+    const int count = static_cast<int>(sizeof(kSupportedHidden) / sizeof(kSupportedHidden[0]));
+    for (int index = 0; index < count && index < capacity && out != nullptr; ++index) {
+        out[index] = kSupportedHidden[index];
+    }
+    return count;
+}
+
+const char* rln_last_error(void) {
+    return rln::t_last_error.c_str();
+}
+
+const char* rln_target_arch(void) {
+    return "gfx950";
+}
+
+const char* rln_version(void) {
+    return "0.2.0";
+}
+
+}  // extern "C"

@@ -1,6 +1,7 @@
-// Fused residual-add + dropout + LayerNorm for MI355X (gfx950, CDNA4).
-//
-// Device kernels and the C ABI declared in include/rln.h. The operator is the
+// Fused residual-add + dropout + LayerNorm for MI355X (gfx950, CDNA4): the
+// device kernels and their launchers, shared by the per-hidden-size
+// translation units (rln_hidden.hip) and the C ABI (rln_api.hip, declared in
+// include/rln.h). The operator is the
 // one implemented by the reference's csrc/residual_layer_norm_kernel.hip
 // (forward :425-545, input backward :548-618, parameter backward :727-869);
 // the kernels here are organised for wave64 CDNA hardware instead:
@@ -42,12 +43,12 @@
 // This file is compiled with -ffp-contract=off so that none of these is
 // fused into an FMA; FMAs appear only where written explicitly.
 
+#ifndef RLN_DEVICE_H
+#define RLN_DEVICE_H
+
 #include <hip/hip_runtime.h>
 
-#include <cstdarg>
 #include <cstdint>
-#include <cstdio>
-#include <string>
 
 #include "rln.h"
 
@@ -65,11 +66,13 @@
 #ifndef RLN_ATOMIC_PARAMETERS
 #define RLN_ATOMIC_PARAMETERS 1
 #endif
-#ifndef RLN_FWD_PREFETCH
-#define RLN_FWD_PREFETCH 1
+// Launches over at least this many elements, with rows of at least
+// RLN_PACED_MIN_HIDDEN, walk their rows paced rather than with look-ahead.
+#ifndef RLN_PACED_ELEMENTS
+#define RLN_PACED_ELEMENTS (1ll << 23)
 #endif
-#ifndef RLN_BWD_PREFETCH
-#define RLN_BWD_PREFETCH 1
+#ifndef RLN_PACED_MIN_HIDDEN
+#define RLN_PACED_MIN_HIDDEN 256
 #endif
 #ifndef RLN_NT_LOADS
 #define RLN_NT_LOADS 1
@@ -78,15 +81,15 @@
 #define RLN_NT_STORES 1
 #endif
 
-namespace {
+namespace rln {
 
 constexpr int kWaveSize = 64;
 constexpr int kForwardThreads = 256;
 constexpr int kBackwardThreads = RLN_BWD_THREADS;
 constexpr int64_t kForwardMaxBlocks = RLN_FWD_MAX_BLOCKS;
 constexpr int64_t kBackwardMaxBlocks = RLN_BWD_MAX_BLOCKS;
-constexpr bool kForwardPrefetch = RLN_FWD_PREFETCH != 0;
-constexpr bool kBackwardPrefetch = RLN_BWD_PREFETCH != 0;
+constexpr int64_t kPacedElements = RLN_PACED_ELEMENTS;
+constexpr int64_t kPacedMinHidden = RLN_PACED_MIN_HIDDEN;
 static_assert(kBackwardThreads % kWaveSize == 0 && kBackwardThreads <= 1024, "backward block");
 
 constexpr int64_t kSupportedHidden[] = {128, 256, 384, 512, 768, 1024};
@@ -98,31 +101,11 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
 // ----------------------------------------------------------------------------
-// Error reporting.
-
-thread_local std::string t_last_error;
-
-int fail(int code, const char* format, ...) {
-    char buffer[512];
-    va_list args;
-    va_start(args, format);
-    vsnprintf(buffer, sizeof(buffer), format, args);
-    va_end(args);
-    t_last_error = buffer;
-    return code;
-}
-
-int check_launch(const char* what) {
-    const hipError_t status = hipGetLastError();
-    if (status != hipSuccess) {
-        return fail(
-            RLN_ERR_HIP,
-            "%s launch failed: %s",
-            what,
-            hipGetErrorString(status));
-    }
-    return RLN_OK;
-}
+// Error reporting (defined in rln_api.hip): `fail` records a message for
+// rln_last_error() and returns `code`; `check_launch` turns a launch error
+// into RLN_ERR_HIP.
+int fail(int code, const char* format, ...);
+int check_launch(const char* what);
 
 // ----------------------------------------------------------------------------
 // Row geometry for a hidden size H.
@@ -138,14 +121,14 @@ struct Geometry {
     static_assert(kVectors % kLanes == 0, "row must split evenly over lanes");
 };
 
-int64_t rows_per_wave(int64_t hidden) {
+inline int64_t rows_per_wave(int64_t hidden) {
     return ((hidden / 4) % kWaveSize == 0) ? 1 : 2;
 }
 
 // Blocks for a launch over `rows`: enough for `groups_per_wave` row groups
 // per wave (a group = the rows one wave handles at once), capped; a function
 // of (rows, hidden) only.
-int64_t launch_blocks(int64_t rows, int64_t hidden, int threads, int64_t cap,
+inline int64_t launch_blocks(int64_t rows, int64_t hidden, int threads, int64_t cap,
                       int64_t groups_per_wave) {
     const int64_t groups = (rows + rows_per_wave(hidden) - 1) / rows_per_wave(hidden);
     const int64_t waves = (groups + groups_per_wave - 1) / groups_per_wave;
@@ -157,17 +140,24 @@ int64_t launch_blocks(int64_t rows, int64_t hidden, int threads, int64_t cap,
 // The forward gives each wave at least two row groups so that its
 // look-ahead load overlaps a row's computation; with 256-thread blocks and
 // ~100 VGPRs per lane the cap of 2048 blocks is two waves of residency.
-int64_t forward_blocks(int64_t rows, int64_t hidden) {
+inline int64_t forward_blocks(int64_t rows, int64_t hidden) {
     return launch_blocks(rows, hidden, kForwardThreads, kForwardMaxBlocks, 2);
 }
 
 // The backward's grid is also the number of weight/bias partials: 256
 // blocks of 8 waves, one block per CU.
-int64_t backward_blocks(int64_t rows, int64_t hidden) {
+inline int64_t backward_blocks(int64_t rows, int64_t hidden) {
     return launch_blocks(rows, hidden, kBackwardThreads, kBackwardMaxBlocks, 1);
 }
 
-bool hidden_supported(int64_t hidden) {
+// 1 if a launch over rows x hidden walks its rows paced (measured on MI355X:
+// faster from about 8 M elements at hidden >= 256, neutral below, slower at
+// C1-sized launches), 0 for look-ahead.
+inline int paced_schedule(int64_t rows, int64_t hidden) {
+    return hidden >= kPacedMinHidden && rows * hidden >= kPacedElements ? 1 : 0;
+}
+
+inline bool hidden_supported(int64_t hidden) {
     for (const int64_t value : kSupportedHidden) {
         if (value == hidden) {
             return true;
@@ -344,6 +334,29 @@ __device__ __forceinline__ f32x4 load_convert4(const T* __restrict__ pointer) {
     }
 }
 
+// Four consecutive elements of type T in their storage type, unconverted.
+// Row loads keep this form so that no arithmetic (and hence no wait for the
+// load) happens until the row is processed.
+template <typename T, bool Aligned>
+__device__ __forceinline__ typename Vector4<T>::type load_raw4(const T* __restrict__ pointer) {
+    using Raw = typename Vector4<T>::type;
+    if constexpr (Aligned) {
+        return stream_load(reinterpret_cast<const Raw*>(pointer));
+    } else {
+        Raw raw;
+        raw.x = stream_load(pointer);
+        raw.y = stream_load(pointer + 1);
+        raw.z = stream_load(pointer + 2);
+        raw.w = stream_load(pointer + 3);
+        return raw;
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ f32x4 widen4(typename Vector4<T>::type raw) {
+    return __builtin_convertvector(raw, f32x4);
+}
+
 // Stores four fp32 values as type T; narrowing rounds to nearest even.
 template <typename T, bool Aligned>
 __device__ __forceinline__ void store_convert4(T* __restrict__ pointer, f32x4 value) {
@@ -356,32 +369,6 @@ __device__ __forceinline__ void store_convert4(T* __restrict__ pointer, f32x4 va
         stream_store(static_cast<T>(packed.y), pointer + 1);
         stream_store(static_cast<T>(packed.z), pointer + 2);
         stream_store(static_cast<T>(packed.w), pointer + 3);
-    }
-}
-
-// The same with the element type chosen at run time (an rln_dtype value,
-// uniform across the launch).
-template <bool Aligned>
-__device__ __forceinline__ f32x4 load_any4(const void* __restrict__ base, int64_t index,
-                                           int dtype) {
-    if (dtype == RLN_DTYPE_F16) {
-        return load_convert4<half_t, Aligned>(static_cast<const half_t*>(base) + index);
-    }
-    if (dtype == RLN_DTYPE_BF16) {
-        return load_convert4<bf16_t, Aligned>(static_cast<const bf16_t*>(base) + index);
-    }
-    return load_convert4<float, Aligned>(static_cast<const float*>(base) + index);
-}
-
-template <bool Aligned>
-__device__ __forceinline__ void store_any4(void* __restrict__ base, int64_t index, f32x4 value,
-                                           int dtype) {
-    if (dtype == RLN_DTYPE_F16) {
-        store_convert4<half_t, Aligned>(static_cast<half_t*>(base) + index, value);
-    } else if (dtype == RLN_DTYPE_BF16) {
-        store_convert4<bf16_t, Aligned>(static_cast<bf16_t*>(base) + index, value);
-    } else {
-        store_convert4<float, Aligned>(static_cast<float*>(base) + index, value);
     }
 }
 
@@ -402,14 +389,15 @@ __device__ __forceinline__ float sum4(f32x4 value) {
 // ----------------------------------------------------------------------------
 // Forward kernel.
 
-// The global values the forward reads for one row, held in registers.
-template <int V>
+// The global values the forward reads for one row, held in registers in
+// their storage types.
+template <int V, typename B>
 struct ForwardRow {
     f32x4 x[V];
-    f32x4 branch[V];
+    typename Vector4<B>::type branch[V];
 };
 
-template <int H, typename B, bool Aligned>
+template <int H, typename B, typename N, bool Aligned>
 __global__ __launch_bounds__(kForwardThreads)
 void rln_forward_kernel(
     const float* __restrict__ x,
@@ -417,8 +405,7 @@ void rln_forward_kernel(
     const float* __restrict__ weight,
     const float* __restrict__ bias,
     float* __restrict__ updated,
-    void* __restrict__ normalized,
-    int normalized_dtype,
+    N* __restrict__ normalized,
     float* __restrict__ mean_out,
     float* __restrict__ rstd_out,
     uint32_t* __restrict__ mask,
@@ -427,7 +414,8 @@ void rln_forward_kernel(
     int dropout,
     float scale,
     uint32_t threshold,
-    PhiloxArgs philox) {
+    PhiloxArgs philox,
+    int paced) {
     using G = Geometry<H>;
     constexpr int L = G::kLanes;
     constexpr int V = G::kV;
@@ -462,30 +450,33 @@ void rln_forward_kernel(
         position = offset / 4;
     }
 
-    // Loads x and the branch of one row; rows past the end read nothing.
-    auto load_row = [&](ForwardRow<V>& r, int64_t row) {
-        const bool valid = row < rows;
-        const int64_t base = row * H;
+    // Loads x and the branch of one row. The loads are unconditional (a
+    // half-wave row past the end reads the last row instead and discards it),
+    // so the compiler can count them and wait for exactly the ones a
+    // computation needs; a load under a branch makes it wait for all.
+    auto load_row = [&](ForwardRow<V, B>& r, int64_t row, bool wait_slices) {
+        const int64_t source = row < rows ? row : rows - 1;
+        const float* x_row = x + source * H;
+        const B* branch_row = branch + source * H;
 #pragma unroll
         for (int v = 0; v < V; ++v) {
             const int column = (v * L + l) * 4;
-            r.x[v] = zero4();
-            r.branch[v] = zero4();
-            if (valid) {
-                r.x[v] = load4<Aligned>(x + base + column);
-                r.branch[v] = load_convert4<B, Aligned>(branch + base + column);
+            r.x[v] = load4<Aligned>(x_row + column);
+            r.branch[v] = load_raw4<B, Aligned>(branch_row + column);
+            if (wait_slices) {
+                __builtin_amdgcn_s_waitcnt(0);
             }
         }
     };
 
-    auto process_row = [&](const ForwardRow<V>& r, int64_t row) {
+    auto process_row = [&](const ForwardRow<V, B>& r, int64_t row) {
         const bool valid = row < rows;
         const int64_t base = row * H;
         f32x4 u[V];
         uint32_t keep_bits[V];
 #pragma unroll
         for (int v = 0; v < V; ++v) {
-            f32x4 bv = r.branch[v];
+            f32x4 bv = widen4<B>(r.branch[v]);
             keep_bits[v] = 0;
             if (dropout) {
                 const uint64_t group = static_cast<uint64_t>(row) * (H / 4) + (v * L + l);
@@ -553,42 +544,51 @@ void rln_forward_kernel(
                     __builtin_fmaf(u[v].y * rstd, w[v].y, b[v].y),
                     __builtin_fmaf(u[v].z * rstd, w[v].z, b[v].z),
                     __builtin_fmaf(u[v].w * rstd, w[v].w, b[v].w)};
-                store_any4<Aligned>(normalized, base + column, y, normalized_dtype);
+                store_convert4<N, Aligned>(normalized + base + column, y);
             }
         }
     };
 
-    // One row of look-ahead: the next row's loads are in flight while the
-    // current row is computed and stored.
+    // Two schedules. Look-ahead (small launches): the next row's loads are
+    // in flight while the current row is computed and stored. Paced (large
+    // launches): a row is loaded after the previous one is stored, one
+    // 4-column slice at a time, each waited for (with every earlier store of
+    // the wave), which keeps fewer reads and writes interleaved per wave and
+    // streams large tensors faster. The last row of a wave is peeled off, so
+    // no load reaches past the wave's rows.
     const int64_t stride = wave_count * G::kRowsPerWave;
     int64_t first = wave * G::kRowsPerWave;
-    ForwardRow<V> current;
-    if constexpr (kForwardPrefetch) {
-        load_row(current, first + sub);
+    if (first >= rows) {
+        return;
     }
-    for (; first < rows; first += stride) {
-        if constexpr (kForwardPrefetch) {
-            ForwardRow<V> next;
-            load_row(next, first + stride + sub);
+    ForwardRow<V, B> current;
+    load_row(current, first + sub, false);
+    if (paced) {
+        for (; first + stride < rows; first += stride) {
+            process_row(current, first + sub);
+            load_row(current, first + stride + sub, true);
+        }
+    } else {
+        for (; first + stride < rows; first += stride) {
+            ForwardRow<V, B> next;
+            load_row(next, first + stride + sub, false);
             process_row(current, first + sub);
             current = next;
-        } else {
-            load_row(current, first + sub);
-            process_row(current, first + sub);
         }
     }
+    process_row(current, first + sub);
 }
 
 // ----------------------------------------------------------------------------
 // Backward kernel: input gradients plus per-block weight/bias partial sums.
 
 // Every global value the backward reads for one row, held in registers.
-template <int V>
+template <int V, typename GY>
 struct BackwardRow {
     f32x4 u[V];
-    f32x4 gy[V];
+    typename Vector4<GY>::type gy[V];  // storage type, widened when processed
     f32x4 gu[V];
-    uint32_t keep_bits[V];
+    uint32_t mask_word[V];  // whole word; the lane's nibble is taken when processed
     float mean;
     float rstd;
 };
@@ -601,12 +601,11 @@ enum BackwardFlags : int {
     kPartials = 16,  // write per-block partials (else fp32 atomics)
 };
 
-template <int H, typename B, bool Aligned>
+template <int H, typename B, typename GY, bool Aligned>
 __global__ __launch_bounds__(kBackwardThreads)
 void rln_backward_kernel(
     const float* __restrict__ grad_updated,
-    const void* __restrict__ grad_normalized,
-    int grad_normalized_dtype,
+    const GY* __restrict__ grad_normalized,
     const float* __restrict__ updated,
     const float* __restrict__ weight,
     const float* __restrict__ mean_in,
@@ -619,7 +618,8 @@ void rln_backward_kernel(
     float* __restrict__ partials,
     int64_t rows,
     int flags,
-    float scale) {
+    float scale,
+    int paced) {
     using G = Geometry<H>;
     constexpr int L = G::kLanes;
     constexpr int V = G::kV;
@@ -648,47 +648,50 @@ void rln_backward_kernel(
         acc_b[v] = zero4();
     }
 
-    // Loads every global value of one row into registers; rows past the end
-    // read nothing and hold zeros.
-    auto load_row = [&](BackwardRow<V>& r, int64_t row) {
-        const bool valid = row < rows;
-        const int64_t base = row * H;
-        r.mean = valid ? mean_in[row] : 0.0f;
-        r.rstd = valid ? rstd_in[row] : 0.0f;
+    // Loads every global value of one row. The loads are unconditional, so
+    // the compiler can count them and wait for exactly the ones a computation
+    // needs (a load under a branch makes it wait for all): an absent input
+    // reads the row of `updated` in its place, and a half-wave row past the
+    // end reads the last row; process_row discards what it read.
+    auto load_row = [&](BackwardRow<V, GY>& r, int64_t row, bool wait_slices) {
+        const int64_t source = row < rows ? row : rows - 1;
+        const int64_t base = source * H;
+        const float* u_row = updated + base;
+        const GY* gy_row = has_gy ? grad_normalized + base : reinterpret_cast<const GY*>(u_row);
+        const float* gu_row = has_gu ? grad_updated + base : u_row;
+        const uint32_t* mask_row = dropout ? mask + source * G::kMaskWords
+                                           : reinterpret_cast<const uint32_t*>(u_row);
+        r.mean = mean_in[source];
+        r.rstd = rstd_in[source];
 #pragma unroll
         for (int v = 0; v < V; ++v) {
             const int column = (v * L + l) * 4;
-            r.u[v] = zero4();
-            r.gy[v] = zero4();
-            r.gu[v] = zero4();
-            r.keep_bits[v] = 0;
-            if (valid) {
-                r.u[v] = load4<Aligned>(updated + base + column);
-                if (has_gy) {
-                    r.gy[v] = load_any4<Aligned>(grad_normalized, base + column, grad_normalized_dtype);
-                }
-                if (has_gu) {
-                    r.gu[v] = load4<Aligned>(grad_updated + base + column);
-                }
-                if (dropout) {
-                    r.keep_bits[v] =
-                        mask[row * G::kMaskWords + (v * L + l) / 8] >> (4 * (l & 7));
-                }
+            r.u[v] = load4<Aligned>(u_row + column);
+            r.gy[v] = load_raw4<GY, Aligned>(gy_row + column);
+            r.gu[v] = load4<Aligned>(gu_row + column);
+            r.mask_word[v] = mask_row[(v * L + l) / 8];
+            if (wait_slices) {
+                __builtin_amdgcn_s_waitcnt(0);
             }
         }
     };
 
     // Input gradients of one row and its contribution to the parameter sums.
-    auto process_row = [&](const BackwardRow<V>& r, int64_t row) {
+    auto process_row = [&](const BackwardRow<V, GY>& r, int64_t row) {
         const bool valid = row < rows;
         const int64_t base = row * H;
         f32x4 xhat[V];
+        f32x4 gy[V];
         float sum_q = 0.0f;
         float sum_qx = 0.0f;
+        // Inputs that were not given, and every input of a row past the end,
+        // count as zero.
+        const bool use_gy = has_gy && valid;
 #pragma unroll
         for (int v = 0; v < V; ++v) {
+            gy[v] = use_gy ? widen4<GY>(r.gy[v]) : zero4();
             xhat[v] = (r.u[v] - r.mean) * r.rstd;
-            const f32x4 q = r.gy[v] * w[v];
+            const f32x4 q = gy[v] * w[v];
             sum_q += sum4(q);
             sum_qx += (q.x * xhat[v].x + q.y * xhat[v].y)
                 + (q.z * xhat[v].z + q.w * xhat[v].w);
@@ -705,14 +708,14 @@ void rln_backward_kernel(
 #pragma unroll
             for (int v = 0; v < V; ++v) {
                 const int column = (v * L + l) * 4;
-                f32x4 g = r.gu[v];
+                f32x4 g = has_gu ? r.gu[v] : zero4();
                 if (has_gy) {
-                    const f32x4 q = r.gy[v] * w[v];
+                    const f32x4 q = gy[v] * w[v];
                     g = g + r.rstd * ((q - mean_q) - xhat[v] * mean_qx);
                 }
                 store4<Aligned>(grad_x + base + column, g);
                 if (dropout) {
-                    const uint32_t bits = r.keep_bits[v];
+                    const uint32_t bits = r.mask_word[v] >> (4 * (l & 7));
                     g.x = g.x * (static_cast<float>(bits & 1u) * scale);
                     g.y = g.y * (static_cast<float>((bits >> 1) & 1u) * scale);
                     g.z = g.z * (static_cast<float>((bits >> 2) & 1u) * scale);
@@ -725,33 +728,41 @@ void rln_backward_kernel(
         if (parameters) {
 #pragma unroll
             for (int v = 0; v < V; ++v) {
-                acc_w[v].x = __builtin_fmaf(r.gy[v].x, xhat[v].x, acc_w[v].x);
-                acc_w[v].y = __builtin_fmaf(r.gy[v].y, xhat[v].y, acc_w[v].y);
-                acc_w[v].z = __builtin_fmaf(r.gy[v].z, xhat[v].z, acc_w[v].z);
-                acc_w[v].w = __builtin_fmaf(r.gy[v].w, xhat[v].w, acc_w[v].w);
-                acc_b[v] = acc_b[v] + r.gy[v];
+                acc_w[v].x = __builtin_fmaf(gy[v].x, xhat[v].x, acc_w[v].x);
+                acc_w[v].y = __builtin_fmaf(gy[v].y, xhat[v].y, acc_w[v].y);
+                acc_w[v].z = __builtin_fmaf(gy[v].z, xhat[v].z, acc_w[v].z);
+                acc_w[v].w = __builtin_fmaf(gy[v].w, xhat[v].w, acc_w[v].w);
+                acc_b[v] = acc_b[v] + gy[v];
             }
         }
     };
 
-    // Each wave walks its rows with the next row's loads in flight while the
-    // current row is reduced and stored (one row of look-ahead).
+    // Each wave walks its rows under one of two schedules: look-ahead (the
+    // next row's loads in flight while the current row is reduced and stored;
+    // small launches) or paced (a row loaded after the previous one is
+    // stored, one 4-column slice at a time, each waited for; large launches,
+    // where fewer interleaved reads and writes per wave stream faster). The
+    // last row of a wave is peeled off, so no load reaches past the wave's
+    // rows. A wave without rows still takes part in the block's combine.
     const int64_t stride = wave_count * G::kRowsPerWave;
     int64_t first = wave * G::kRowsPerWave;
-    BackwardRow<V> current;
-    if constexpr (kBackwardPrefetch) {
-        load_row(current, first + sub);
-    }
-    for (; first < rows; first += stride) {
-        if constexpr (kBackwardPrefetch) {
-            BackwardRow<V> next;
-            load_row(next, first + stride + sub);
-            process_row(current, first + sub);
-            current = next;
+    if (first < rows) {
+        BackwardRow<V, GY> current;
+        load_row(current, first + sub, false);
+        if (paced) {
+            for (; first + stride < rows; first += stride) {
+                process_row(current, first + sub);
+                load_row(current, first + stride + sub, true);
+            }
         } else {
-            load_row(current, first + sub);
-            process_row(current, first + sub);
+            for (; first + stride < rows; first += stride) {
+                BackwardRow<V, GY> next;
+                load_row(next, first + stride + sub, false);
+                process_row(current, first + sub);
+                current = next;
+            }
         }
+        process_row(current, first + sub);
     }
 
     if (!parameters) {
@@ -791,61 +802,6 @@ void rln_backward_kernel(
     }
 }
 
-// Fixed-order reduction of per-block partials [groups][2][H] into
-// grad_weight / grad_bias. Block = 16 waves over 64 consecutive entries of the
-// flattened [2][H] output; wave k sums its contiguous share of the groups in
-// ascending order, then wave sums are added in ascending wave order.
-constexpr int kReduceWaves = 16;
-
-__global__ __launch_bounds__(kReduceWaves * kWaveSize)
-void rln_parameter_reduce_kernel(
-    const float* __restrict__ partials,
-    float* __restrict__ grad_weight,
-    float* __restrict__ grad_bias,
-    int64_t groups,
-    int hidden,
-    int accumulate) {
-    __shared__ float wave_totals[kReduceWaves][kWaveSize];
-    const int lane = threadIdx.x & (kWaveSize - 1);
-    const int wave = threadIdx.x / kWaveSize;
-    const int entry = blockIdx.x * kWaveSize + lane;  // index into [2][H]
-    const bool active = entry < 2 * hidden;
-    const int64_t share = (groups + kReduceWaves - 1) / kReduceWaves;
-    const int64_t begin = wave * share;
-    const int64_t end = begin + share < groups ? begin + share : groups;
-    const int which = active ? entry / hidden : 0;
-    const int column = active ? entry % hidden : 0;
-    float total = 0.0f;
-    if (active) {
-        const float* source = partials + static_cast<int64_t>(which) * hidden + column;
-        const int64_t stride = 2 * static_cast<int64_t>(hidden);
-#pragma unroll 16
-        for (int64_t group = begin; group < end; ++group) {
-            total += source[group * stride];
-        }
-    }
-    wave_totals[wave][lane] = total;
-    __syncthreads();
-    if (wave == 0 && active) {
-        float sum = 0.0f;
-#pragma unroll
-        for (int source = 0; source < kReduceWaves; ++source) {
-            sum += wave_totals[source][lane];
-        }
-        float* target = (which ? grad_bias : grad_weight) + column;
-        *target = accumulate ? *target + sum : sum;
-    }
-}
-
-__global__ __launch_bounds__(256)
-void rln_zero_parameters_kernel(float* __restrict__ grad_weight, float* __restrict__ grad_bias, int hidden) {
-    const int index = blockIdx.x * blockDim.x + threadIdx.x;
-    if (index < hidden) {
-        grad_weight[index] = 0.0f;
-        grad_bias[index] = 0.0f;
-    }
-}
-
 // ----------------------------------------------------------------------------
 // Host-side launch helpers.
 
@@ -856,7 +812,6 @@ struct ForwardArgs {
     const float* bias;
     float* updated;
     void* normalized;
-    int normalized_dtype;
     float* mean;
     float* rstd;
     uint32_t* mask;
@@ -869,49 +824,9 @@ struct ForwardArgs {
     hipStream_t stream;
 };
 
-template <int H, typename B, bool Aligned>
-int launch_forward(const ForwardArgs& a) {
-    const dim3 grid(static_cast<unsigned>(forward_blocks(a.rows, H)));
-    rln_forward_kernel<H, B, Aligned><<<grid, kForwardThreads, 0, a.stream>>>(
-        a.x,
-        static_cast<const B*>(a.branch),
-        a.weight,
-        a.bias,
-        a.updated,
-        a.normalized,
-        a.normalized_dtype,
-        a.mean,
-        a.rstd,
-        a.mask,
-        a.rows,
-        a.eps,
-        a.dropout,
-        a.scale,
-        a.threshold,
-        a.philox);
-    return check_launch("rln_forward_kernel");
-}
-
-template <int H, typename B>
-int launch_forward_branch(const ForwardArgs& a, bool aligned) {
-    return aligned ? launch_forward<H, B, true>(a) : launch_forward<H, B, false>(a);
-}
-
-template <int H>
-int launch_forward_hidden(const ForwardArgs& a, int branch_dtype, bool aligned) {
-    if (branch_dtype == RLN_DTYPE_F16) {
-        return launch_forward_branch<H, half_t>(a, aligned);
-    }
-    if (branch_dtype == RLN_DTYPE_BF16) {
-        return launch_forward_branch<H, bf16_t>(a, aligned);
-    }
-    return launch_forward_branch<H, float>(a, aligned);
-}
-
 struct BackwardArgs {
     const float* grad_updated;
     const void* grad_normalized;
-    int grad_normalized_dtype;
     const float* updated;
     const float* weight;
     const float* mean;
@@ -928,13 +843,35 @@ struct BackwardArgs {
     hipStream_t stream;
 };
 
-template <int H, typename B, bool Aligned>
+template <int H, typename B, typename N, bool Aligned>
+int launch_forward(const ForwardArgs& a) {
+    const dim3 grid(static_cast<unsigned>(forward_blocks(a.rows, H)));
+    rln_forward_kernel<H, B, N, Aligned><<<grid, kForwardThreads, 0, a.stream>>>(
+        a.x,
+        static_cast<const B*>(a.branch),
+        a.weight,
+        a.bias,
+        a.updated,
+        static_cast<N*>(a.normalized),
+        a.mean,
+        a.rstd,
+        a.mask,
+        a.rows,
+        a.eps,
+        a.dropout,
+        a.scale,
+        a.threshold,
+        a.philox,
+        paced_schedule(a.rows, H));
+    return check_launch("rln_forward_kernel");
+}
+
+template <int H, typename B, typename GY, bool Aligned>
 int launch_backward(const BackwardArgs& a) {
     const dim3 grid(static_cast<unsigned>(backward_blocks(a.rows, H)));
-    rln_backward_kernel<H, B, Aligned><<<grid, kBackwardThreads, 0, a.stream>>>(
+    rln_backward_kernel<H, B, GY, Aligned><<<grid, kBackwardThreads, 0, a.stream>>>(
         a.grad_updated,
-        a.grad_normalized,
-        a.grad_normalized_dtype,
+        static_cast<const GY*>(a.grad_normalized),
         a.updated,
         a.weight,
         a.mean,
@@ -947,341 +884,52 @@ int launch_backward(const BackwardArgs& a) {
         a.partials,
         a.rows,
         a.flags,
-        a.scale);
+        a.scale,
+        paced_schedule(a.rows, H));
     return check_launch("rln_backward_kernel");
 }
 
-template <int H, typename B>
-int launch_backward_branch(const BackwardArgs& a, bool aligned) {
-    return aligned ? launch_backward<H, B, true>(a) : launch_backward<H, B, false>(a);
+// Calls `launch.template operator()<T>()` with T the element type of `dtype`.
+template <typename Launch>
+int with_dtype(int dtype, Launch&& launch) {
+    if (dtype == RLN_DTYPE_F16) {
+        return launch.template operator()<half_t>();
+    }
+    if (dtype == RLN_DTYPE_BF16) {
+        return launch.template operator()<bf16_t>();
+    }
+    return launch.template operator()<float>();
+}
+
+// Every (branch, normalized, alignment) instantiation for one hidden size;
+// explicitly instantiated once per H in rln_hidden.hip.
+template <int H>
+int launch_forward_hidden(const ForwardArgs& a, int branch_dtype, int normalized_dtype,
+                          bool aligned) {
+    return with_dtype(branch_dtype, [&]<typename B>() {
+        return with_dtype(normalized_dtype, [&]<typename N>() {
+            return aligned ? launch_forward<H, B, N, true>(a) : launch_forward<H, B, N, false>(a);
+        });
+    });
 }
 
 template <int H>
-int launch_backward_hidden(const BackwardArgs& a, int branch_dtype, bool aligned) {
-    if (branch_dtype == RLN_DTYPE_F16) {
-        return launch_backward_branch<H, half_t>(a, aligned);
-    }
-    if (branch_dtype == RLN_DTYPE_BF16) {
-        return launch_backward_branch<H, bf16_t>(a, aligned);
-    }
-    return launch_backward_branch<H, float>(a, aligned);
+int launch_backward_hidden(const BackwardArgs& a, int branch_dtype, int grad_normalized_dtype,
+                           bool aligned) {
+    return with_dtype(branch_dtype, [&]<typename B>() {
+        return with_dtype(grad_normalized_dtype, [&]<typename GY>() {
+            return aligned ? launch_backward<H, B, GY, true>(a)
+                           : launch_backward<H, B, GY, false>(a);
+        });
+    });
 }
 
-bool aligned_to(const void* pointer, uintptr_t alignment) {
-    return pointer == nullptr || (reinterpret_cast<uintptr_t>(pointer) & (alignment - 1)) == 0;
-}
+#define RLN_FOR_EACH_HIDDEN(X) X(128) X(256) X(384) X(512) X(768) X(1024)
 
-// Mirrors the reference's conversion of the double probability
-// (csrc/residual_layer_norm_kernel.hip:893-899, :1883-1886).
-struct DropoutConstants {
-    bool active;
-    float scale;
-    uint32_t threshold;
-};
+#define RLN_DECLARE_HIDDEN(H)                                                            \
+    extern template int launch_forward_hidden<H>(const ForwardArgs&, int, int, bool);    \
+    extern template int launch_backward_hidden<H>(const BackwardArgs&, int, int, bool);
 
-int dropout_constants(double dropout_p, int training, DropoutConstants* out) {
-    if (!(dropout_p >= 0.0 && dropout_p < 1.0)) {
-        return fail(RLN_ERR_INVALID, "dropout_p must be in [0, 1)");
-    }
-    const float p = static_cast<float>(dropout_p);
-    out->active = training && dropout_p > 0.0;
-    if (out->active && !(p < 1.0f)) {
-        return fail(RLN_ERR_INVALID, "dropout_p must be in [0, 1)");
-    }
-    out->scale = out->active ? 1.0f / (1.0f - p) : 1.0f;
-    out->threshold = out->active
-        ? static_cast<uint32_t>(static_cast<double>(p) * 4294967296.0)
-        : 0u;
-    return RLN_OK;
-}
+}  // namespace rln
 
-bool valid_dtype(int dtype) {
-    return dtype == RLN_DTYPE_F32 || dtype == RLN_DTYPE_F16 || dtype == RLN_DTYPE_BF16;
-}
-
-// Alignment of one four-element vector of `dtype`.
-uintptr_t vector_alignment(int dtype) {
-    return dtype == RLN_DTYPE_F32 ? 16 : 8;
-}
-
-int check_common(int64_t rows, int64_t hidden, int branch_dtype) {
-    if (rows <= 0) {
-        return fail(RLN_ERR_INVALID, "empty tensors are unsupported");
-    }
-    if (!hidden_supported(hidden)) {
-        return fail(
-            RLN_ERR_UNSUPPORTED,
-            "unsupported native hidden size: %lld",
-            static_cast<long long>(hidden));
-    }
-    if (!valid_dtype(branch_dtype)) {
-        return fail(RLN_ERR_INVALID, "branch must use float16, bfloat16 or float32");
-    }
-    if (rows > (INT64_MAX / hidden)) {
-        return fail(RLN_ERR_INVALID, "rows * hidden overflows int64");
-    }
-    return RLN_OK;
-}
-
-// Whether the parameter gradients of this call go through per-block partials
-// (and therefore the workspace and the reduce kernel).
-bool uses_partials(int deterministic) {
-    return deterministic || !RLN_ATOMIC_PARAMETERS;
-}
-
-}  // namespace
-
-// ----------------------------------------------------------------------------
-// C ABI.
-
-extern "C" {
-
-int rln_forward(
-    const float* x,
-    const void* branch,
-    int branch_dtype,
-    const float* weight,
-    const float* bias,
-    float* updated,
-    void* normalized,
-    int normalized_dtype,
-    float* mean,
-    float* rstd,
-    uint32_t* dropout_mask,
-    int64_t rows,
-    int64_t hidden,
-    double dropout_p,
-    double eps,
-    int training,
-    const rln_philox_t* philox,
-    void* stream) {
-    t_last_error.clear();
-    int status = check_common(rows, hidden, branch_dtype);
-    if (status != RLN_OK) {
-        return status;
-    }
-    if (!valid_dtype(normalized_dtype)) {
-        return fail(RLN_ERR_INVALID, "normalized must use float16, bfloat16 or float32");
-    }
-    if (!x || !branch || !weight || !bias || !updated || !normalized || !mean || !rstd) {
-        return fail(RLN_ERR_INVALID, "forward tensors must not be null");
-    }
-    if (!(eps > 0.0)) {
-        return fail(RLN_ERR_INVALID, "eps must be positive");
-    }
-    DropoutConstants drop{};
-    status = dropout_constants(dropout_p, training, &drop);
-    if (status != RLN_OK) {
-        return status;
-    }
-    ForwardArgs a{};
-    a.x = x;
-    a.branch = branch;
-    a.weight = weight;
-    a.bias = bias;
-    a.updated = updated;
-    a.normalized = normalized;
-    a.normalized_dtype = normalized_dtype;
-    a.mean = mean;
-    a.rstd = rstd;
-    a.mask = dropout_mask;
-    a.rows = rows;
-    a.eps = static_cast<float>(eps);
-    a.dropout = drop.active ? 1 : 0;
-    a.scale = drop.scale;
-    a.threshold = drop.threshold;
-    a.stream = static_cast<hipStream_t>(stream);
-    if (drop.active) {
-        if (!dropout_mask) {
-            return fail(RLN_ERR_INVALID, "dropout_mask must not be null when dropout is active");
-        }
-        if (!philox) {
-            return fail(RLN_ERR_INVALID, "philox must not be null when dropout is active");
-        }
-        a.philox.seed = philox->seed;
-        a.philox.offset = philox->offset;
-        a.philox.seed_ptr = philox->seed_ptr;
-        a.philox.offset_ptr = philox->offset_ptr;
-    }
-    const bool aligned = aligned_to(x, 16) && aligned_to(weight, 16) && aligned_to(bias, 16)
-        && aligned_to(updated, 16)
-        && aligned_to(normalized, vector_alignment(normalized_dtype))
-        && aligned_to(branch, vector_alignment(branch_dtype));
-    switch (hidden) {
-        case 128: return launch_forward_hidden<128>(a, branch_dtype, aligned);
-        case 256: return launch_forward_hidden<256>(a, branch_dtype, aligned);
-        case 384: return launch_forward_hidden<384>(a, branch_dtype, aligned);
-        case 512: return launch_forward_hidden<512>(a, branch_dtype, aligned);
-        case 768: return launch_forward_hidden<768>(a, branch_dtype, aligned);
-        case 1024: return launch_forward_hidden<1024>(a, branch_dtype, aligned);
-        default: break;
-    }
-    return fail(RLN_ERR_UNSUPPORTED, "unsupported native hidden size: %lld", static_cast<long long>(hidden));
-}
-
-size_t rln_backward_workspace_bytes(int64_t rows, int64_t hidden, int deterministic) {
-    if (!uses_partials(deterministic) || rows <= 0 || !hidden_supported(hidden)) {
-        return 0;
-    }
-    return static_cast<size_t>(backward_blocks(rows, hidden)) * 2 * static_cast<size_t>(hidden)
-        * sizeof(float);
-}
-
-int rln_backward(
-    const float* grad_updated,
-    const void* grad_normalized,
-    int grad_normalized_dtype,
-    const float* updated,
-    const float* weight,
-    const float* mean,
-    const float* rstd,
-    const uint32_t* dropout_mask,
-    float* grad_x,
-    void* grad_branch,
-    int branch_dtype,
-    float* grad_weight,
-    float* grad_bias,
-    int64_t rows,
-    int64_t hidden,
-    double dropout_p,
-    int training,
-    int deterministic,
-    int accumulate_parameters,
-    void* workspace,
-    size_t workspace_bytes,
-    void* stream) {
-    t_last_error.clear();
-    int status = check_common(rows, hidden, branch_dtype);
-    if (status != RLN_OK) {
-        return status;
-    }
-    if (!updated || !weight || !mean || !rstd || !grad_x || !grad_branch) {
-        return fail(RLN_ERR_INVALID, "backward tensors must not be null");
-    }
-    if (!valid_dtype(grad_normalized_dtype)) {
-        return fail(RLN_ERR_INVALID, "grad_normalized must use float16, bfloat16 or float32");
-    }
-    if ((grad_weight == nullptr) != (grad_bias == nullptr)) {
-        return fail(RLN_ERR_INVALID, "grad_weight and grad_bias must both be given or both be null");
-    }
-    DropoutConstants drop{};
-    status = dropout_constants(dropout_p, training, &drop);
-    if (status != RLN_OK) {
-        return status;
-    }
-    if (drop.active && !dropout_mask) {
-        return fail(RLN_ERR_INVALID, "dropout_mask must not be null when dropout is active");
-    }
-    const bool parameters = grad_weight != nullptr && grad_normalized != nullptr;
-    const bool partials = parameters && uses_partials(deterministic);
-    const size_t needed = partials ? rln_backward_workspace_bytes(rows, hidden, deterministic) : 0;
-    if (needed > 0) {
-        if (workspace == nullptr || workspace_bytes < needed) {
-            return fail(
-                RLN_ERR_INVALID,
-                "workspace too small: need %zu bytes, got %zu",
-                needed,
-                workspace == nullptr ? static_cast<size_t>(0) : workspace_bytes);
-        }
-        if (!aligned_to(workspace, 16)) {
-            return fail(RLN_ERR_INVALID, "workspace must be 16-byte aligned");
-        }
-    }
-
-    BackwardArgs a{};
-    a.grad_updated = grad_updated;
-    a.grad_normalized = grad_normalized;
-    a.grad_normalized_dtype = grad_normalized_dtype;
-    a.updated = updated;
-    a.weight = weight;
-    a.mean = mean;
-    a.rstd = rstd;
-    a.mask = dropout_mask;
-    a.grad_x = grad_x;
-    a.grad_branch = grad_branch;
-    a.grad_weight = grad_weight;
-    a.grad_bias = grad_bias;
-    a.partials = static_cast<float*>(workspace);
-    a.rows = rows;
-    a.scale = drop.scale;
-    a.stream = static_cast<hipStream_t>(stream);
-    a.flags = (grad_updated ? kHasGradUpdated : 0)
-        | (grad_normalized ? kHasGradNormalized : 0)
-        | (drop.active ? kDropout : 0)
-        | (parameters ? kParameters : 0)
-        | (partials ? kPartials : 0);
-
-    if (parameters && !partials && !accumulate_parameters) {
-        rln_zero_parameters_kernel<<<dim3(static_cast<unsigned>((hidden + 255) / 256)), 256, 0, a.stream>>>(
-            grad_weight, grad_bias, static_cast<int>(hidden));
-        status = check_launch("rln_zero_parameters_kernel");
-        if (status != RLN_OK) {
-            return status;
-        }
-    }
-
-    const bool aligned = aligned_to(grad_updated, 16)
-        && aligned_to(grad_normalized, vector_alignment(grad_normalized_dtype))
-        && aligned_to(updated, 16) && aligned_to(weight, 16) && aligned_to(grad_x, 16)
-        && aligned_to(grad_branch, vector_alignment(branch_dtype));
-    switch (hidden) {
-        case 128: status = launch_backward_hidden<128>(a, branch_dtype, aligned); break;
-        case 256: status = launch_backward_hidden<256>(a, branch_dtype, aligned); break;
-        case 384: status = launch_backward_hidden<384>(a, branch_dtype, aligned); break;
-        case 512: status = launch_backward_hidden<512>(a, branch_dtype, aligned); break;
-        case 768: status = launch_backward_hidden<768>(a, branch_dtype, aligned); break;
-        case 1024: status = launch_backward_hidden<1024>(a, branch_dtype, aligned); break;
-        default:
-            return fail(RLN_ERR_UNSUPPORTED, "unsupported native hidden size: %lld", static_cast<long long>(hidden));
-    }
-    if (status != RLN_OK) {
-        return status;
-    }
-    if (partials) {
-        const int64_t groups = backward_blocks(rows, hidden);
-        const unsigned blocks = static_cast<unsigned>((2 * hidden + kWaveSize - 1) / kWaveSize);
-        rln_parameter_reduce_kernel<<<dim3(blocks), kReduceWaves * kWaveSize, 0, a.stream>>>(
-            a.partials, grad_weight, grad_bias, groups, static_cast<int>(hidden),
-            accumulate_parameters ? 1 : 0);
-        status = check_launch("rln_parameter_reduce_kernel");
-    }
-    return status;
-}
-
-uint64_t rln_philox_increment(int64_t hidden) {
-    (void)hidden;
-    return 4;
-}
-
-int64_t rln_mask_words(int64_t rows, int64_t hidden) {
-    if (rows <= 0 || hidden <= 0 || hidden % 32 != 0) {
-        return 0;
-    }
-    return rows * (hidden / 32);
-}
-
-int rln_hidden_supported(int64_t hidden) {
-    return hidden_supported(hidden) ? 1 : 0;
-}
-
-int rln_supported_hidden_sizes(int64_t* out, int capacity) {
-    const int count = static_cast<int>(sizeof(kSupportedHidden) / sizeof(kSupportedHidden[0]));
-    for (int index = 0; index < count && index < capacity && out != nullptr; ++index) {
-        out[index] = kSupportedHidden[index];
-    }
-    return count;
-}
-
-const char* rln_last_error(void) {
-    return t_last_error.c_str();
-}
-
-const char* rln_target_arch(void) {
-    return "gfx950";
-}
-
-const char* rln_version(void) {
-    return "0.2.0";
-}
-
-}  // extern "C"
+#endif  // RLN_DEVICE_H
