@@ -133,6 +133,13 @@ def sweep_workloads() -> list[Workload]:
                               normalized="bf16"))
     workloads.append(Workload("C2 H=768 bf16-out", 262144, 768, "bf16", 1.0, 0.15,
                               seed=1770, normalized="bf16"))
+    # Hidden sizes the reference does not serve natively (run-time row length,
+    # several waves per row above 1024): GPT-2 XL's 1600 at the C1 batch, and
+    # ~134 M-element sweeps like C2's.
+    workloads.append(Workload("W H=1600 [8,1024]", 8 * 1024, 1600, "f16", 0.5, 0.1, seed=1600))
+    for hidden in (640, 1280, 1600, 2048, 4096, 8192):
+        workloads.append(Workload(f"W H={hidden}", (1 << 27) // hidden, hidden, "f16", 1.0, 0.15,
+                                  seed=2000 + hidden))
     return workloads
 
 
@@ -333,6 +340,25 @@ def gbps(nbytes: int, ms: float) -> float:
     return nbytes / (ms * 1e-3) / 1e9
 
 
+SPECIALIZED_HIDDEN = (128, 256, 384, 512, 768, 1024)
+
+
+def kernel_name(kernel: str, workload: Workload) -> str:
+    """The template instance of `kernel` this workload launches (as rocprofv3
+    names it): its row shape, branch type, normalized / gradient type, and the
+    aligned access path."""
+    if workload.hidden in SPECIALIZED_HIDDEN:
+        shape = f"rln::FixedShape<{workload.hidden}>"
+    else:
+        parts = 1 if workload.hidden <= 1024 else 2 if workload.hidden <= 2048 else (
+            4 if workload.hidden <= 4096 else 8)
+        vectors = -(-workload.hidden // (256 * parts))
+        shape = f"rln::WideShape<{vectors}, {parts}>"
+    types = {"f32": "float", "f16": "_Float16", "bf16": "__bf16"}
+    return (f"rln::{kernel}<{shape}, {types[workload.branch]}, "
+            f"{types[workload.normalized]}, true>")
+
+
 def result_line(torch, workload: Workload, timing: dict, steps: int, warmup: int,
                 sets: int, traffic) -> dict:
     total = workload.forward_bytes() + workload.backward_bytes()
@@ -344,7 +370,6 @@ def result_line(torch, workload: Workload, timing: dict, steps: int, warmup: int
     else:
         dominant, dominant_ms = "rln_forward_kernel", timing["forward_ms"]
         dominant_bytes = workload.forward_bytes()
-    branch_type = {"f32": "float", "f16": "_Float16", "bf16": "__bf16"}[workload.branch]
     dominant_gbps = gbps(dominant_bytes, dominant_ms)
     line = {
         "metric": METRIC,
@@ -376,7 +401,7 @@ def result_line(torch, workload: Workload, timing: dict, steps: int, warmup: int
         "algorithmic_bytes_per_step": total,
         "roofline": {
             "bound": "hbm",
-            "kernel": f"{dominant}<{workload.hidden}, {branch_type}, true>",
+            "kernel": kernel_name(dominant, workload),
             "achieved": round(dominant_gbps, 2),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",

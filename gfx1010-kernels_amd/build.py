@@ -48,9 +48,12 @@ HIP_FLAGS = [
     "-Wno-unused-command-line-argument",
 ]
 
-# One translation unit per hidden size (every dtype and alignment variant of
+# One translation unit per row shape (every dtype and alignment variant of
 # its kernels), plus the C ABI; compiled in parallel, linked into one library.
+# Specialized hidden sizes, and the (slots per lane, waves per row) pairs of
+# the run-time-length kernels that serve every other multiple of 64 up to 8192.
 HIDDEN_SIZES = (128, 256, 384, 512, 768, 1024)
+WIDE_SHAPES = ((1, 1), (2, 1), (3, 1), (4, 1), (3, 2), (4, 2), (3, 4), (4, 4), (3, 8), (4, 8))
 BUILD_DIR = ROOT / "_build"
 
 
@@ -78,6 +81,11 @@ def build_library(jobs: int | None = None) -> Path:
     units += [
         (CSRC / "rln_hidden.hip", BUILD_DIR / f"rln_hidden_{hidden}.o", [f"-DRLN_HIDDEN={hidden}"])
         for hidden in HIDDEN_SIZES
+    ]
+    units += [
+        (CSRC / "rln_hidden.hip", BUILD_DIR / f"rln_wide_{v}x{p}.o",
+         [f"-DRLN_WIDE_V={v}", f"-DRLN_WIDE_P={p}"])
+        for v, p in WIDE_SHAPES
     ]
     workers = jobs or min(len(units), max(1, (os.cpu_count() or 1)))
     with ThreadPoolExecutor(max_workers=workers) as pool:

@@ -1,5 +1,5 @@
 // C ABI of the MI355X fused residual LayerNorm (include/rln.h): argument
-// checks, dropout constants, dispatch to the per-hidden-size launchers
+// checks, dropout constants, dispatch to the per-row-shape launchers
 // (rln_device.h, instantiated in rln_hidden.hip), and the small kernels that
 // zero or reduce the weight/bias gradients.
 
@@ -11,7 +11,7 @@
 
 namespace rln {
 
-RLN_FOR_EACH_HIDDEN(RLN_DECLARE_HIDDEN)
+RLN_FOR_EACH_SHAPE(RLN_DECLARE_SHAPE)
 
 namespace {
 
@@ -240,16 +240,9 @@ int rln_forward(
         && aligned_to(updated, 16)
         && aligned_to(normalized, vector_alignment(normalized_dtype))
         && aligned_to(branch, vector_alignment(branch_dtype));
-    switch (hidden) {
-        case 128: return launch_forward_hidden<128>(a, branch_dtype, normalized_dtype, aligned);
-        case 256: return launch_forward_hidden<256>(a, branch_dtype, normalized_dtype, aligned);
-        case 384: return launch_forward_hidden<384>(a, branch_dtype, normalized_dtype, aligned);
-        case 512: return launch_forward_hidden<512>(a, branch_dtype, normalized_dtype, aligned);
-        case 768: return launch_forward_hidden<768>(a, branch_dtype, normalized_dtype, aligned);
-        case 1024: return launch_forward_hidden<1024>(a, branch_dtype, normalized_dtype, aligned);
-        default: break;
-    }
-    return fail(RLN_ERR_UNSUPPORTED, "unsupported native hidden size: %lld", static_cast<long long>(hidden));
+    return with_shape(hidden, [&](auto shape) {
+        return launch_forward_shape(a, shape, branch_dtype, normalized_dtype, aligned);
+    });
 }
 
 size_t rln_backward_workspace_bytes(int64_t rows, int64_t hidden, int deterministic) {
@@ -356,16 +349,9 @@ int rln_backward(
         && aligned_to(grad_normalized, vector_alignment(grad_normalized_dtype))
         && aligned_to(updated, 16) && aligned_to(weight, 16) && aligned_to(grad_x, 16)
         && aligned_to(grad_branch, vector_alignment(branch_dtype));
-    switch (hidden) {
-        case 128: status = launch_backward_hidden<128>(a, branch_dtype, grad_normalized_dtype, aligned); break;
-        case 256: status = launch_backward_hidden<256>(a, branch_dtype, grad_normalized_dtype, aligned); break;
-        case 384: status = launch_backward_hidden<384>(a, branch_dtype, grad_normalized_dtype, aligned); break;
-        case 512: status = launch_backward_hidden<512>(a, branch_dtype, grad_normalized_dtype, aligned); break;
-        case 768: status = launch_backward_hidden<768>(a, branch_dtype, grad_normalized_dtype, aligned); break;
-        case 1024: status = launch_backward_hidden<1024>(a, branch_dtype, grad_normalized_dtype, aligned); break;
-        default:
-            return fail(RLN_ERR_UNSUPPORTED, "unsupported native hidden size: %lld", static_cast<long long>(hidden));
-    }
+    status = with_shape(hidden, [&](auto shape) {
+        return launch_backward_shape(a, shape, branch_dtype, grad_normalized_dtype, aligned);
+    });
     if (status != RLN_OK) {
         return status;
     }
@@ -397,9 +383,15 @@ int rln_hidden_supported(int64_t hidden) {
 }
 
 int rln_supported_hidden_sizes(int64_t* out, int capacity) {
-    const int count = static_cast<int>(sizeof(kSupportedHidden) / sizeof(kSupportedHidden[0]));
-    for (int index = 0; index < count && index < capacity && out != nullptr; ++index) {
-        out[index] = kSupportedHidden[index];
+    int count = 0;
+    for (int64_t hidden = kHiddenMultiple; hidden <= kMaxHidden; hidden += kHiddenMultiple) {
+        if (!hidden_supported(hidden)) {
+            continue;
+        }
+        if (out != nullptr && count < capacity) {
+            out[count] = hidden;
+        }
+        ++count;
     }
     return count;
 }

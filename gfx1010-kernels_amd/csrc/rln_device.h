@@ -57,6 +57,9 @@
 #ifndef RLN_FWD_MAX_BLOCKS
 #define RLN_FWD_MAX_BLOCKS 2048
 #endif
+#ifndef RLN_FWD_GROUPS_PER_WAVE
+#define RLN_FWD_GROUPS_PER_WAVE 2
+#endif
 #ifndef RLN_BWD_MAX_BLOCKS
 #define RLN_BWD_MAX_BLOCKS 256
 #endif
@@ -84,15 +87,12 @@
 namespace rln {
 
 constexpr int kWaveSize = 64;
-constexpr int kForwardThreads = 256;
 constexpr int kBackwardThreads = RLN_BWD_THREADS;
 constexpr int64_t kForwardMaxBlocks = RLN_FWD_MAX_BLOCKS;
 constexpr int64_t kBackwardMaxBlocks = RLN_BWD_MAX_BLOCKS;
 constexpr int64_t kPacedElements = RLN_PACED_ELEMENTS;
 constexpr int64_t kPacedMinHidden = RLN_PACED_MIN_HIDDEN;
 static_assert(kBackwardThreads % kWaveSize == 0 && kBackwardThreads <= 1024, "backward block");
-
-constexpr int64_t kSupportedHidden[] = {128, 256, 384, 512, 768, 1024};
 
 using half_t = _Float16;
 using bf16_t = __bf16;
@@ -108,44 +108,111 @@ int fail(int code, const char* format, ...);
 int check_launch(const char* what);
 
 // ----------------------------------------------------------------------------
-// Row geometry for a hidden size H.
+// Row shapes. A row of `hidden` values is split into four-element vectors; a
+// team of lanes owns the row, and vector j of the row sits in slot v of lane
+// l of part p, with j = (v * kParts + p) * kLanes + l.
+//
+//  * FixedShape<H>: the reference's hidden sizes, known at compile time. One
+//    wave owns a row, or half a wave (32 lanes) when H/4 is not a multiple
+//    of 64 (H = 128, 384); every slot holds columns.
+//  * WideShape<V, P>: every other multiple of 64 from kMinHidden to
+//    kMaxHidden, passed at run time. P waves own a row (P > 1 add their row
+//    sums through LDS), V slots per lane; slots past the end of the row
+//    stay idle.
+
+constexpr int64_t kSpecializedHidden[] = {128, 256, 384, 512, 768, 1024};
+constexpr int64_t kMinHidden = 128;
+constexpr int64_t kMaxHidden = 8192;
+constexpr int64_t kHiddenMultiple = 64;
 
 template <int H>
-struct Geometry {
-    static constexpr int kVectors = H / 4;  // four-element vectors per row
-    static constexpr int kLanes = (kVectors % kWaveSize == 0) ? 64 : 32;
-    static constexpr int kV = kVectors / kLanes;  // vectors per lane
+struct FixedShape {
+    static constexpr int kLanes = ((H / 4) % kWaveSize == 0) ? 64 : 32;
+    static constexpr int kV = (H / 4) / kLanes;
+    static constexpr int kParts = 1;
     static constexpr int kRowsPerWave = kWaveSize / kLanes;
-    static constexpr int kMaskWords = H / 32;
-    static_assert(H % 64 == 0, "hidden size must be a multiple of 64");
-    static_assert(kVectors % kLanes == 0, "row must split evenly over lanes");
+    static constexpr bool kRagged = false;
+    static constexpr int kForwardThreads = 256;
+    static_assert(H % 64 == 0 && (H / 4) % kLanes == 0, "row must split evenly over lanes");
+    __host__ __device__ constexpr int64_t hidden() const { return H; }
+    __host__ __device__ constexpr float inv_hidden() const {
+        return 1.0f / static_cast<float>(H);
+    }
 };
 
-inline int64_t rows_per_wave(int64_t hidden) {
-    return ((hidden / 4) % kWaveSize == 0) ? 1 : 2;
+template <int V, int P>
+struct WideShape {
+    static constexpr int kLanes = kWaveSize;
+    static constexpr int kV = V;
+    static constexpr int kParts = P;
+    static constexpr int kRowsPerWave = 1;
+    static constexpr bool kRagged = true;
+    static constexpr int kForwardThreads = P > 4 ? P * kWaveSize : 256;
+    static_assert(P == 1 || P == 2 || P == 4 || P == 8, "parts per row");
+    int64_t hidden_;
+    float inv_hidden_;  // 1.0f / hidden, rounded once on the host
+    __host__ __device__ int64_t hidden() const { return hidden_; }
+    __host__ __device__ float inv_hidden() const { return inv_hidden_; }
+};
+
+inline bool specialized_hidden(int64_t hidden) {
+    for (const int64_t value : kSpecializedHidden) {
+        if (value == hidden) {
+            return true;
+        }
+    }
+    return false;
 }
 
-// Blocks for a launch over `rows`: enough for `groups_per_wave` row groups
-// per wave (a group = the rows one wave handles at once), capped; a function
-// of (rows, hidden) only.
+inline bool hidden_supported(int64_t hidden) {
+    return specialized_hidden(hidden)
+        || (hidden >= kMinHidden && hidden <= kMaxHidden && hidden % kHiddenMultiple == 0);
+}
+
+// The shape parameters a supported hidden size runs with (host side; the
+// kernels' template parameters must match them).
+struct ShapeInfo {
+    int rows_per_wave;
+    int parts;
+    int vectors;  // slots per lane
+    int forward_threads;
+};
+
+inline ShapeInfo shape_info(int64_t hidden) {
+    if (specialized_hidden(hidden)) {
+        const int rows_per_wave = ((hidden / 4) % kWaveSize == 0) ? 1 : 2;
+        return {rows_per_wave, 1, static_cast<int>(hidden / 4 / (kWaveSize / rows_per_wave)),
+                256};
+    }
+    const int parts = hidden <= 1024 ? 1 : hidden <= 2048 ? 2 : hidden <= 4096 ? 4 : 8;
+    const int64_t per_slot = 4 * kWaveSize * parts;
+    const int vectors = static_cast<int>((hidden + per_slot - 1) / per_slot);
+    return {1, parts, vectors, parts > 4 ? parts * kWaveSize : 256};
+}
+
+// Blocks for a launch over `rows`: each block works on
+// (threads / 64) * rows_per_wave / parts rows at a time, and gets enough
+// blocks for `iterations` such steps, capped; a function of (rows, hidden)
+// only.
 inline int64_t launch_blocks(int64_t rows, int64_t hidden, int threads, int64_t cap,
-                      int64_t groups_per_wave) {
-    const int64_t groups = (rows + rows_per_wave(hidden) - 1) / rows_per_wave(hidden);
-    const int64_t waves = (groups + groups_per_wave - 1) / groups_per_wave;
-    const int64_t waves_per_block = threads / kWaveSize;
-    const int64_t blocks = (waves + waves_per_block - 1) / waves_per_block;
+                             int64_t iterations) {
+    const ShapeInfo info = shape_info(hidden);
+    const int64_t rows_per_block = (threads / kWaveSize) * info.rows_per_wave / info.parts;
+    const int64_t steps = (rows + rows_per_block - 1) / rows_per_block;
+    const int64_t blocks = (steps + iterations - 1) / iterations;
     return blocks < cap ? blocks : cap;
 }
 
-// The forward gives each wave at least two row groups so that its
+// The forward gives each team at least two row steps so that its
 // look-ahead load overlaps a row's computation; with 256-thread blocks and
 // ~100 VGPRs per lane the cap of 2048 blocks is two waves of residency.
 inline int64_t forward_blocks(int64_t rows, int64_t hidden) {
-    return launch_blocks(rows, hidden, kForwardThreads, kForwardMaxBlocks, 2);
+    return launch_blocks(rows, hidden, shape_info(hidden).forward_threads, kForwardMaxBlocks,
+                         RLN_FWD_GROUPS_PER_WAVE);
 }
 
-// The backward's grid is also the number of weight/bias partials: 256
-// blocks of 8 waves, one block per CU.
+// The backward's grid is also the number of weight/bias partials: at most
+// 256 blocks of 8 waves, one block per CU.
 inline int64_t backward_blocks(int64_t rows, int64_t hidden) {
     return launch_blocks(rows, hidden, kBackwardThreads, kBackwardMaxBlocks, 1);
 }
@@ -155,15 +222,6 @@ inline int64_t backward_blocks(int64_t rows, int64_t hidden) {
 // C1-sized launches), 0 for look-ahead.
 inline int paced_schedule(int64_t rows, int64_t hidden) {
     return hidden >= kPacedMinHidden && rows * hidden >= kPacedElements ? 1 : 0;
-}
-
-inline bool hidden_supported(int64_t hidden) {
-    for (const int64_t value : kSupportedHidden) {
-        if (value == hidden) {
-            return true;
-        }
-    }
-    return false;
 }
 
 // ----------------------------------------------------------------------------
@@ -397,8 +455,88 @@ struct ForwardRow {
     typename Vector4<B>::type branch[V];
 };
 
-template <int H, typename B, typename N, bool Aligned>
-__global__ __launch_bounds__(kForwardThreads)
+// Where a lane's slots sit in its row, for shape S: vector index of slot v,
+// whether the slot holds columns, and the first column to access (slot 0's
+// column for an idle slot, so that its accesses stay inside the row).
+template <typename S>
+struct Slots {
+    int part;
+    int lane;  // lane within the part's lanes
+    int64_t hidden;
+
+    __device__ __forceinline__ int vector(int v) const {
+        return (v * S::kParts + part) * S::kLanes + lane;
+    }
+    __device__ __forceinline__ bool active(int v) const {
+        return !S::kRagged || static_cast<int64_t>(vector(v)) * 4 < hidden;
+    }
+    __device__ __forceinline__ int column(int v) const {
+        return active(v) ? vector(v) * 4 : 0;
+    }
+};
+
+// Sum of `value` over a row's lanes (all lanes receive the same bits). With
+// P > 1 parts, each wave's total goes through `exchange[group][part]` in
+// LDS and the parts are added in ascending order; every wave of the block
+// must call it (it holds a block barrier).
+template <typename S>
+__device__ __forceinline__ float team_sum(float value, float (*exchange)[S::kParts], int group,
+                                          int part) {
+    const float wave_total = row_sum<S::kLanes>(value);
+    if constexpr (S::kParts == 1) {
+        return wave_total;
+    } else {
+        if ((threadIdx.x & (kWaveSize - 1)) == 0) {
+            exchange[group][part] = wave_total;
+        }
+        __syncthreads();
+        float total = exchange[group][0];
+#pragma unroll
+        for (int other = 1; other < S::kParts; ++other) {
+            total += exchange[group][other];
+        }
+        return total;
+    }
+}
+
+// Rows are walked by teams: a wave (one or two rows at a time) when a row
+// fits one wave, else the whole block (kWaves / P rows at a time), so that
+// every wave of a block meets the same barriers.
+template <typename S, int Threads>
+struct Teams {
+    static constexpr int kWaves = Threads / kWaveSize;
+    static constexpr int kGroups = S::kParts == 1 ? kWaves : kWaves / S::kParts;
+    static constexpr int kRowsPerTeam = S::kParts == 1 ? S::kRowsPerWave : kGroups;
+    static_assert(kWaves % S::kParts == 0, "a block holds whole rows");
+
+    int64_t first;   // first row of this thread's team
+    int64_t stride;  // rows between a team's consecutive steps
+    int offset;      // this thread's row within the team's step
+    int group;       // row slot within the block for the LDS exchange
+    int part;
+
+    __device__ __forceinline__ Teams() {
+        const int lane = threadIdx.x & (kWaveSize - 1);
+        const int wave = threadIdx.x / kWaveSize;
+        if constexpr (S::kParts == 1) {
+            const int64_t team = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
+            first = team * kRowsPerTeam;
+            stride = static_cast<int64_t>(gridDim.x) * kWaves * kRowsPerTeam;
+            offset = lane / S::kLanes;
+            group = wave;
+            part = 0;
+        } else {
+            first = static_cast<int64_t>(blockIdx.x) * kRowsPerTeam;
+            stride = static_cast<int64_t>(gridDim.x) * kRowsPerTeam;
+            offset = wave / S::kParts;
+            group = offset;
+            part = wave % S::kParts;
+        }
+    }
+};
+
+template <typename S, typename B, typename N, bool Aligned>
+__global__ __launch_bounds__(S::kForwardThreads)
 void rln_forward_kernel(
     const float* __restrict__ x,
     const B* __restrict__ branch,
@@ -410,30 +548,32 @@ void rln_forward_kernel(
     float* __restrict__ rstd_out,
     uint32_t* __restrict__ mask,
     int64_t rows,
+    S shape,
     float eps,
     int dropout,
     float scale,
     uint32_t threshold,
     PhiloxArgs philox,
     int paced) {
-    using G = Geometry<H>;
-    constexpr int L = G::kLanes;
-    constexpr int V = G::kV;
-    constexpr int kWaves = kForwardThreads / kWaveSize;
-    constexpr float kInvHidden = 1.0f / static_cast<float>(H);
-
-    const int lane = threadIdx.x & (kWaveSize - 1);
-    const int sub = lane / L;
-    const int l = lane % L;
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x / kWaveSize);
-    const int64_t wave_count = static_cast<int64_t>(gridDim.x) * kWaves;
+    constexpr int V = S::kV;
+    using T = Teams<S, S::kForwardThreads>;
+    const int64_t hidden = shape.hidden();
+    const float inv_hidden = shape.inv_hidden();
+    const T team;
+    const Slots<S> slots{team.part, static_cast<int>(threadIdx.x & (kWaveSize - 1)) % S::kLanes,
+                         hidden};
+    const int l = slots.lane;
+    // Row sums of multi-wave rows: [0] the mean's, [1] the variance's. Two
+    // arrays and a barrier per sum keep a wave that runs ahead from
+    // overwriting a value another wave has yet to read.
+    __shared__ float exchange[2][T::kGroups][S::kParts];
 
     f32x4 w[V];
     f32x4 b[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) {
-        w[v] = load_parameter4<Aligned>(weight + (v * L + l) * 4);
-        b[v] = load_parameter4<Aligned>(bias + (v * L + l) * 4);
+        w[v] = load_parameter4<Aligned>(weight + slots.column(v));
+        b[v] = load_parameter4<Aligned>(bias + slots.column(v));
     }
 
     uint32_t key0 = 0;
@@ -450,17 +590,18 @@ void rln_forward_kernel(
         position = offset / 4;
     }
 
-    // Loads x and the branch of one row. The loads are unconditional (a
-    // half-wave row past the end reads the last row instead and discards it),
-    // so the compiler can count them and wait for exactly the ones a
-    // computation needs; a load under a branch makes it wait for all.
+    // Loads x and the branch of one row. The loads are unconditional (a row
+    // past the end reads the last row instead, an idle slot its row's first
+    // columns, and both are discarded), so the compiler can count them and
+    // wait for exactly the ones a computation needs; a load under a branch
+    // makes it wait for all.
     auto load_row = [&](ForwardRow<V, B>& r, int64_t row, bool wait_slices) {
         const int64_t source = row < rows ? row : rows - 1;
-        const float* x_row = x + source * H;
-        const B* branch_row = branch + source * H;
+        const float* x_row = x + source * hidden;
+        const B* branch_row = branch + source * hidden;
 #pragma unroll
         for (int v = 0; v < V; ++v) {
-            const int column = (v * L + l) * 4;
+            const int column = slots.column(v);
             r.x[v] = load4<Aligned>(x_row + column);
             r.branch[v] = load_raw4<B, Aligned>(branch_row + column);
             if (wait_slices) {
@@ -471,7 +612,7 @@ void rln_forward_kernel(
 
     auto process_row = [&](const ForwardRow<V, B>& r, int64_t row) {
         const bool valid = row < rows;
-        const int64_t base = row * H;
+        const int64_t base = row * hidden;
         f32x4 u[V];
         uint32_t keep_bits[V];
 #pragma unroll
@@ -479,7 +620,7 @@ void rln_forward_kernel(
             f32x4 bv = widen4<B>(r.branch[v]);
             keep_bits[v] = 0;
             if (dropout) {
-                const uint64_t group = static_cast<uint64_t>(row) * (H / 4) + (v * L + l);
+                const uint64_t group = static_cast<uint64_t>(row) * (hidden / 4) + slots.vector(v);
                 const uint4 random = philox4x32_10(
                     make_uint4(
                         static_cast<uint32_t>(position),
@@ -499,17 +640,22 @@ void rln_forward_kernel(
                 keep_bits[v] = k0 | (k1 << 1) | (k2 << 2) | (k3 << 3);
             }
             u[v] = r.x[v] + bv;
-            if (valid) {
-                store4<Aligned>(updated + base + (v * L + l) * 4, u[v]);
+            if (valid && slots.active(v)) {
+                store4<Aligned>(updated + base + slots.column(v), u[v]);
+            }
+            if (!slots.active(v)) {
+                u[v] = zero4();
             }
         }
 
         if (dropout) {
 #pragma unroll
             for (int v = 0; v < V; ++v) {
+                // A word's 32 columns belong to 8 lanes of one slot, all
+                // active or all idle (hidden is a multiple of 32).
                 const uint32_t word = or8(keep_bits[v] << (4 * (l & 7)));
-                if (valid && (l & 7) == 0) {
-                    stream_store(word, mask + row * G::kMaskWords + (v * L + l) / 8);
+                if (valid && slots.active(v) && (l & 7) == 0) {
+                    stream_store(word, mask + row * (hidden / 32) + slots.vector(v) / 8);
                 }
             }
         }
@@ -519,32 +665,34 @@ void rln_forward_kernel(
         for (int v = 0; v < V; ++v) {
             partial += sum4(u[v]);
         }
-        const float mean = row_sum<L>(partial) * kInvHidden;
+        const float mean = team_sum<S>(partial, exchange[0], team.group, team.part) * inv_hidden;
 
         float square = 0.0f;
 #pragma unroll
         for (int v = 0; v < V; ++v) {
-            u[v] = u[v] - mean;
+            u[v] = slots.active(v) ? u[v] - mean : zero4();
             square += (u[v].x * u[v].x + u[v].y * u[v].y)
                 + (u[v].z * u[v].z + u[v].w * u[v].w);
         }
-        const float variance = row_sum<L>(square) * kInvHidden;
+        const float variance =
+            team_sum<S>(square, exchange[1], team.group, team.part) * inv_hidden;
         const float rstd = rsqrtf(variance + eps);
 
         if (valid) {
-            if (l == 0) {
+            if (l == 0 && team.part == 0) {
                 mean_out[row] = mean;
                 rstd_out[row] = rstd;
             }
 #pragma unroll
             for (int v = 0; v < V; ++v) {
-                const int column = (v * L + l) * 4;
                 const f32x4 y = {
                     __builtin_fmaf(u[v].x * rstd, w[v].x, b[v].x),
                     __builtin_fmaf(u[v].y * rstd, w[v].y, b[v].y),
                     __builtin_fmaf(u[v].z * rstd, w[v].z, b[v].z),
                     __builtin_fmaf(u[v].w * rstd, w[v].w, b[v].w)};
-                store_convert4<N, Aligned>(normalized + base + column, y);
+                if (slots.active(v)) {
+                    store_convert4<N, Aligned>(normalized + base + slots.column(v), y);
+                }
             }
         }
     };
@@ -554,29 +702,30 @@ void rln_forward_kernel(
     // launches): a row is loaded after the previous one is stored, one
     // 4-column slice at a time, each waited for (with every earlier store of
     // the wave), which keeps fewer reads and writes interleaved per wave and
-    // streams large tensors faster. The last row of a wave is peeled off, so
-    // no load reaches past the wave's rows.
-    const int64_t stride = wave_count * G::kRowsPerWave;
-    int64_t first = wave * G::kRowsPerWave;
+    // streams large tensors faster. The last row of a team is peeled off, so
+    // no load reaches past the team's rows. `first` is uniform over a team,
+    // so a multi-wave team meets its barriers together.
+    const int64_t stride = team.stride;
+    int64_t first = team.first;
     if (first >= rows) {
         return;
     }
     ForwardRow<V, B> current;
-    load_row(current, first + sub, false);
+    load_row(current, first + team.offset, false);
     if (paced) {
         for (; first + stride < rows; first += stride) {
-            process_row(current, first + sub);
-            load_row(current, first + stride + sub, true);
+            process_row(current, first + team.offset);
+            load_row(current, first + stride + team.offset, true);
         }
     } else {
         for (; first + stride < rows; first += stride) {
             ForwardRow<V, B> next;
-            load_row(next, first + stride + sub, false);
-            process_row(current, first + sub);
+            load_row(next, first + stride + team.offset, false);
+            process_row(current, first + team.offset);
             current = next;
         }
     }
-    process_row(current, first + sub);
+    process_row(current, first + team.offset);
 }
 
 // ----------------------------------------------------------------------------
@@ -601,7 +750,7 @@ enum BackwardFlags : int {
     kPartials = 16,  // write per-block partials (else fp32 atomics)
 };
 
-template <int H, typename B, typename GY, bool Aligned>
+template <typename S, typename B, typename GY, bool Aligned>
 __global__ __launch_bounds__(kBackwardThreads)
 void rln_backward_kernel(
     const float* __restrict__ grad_updated,
@@ -617,21 +766,26 @@ void rln_backward_kernel(
     float* __restrict__ grad_bias,
     float* __restrict__ partials,
     int64_t rows,
+    S shape,
     int flags,
     float scale,
     int paced) {
-    using G = Geometry<H>;
-    constexpr int L = G::kLanes;
-    constexpr int V = G::kV;
-    constexpr int kWaves = kBackwardThreads / kWaveSize;
-    constexpr float kInvHidden = 1.0f / static_cast<float>(H);
-
+    constexpr int L = S::kLanes;
+    constexpr int V = S::kV;
+    constexpr int P = S::kParts;
+    using T = Teams<S, kBackwardThreads>;
+    constexpr int kWaves = T::kWaves;
+    const int64_t hidden = shape.hidden();
+    const float inv_hidden = shape.inv_hidden();
     const int lane = threadIdx.x & (kWaveSize - 1);
-    const int sub = lane / L;
-    const int l = lane % L;
     const int wave_in_block = threadIdx.x / kWaveSize;
-    const int64_t wave = static_cast<int64_t>(blockIdx.x) * kWaves + wave_in_block;
-    const int64_t wave_count = static_cast<int64_t>(gridDim.x) * kWaves;
+    const T team;
+    const Slots<S> slots{team.part, lane % L, hidden};
+    const int l = slots.lane;
+    // Row sums of multi-wave rows: [0] Σq, [1] Σq·x̂. Two arrays and a
+    // barrier per sum keep a wave that runs ahead from overwriting a value
+    // another wave has yet to read.
+    __shared__ float exchange[2][T::kGroups][P];
 
     const bool has_gu = flags & kHasGradUpdated;
     const bool has_gy = flags & kHasGradNormalized;
@@ -643,7 +797,7 @@ void rln_backward_kernel(
     f32x4 acc_b[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) {
-        w[v] = load_parameter4<Aligned>(weight + (v * L + l) * 4);
+        w[v] = load_parameter4<Aligned>(weight + slots.column(v));
         acc_w[v] = zero4();
         acc_b[v] = zero4();
     }
@@ -651,25 +805,26 @@ void rln_backward_kernel(
     // Loads every global value of one row. The loads are unconditional, so
     // the compiler can count them and wait for exactly the ones a computation
     // needs (a load under a branch makes it wait for all): an absent input
-    // reads the row of `updated` in its place, and a half-wave row past the
-    // end reads the last row; process_row discards what it read.
+    // reads the row of `updated` in its place, a row past the end reads the
+    // last row, an idle slot its row's first columns; process_row discards
+    // what it read.
     auto load_row = [&](BackwardRow<V, GY>& r, int64_t row, bool wait_slices) {
         const int64_t source = row < rows ? row : rows - 1;
-        const int64_t base = source * H;
+        const int64_t base = source * hidden;
         const float* u_row = updated + base;
         const GY* gy_row = has_gy ? grad_normalized + base : reinterpret_cast<const GY*>(u_row);
         const float* gu_row = has_gu ? grad_updated + base : u_row;
-        const uint32_t* mask_row = dropout ? mask + source * G::kMaskWords
+        const uint32_t* mask_row = dropout ? mask + source * (hidden / 32)
                                            : reinterpret_cast<const uint32_t*>(u_row);
         r.mean = mean_in[source];
         r.rstd = rstd_in[source];
 #pragma unroll
         for (int v = 0; v < V; ++v) {
-            const int column = (v * L + l) * 4;
+            const int column = slots.column(v);
             r.u[v] = load4<Aligned>(u_row + column);
             r.gy[v] = load_raw4<GY, Aligned>(gy_row + column);
             r.gu[v] = load4<Aligned>(gu_row + column);
-            r.mask_word[v] = mask_row[(v * L + l) / 8];
+            r.mask_word[v] = mask_row[column / 32];
             if (wait_slices) {
                 __builtin_amdgcn_s_waitcnt(0);
             }
@@ -679,18 +834,19 @@ void rln_backward_kernel(
     // Input gradients of one row and its contribution to the parameter sums.
     auto process_row = [&](const BackwardRow<V, GY>& r, int64_t row) {
         const bool valid = row < rows;
-        const int64_t base = row * H;
+        const int64_t base = row * hidden;
         f32x4 xhat[V];
         f32x4 gy[V];
         float sum_q = 0.0f;
         float sum_qx = 0.0f;
-        // Inputs that were not given, and every input of a row past the end,
-        // count as zero.
+        // Inputs that were not given, every input of a row past the end and
+        // idle slots count as zero.
         const bool use_gy = has_gy && valid;
 #pragma unroll
         for (int v = 0; v < V; ++v) {
-            gy[v] = use_gy ? widen4<GY>(r.gy[v]) : zero4();
-            xhat[v] = (r.u[v] - r.mean) * r.rstd;
+            const bool live = use_gy && slots.active(v);
+            gy[v] = live ? widen4<GY>(r.gy[v]) : zero4();
+            xhat[v] = slots.active(v) ? (r.u[v] - r.mean) * r.rstd : zero4();
             const f32x4 q = gy[v] * w[v];
             sum_q += sum4(q);
             sum_qx += (q.x * xhat[v].x + q.y * xhat[v].y)
@@ -700,14 +856,17 @@ void rln_backward_kernel(
         float mean_q = 0.0f;
         float mean_qx = 0.0f;
         if (has_gy) {
-            mean_q = row_sum<L>(sum_q) * kInvHidden;
-            mean_qx = row_sum<L>(sum_qx) * kInvHidden;
+            mean_q = team_sum<S>(sum_q, exchange[0], team.group, team.part) * inv_hidden;
+            mean_qx = team_sum<S>(sum_qx, exchange[1], team.group, team.part) * inv_hidden;
         }
 
         if (valid) {
 #pragma unroll
             for (int v = 0; v < V; ++v) {
-                const int column = (v * L + l) * 4;
+                if (!slots.active(v)) {
+                    continue;
+                }
+                const int column = slots.column(v);
                 f32x4 g = has_gu ? r.gu[v] : zero4();
                 if (has_gy) {
                     const f32x4 q = gy[v] * w[v];
@@ -737,40 +896,43 @@ void rln_backward_kernel(
         }
     };
 
-    // Each wave walks its rows under one of two schedules: look-ahead (the
+    // Each team walks its rows under one of two schedules: look-ahead (the
     // next row's loads in flight while the current row is reduced and stored;
     // small launches) or paced (a row loaded after the previous one is
     // stored, one 4-column slice at a time, each waited for; large launches,
     // where fewer interleaved reads and writes per wave stream faster). The
-    // last row of a wave is peeled off, so no load reaches past the wave's
-    // rows. A wave without rows still takes part in the block's combine.
-    const int64_t stride = wave_count * G::kRowsPerWave;
-    int64_t first = wave * G::kRowsPerWave;
+    // last row of a team is peeled off, so no load reaches past the team's
+    // rows. `first` is uniform over a team, so a multi-wave team meets its
+    // barriers together; a team without rows still takes part in the block's
+    // combine below.
+    const int64_t stride = team.stride;
+    int64_t first = team.first;
     if (first < rows) {
         BackwardRow<V, GY> current;
-        load_row(current, first + sub, false);
+        load_row(current, first + team.offset, false);
         if (paced) {
             for (; first + stride < rows; first += stride) {
-                process_row(current, first + sub);
-                load_row(current, first + stride + sub, true);
+                process_row(current, first + team.offset);
+                load_row(current, first + stride + team.offset, true);
             }
         } else {
             for (; first + stride < rows; first += stride) {
                 BackwardRow<V, GY> next;
-                load_row(next, first + stride + sub, false);
-                process_row(current, first + sub);
+                load_row(next, first + stride + team.offset, false);
+                process_row(current, first + team.offset);
                 current = next;
             }
         }
-        process_row(current, first + sub);
+        process_row(current, first + team.offset);
     }
 
     if (!parameters) {
         return;
     }
 
-    // Combine the block's sums in a fixed order: for every column, waves
-    // 0..kWaves-1 and, within a wave, row slots 0..kRowsPerWave-1.
+    // Combine the block's sums in a fixed order. A column is owned by one
+    // (part, lane) pair; for each, the block adds groups 0..kGroups-1 and,
+    // within a wave, row slots 0..kRowsPerWave-1.
     __shared__ f32x4 staging[kWaves][kWaveSize][2];
     const bool write_partials = flags & kPartials;
 #pragma unroll
@@ -778,22 +940,29 @@ void rln_backward_kernel(
         staging[wave_in_block][lane][0] = acc_w[v];
         staging[wave_in_block][lane][1] = acc_b[v];
         __syncthreads();
-        // L lanes x 8 floats to produce; the block's threads share them.
-        for (int entry = threadIdx.x; entry < L * 8; entry += kBackwardThreads) {
-            const int slot = entry / 8;
+        // P x L owners x 8 floats to produce; the block's threads share them.
+        for (int entry = threadIdx.x; entry < P * L * 8; entry += kBackwardThreads) {
+            const int owner = entry / 8;
+            const int owner_part = owner / L;
+            const int slot = owner % L;
             const int which = (entry / 4) & 1;  // 0 = weight, 1 = bias
             const int component = entry & 3;
+            const int64_t column = static_cast<int64_t>((v * P + owner_part) * L + slot) * 4
+                + component;
+            if (S::kRagged && column >= hidden) {
+                continue;
+            }
             float total = 0.0f;
 #pragma unroll
-            for (int source_wave = 0; source_wave < kWaves; ++source_wave) {
+            for (int group = 0; group < T::kGroups; ++group) {
 #pragma unroll
-                for (int source_sub = 0; source_sub < G::kRowsPerWave; ++source_sub) {
-                    total += staging[source_wave][source_sub * L + slot][which][component];
+                for (int source_sub = 0; source_sub < S::kRowsPerWave; ++source_sub) {
+                    total += staging[group * P + owner_part][source_sub * L + slot][which]
+                                    [component];
                 }
             }
-            const int column = (v * L + slot) * 4 + component;
             if (write_partials) {
-                partials[(static_cast<int64_t>(blockIdx.x) * 2 + which) * H + column] = total;
+                partials[(static_cast<int64_t>(blockIdx.x) * 2 + which) * hidden + column] = total;
             } else {
                 unsafeAtomicAdd((which ? grad_bias : grad_weight) + column, total);
             }
@@ -843,10 +1012,24 @@ struct BackwardArgs {
     hipStream_t stream;
 };
 
-template <int H, typename B, typename N, bool Aligned>
-int launch_forward(const ForwardArgs& a) {
-    const dim3 grid(static_cast<unsigned>(forward_blocks(a.rows, H)));
-    rln_forward_kernel<H, B, N, Aligned><<<grid, kForwardThreads, 0, a.stream>>>(
+// The kernels' template shape must be the one shape_info() describes for the
+// hidden size, since the grid (and so the deterministic order) is computed
+// from the latter.
+template <typename S>
+int check_shape(const S& shape) {
+    const ShapeInfo info = shape_info(shape.hidden());
+    if (info.parts != S::kParts || info.rows_per_wave != S::kRowsPerWave
+        || info.vectors != S::kV || info.forward_threads != S::kForwardThreads) {
+        return fail(RLN_ERR_UNSUPPORTED, "shape mismatch for hidden size %lld",
+                    static_cast<long long>(shape.hidden()));
+    }
+    return RLN_OK;
+}
+
+template <typename S, typename B, typename N, bool Aligned>
+int launch_forward(const ForwardArgs& a, S shape) {
+    const dim3 grid(static_cast<unsigned>(forward_blocks(a.rows, shape.hidden())));
+    rln_forward_kernel<S, B, N, Aligned><<<grid, S::kForwardThreads, 0, a.stream>>>(
         a.x,
         static_cast<const B*>(a.branch),
         a.weight,
@@ -857,19 +1040,20 @@ int launch_forward(const ForwardArgs& a) {
         a.rstd,
         a.mask,
         a.rows,
+        shape,
         a.eps,
         a.dropout,
         a.scale,
         a.threshold,
         a.philox,
-        paced_schedule(a.rows, H));
+        paced_schedule(a.rows, shape.hidden()));
     return check_launch("rln_forward_kernel");
 }
 
-template <int H, typename B, typename GY, bool Aligned>
-int launch_backward(const BackwardArgs& a) {
-    const dim3 grid(static_cast<unsigned>(backward_blocks(a.rows, H)));
-    rln_backward_kernel<H, B, GY, Aligned><<<grid, kBackwardThreads, 0, a.stream>>>(
+template <typename S, typename B, typename GY, bool Aligned>
+int launch_backward(const BackwardArgs& a, S shape) {
+    const dim3 grid(static_cast<unsigned>(backward_blocks(a.rows, shape.hidden())));
+    rln_backward_kernel<S, B, GY, Aligned><<<grid, kBackwardThreads, 0, a.stream>>>(
         a.grad_updated,
         static_cast<const GY*>(a.grad_normalized),
         a.updated,
@@ -883,9 +1067,10 @@ int launch_backward(const BackwardArgs& a) {
         a.grad_bias,
         a.partials,
         a.rows,
+        shape,
         a.flags,
         a.scale,
-        paced_schedule(a.rows, H));
+        paced_schedule(a.rows, shape.hidden()));
     return check_launch("rln_backward_kernel");
 }
 
@@ -901,34 +1086,84 @@ int with_dtype(int dtype, Launch&& launch) {
     return launch.template operator()<float>();
 }
 
-// Every (branch, normalized, alignment) instantiation for one hidden size;
-// explicitly instantiated once per H in rln_hidden.hip.
-template <int H>
-int launch_forward_hidden(const ForwardArgs& a, int branch_dtype, int normalized_dtype,
-                          bool aligned) {
+// Every (branch, normalized, alignment) instantiation for one row shape;
+// explicitly instantiated once per shape in rln_hidden.hip.
+template <typename S>
+int launch_forward_shape(const ForwardArgs& a, S shape, int branch_dtype, int normalized_dtype,
+                         bool aligned) {
+    const int status = check_shape(shape);
+    if (status != RLN_OK) {
+        return status;
+    }
     return with_dtype(branch_dtype, [&]<typename B>() {
         return with_dtype(normalized_dtype, [&]<typename N>() {
-            return aligned ? launch_forward<H, B, N, true>(a) : launch_forward<H, B, N, false>(a);
+            return aligned ? launch_forward<S, B, N, true>(a, shape)
+                           : launch_forward<S, B, N, false>(a, shape);
         });
     });
 }
 
-template <int H>
-int launch_backward_hidden(const BackwardArgs& a, int branch_dtype, int grad_normalized_dtype,
-                           bool aligned) {
+template <typename S>
+int launch_backward_shape(const BackwardArgs& a, S shape, int branch_dtype,
+                          int grad_normalized_dtype, bool aligned) {
+    const int status = check_shape(shape);
+    if (status != RLN_OK) {
+        return status;
+    }
     return with_dtype(branch_dtype, [&]<typename B>() {
         return with_dtype(grad_normalized_dtype, [&]<typename GY>() {
-            return aligned ? launch_backward<H, B, GY, true>(a)
-                           : launch_backward<H, B, GY, false>(a);
+            return aligned ? launch_backward<S, B, GY, true>(a, shape)
+                           : launch_backward<S, B, GY, false>(a, shape);
         });
     });
 }
 
-#define RLN_FOR_EACH_HIDDEN(X) X(128) X(256) X(384) X(512) X(768) X(1024)
+// Calls `launch(shape)` with the row shape of a supported hidden size.
+template <typename Launch>
+int with_shape(int64_t hidden, Launch&& launch) {
+    switch (hidden) {
+        case 128: return launch(FixedShape<128>{});
+        case 256: return launch(FixedShape<256>{});
+        case 384: return launch(FixedShape<384>{});
+        case 512: return launch(FixedShape<512>{});
+        case 768: return launch(FixedShape<768>{});
+        case 1024: return launch(FixedShape<1024>{});
+        default: break;
+    }
+    if (!hidden_supported(hidden)) {
+        return fail(RLN_ERR_UNSUPPORTED, "unsupported native hidden size: %lld",
+                    static_cast<long long>(hidden));
+    }
+    const ShapeInfo info = shape_info(hidden);
+    const float inv_hidden = 1.0f / static_cast<float>(hidden);
+    switch (info.parts * 16 + info.vectors) {
+        case 1 * 16 + 1: return launch(WideShape<1, 1>{hidden, inv_hidden});
+        case 1 * 16 + 2: return launch(WideShape<2, 1>{hidden, inv_hidden});
+        case 1 * 16 + 3: return launch(WideShape<3, 1>{hidden, inv_hidden});
+        case 1 * 16 + 4: return launch(WideShape<4, 1>{hidden, inv_hidden});
+        case 2 * 16 + 3: return launch(WideShape<3, 2>{hidden, inv_hidden});
+        case 2 * 16 + 4: return launch(WideShape<4, 2>{hidden, inv_hidden});
+        case 4 * 16 + 3: return launch(WideShape<3, 4>{hidden, inv_hidden});
+        case 4 * 16 + 4: return launch(WideShape<4, 4>{hidden, inv_hidden});
+        case 8 * 16 + 3: return launch(WideShape<3, 8>{hidden, inv_hidden});
+        case 8 * 16 + 4: return launch(WideShape<4, 8>{hidden, inv_hidden});
+        default: break;
+    }
+    return fail(RLN_ERR_UNSUPPORTED, "no row shape for hidden size %lld",
+                static_cast<long long>(hidden));
+}
 
-#define RLN_DECLARE_HIDDEN(H)                                                            \
-    extern template int launch_forward_hidden<H>(const ForwardArgs&, int, int, bool);    \
-    extern template int launch_backward_hidden<H>(const BackwardArgs&, int, int, bool);
+// The row shapes, one translation unit each (rln_hidden.hip).
+#define RLN_FOR_EACH_SHAPE(X)                                                     \
+    X(FixedShape<128>) X(FixedShape<256>) X(FixedShape<384>) X(FixedShape<512>)   \
+    X(FixedShape<768>) X(FixedShape<1024>) X(RLN_WIDE(1, 1)) X(RLN_WIDE(2, 1))   \
+    X(RLN_WIDE(3, 1)) X(RLN_WIDE(4, 1)) X(RLN_WIDE(3, 2)) X(RLN_WIDE(4, 2))       \
+    X(RLN_WIDE(3, 4)) X(RLN_WIDE(4, 4)) X(RLN_WIDE(3, 8)) X(RLN_WIDE(4, 8))
+#define RLN_WIDE(V, P) WideShape<V, P>
+
+#define RLN_DECLARE_SHAPE(S)                                                                  \
+    extern template int launch_forward_shape<S>(const ForwardArgs&, S, int, int, bool);      \
+    extern template int launch_backward_shape<S>(const BackwardArgs&, S, int, int, bool);
 
 }  // namespace rln
 

@@ -1,15 +1,20 @@
-// Instantiates every forward and backward kernel of one hidden size, so that
-// the build compiles the six hidden sizes as separate translation units in
-// parallel. Compiled once per size with -DRLN_HIDDEN=<H>.
+// Instantiates every forward and backward kernel of one row shape, so that
+// the build compiles the shapes as separate translation units in parallel.
+// Compiled once per shape, with -DRLN_HIDDEN=<H> for a specialized hidden
+// size or -DRLN_WIDE_V=<V> -DRLN_WIDE_P=<P> for a run-time one.
 #include "rln_device.h"
 
-#ifndef RLN_HIDDEN
-#error "compile with -DRLN_HIDDEN=<hidden size>"
+#if defined(RLN_HIDDEN)
+#define RLN_SHAPE FixedShape<RLN_HIDDEN>
+#elif defined(RLN_WIDE_V) && defined(RLN_WIDE_P)
+#define RLN_SHAPE WideShape<RLN_WIDE_V, RLN_WIDE_P>
+#else
+#error "compile with -DRLN_HIDDEN=<H> or -DRLN_WIDE_V=<V> -DRLN_WIDE_P=<P>"
 #endif
 
 namespace rln {
 
-template int launch_forward_hidden<RLN_HIDDEN>(const ForwardArgs&, int, int, bool);
-template int launch_backward_hidden<RLN_HIDDEN>(const BackwardArgs&, int, int, bool);
+template int launch_forward_shape<RLN_SHAPE>(const ForwardArgs&, RLN_SHAPE, int, int, bool);
+template int launch_backward_shape<RLN_SHAPE>(const BackwardArgs&, RLN_SHAPE, int, int, bool);
 
 }  // namespace rln

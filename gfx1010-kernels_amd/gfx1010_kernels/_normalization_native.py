@@ -16,7 +16,18 @@ from functools import lru_cache
 # HIP runtime (libamdhip64.so.7) from the already-loaded copies.
 import torch  # noqa: F401
 
-NATIVE_HIDDEN_SIZES = (128, 256, 384, 512, 768, 1024)
+# Hidden sizes the native path serves: the reference's six (specialized
+# kernels, reference normalization.py:12) and every other multiple of 64 up to
+# 8192 (kernels with a run-time row length).
+SPECIALIZED_HIDDEN_SIZES = (128, 256, 384, 512, 768, 1024)
+MIN_NATIVE_HIDDEN_SIZE = 128
+MAX_NATIVE_HIDDEN_SIZE = 8192
+NATIVE_HIDDEN_MULTIPLE = 64
+NATIVE_HIDDEN_SIZES = tuple(
+    range(MIN_NATIVE_HIDDEN_SIZE, MAX_NATIVE_HIDDEN_SIZE + 1, NATIVE_HIDDEN_MULTIPLE))
+NATIVE_HIDDEN_SIZES_TEXT = (
+    f"the multiples of {NATIVE_HIDDEN_MULTIPLE} from {MIN_NATIVE_HIDDEN_SIZE} "
+    f"to {MAX_NATIVE_HIDDEN_SIZE}")
 TARGET_ARCHITECTURE = "gfx950"
 
 # Interface-compatibility launch hints (threads, block_rows, parameter_threads,
@@ -70,6 +81,7 @@ def native_residual_layer_norm(
 
 __all__ = [
     "NATIVE_HIDDEN_SIZES",
+    "SPECIALIZED_HIDDEN_SIZES",
     "TARGET_ARCHITECTURE",
     "native_extension_status",
     "native_residual_layer_norm",

@@ -21,7 +21,10 @@ Dispatch rules (same order and messages as the reference):
   whose native extension cannot be loaded, ``auto`` raises instead of falling
   back, so a broken install on the target hardware is never silently served by
   the slow path;
-* ``"triton"`` is not part of this build and raises ``RuntimeError``.
+* ``"triton"`` is not part of this build and raises ``RuntimeError``;
+* the native path serves every multiple of 64 from 128 to 8192 (the reference
+  compiles 128, 256, 384, 512, 768 and 1024 only, reference :12), so ``auto``
+  accepts hidden sizes up to 8192 where the reference stops at 1024 (:118-120).
 """
 
 from __future__ import annotations
@@ -32,17 +35,23 @@ import warnings
 import torch
 from torch.nn import functional as F
 
-from ._normalization_native import NATIVE_HIDDEN_SIZES, TARGET_ARCHITECTURE
+from ._normalization_native import (
+    MAX_NATIVE_HIDDEN_SIZE,
+    NATIVE_HIDDEN_SIZES,
+    NATIVE_HIDDEN_SIZES_TEXT,
+    TARGET_ARCHITECTURE,
+)
 from ._ops import residual_layer_norm_op
 from ._status import BackendStatus
 
 MIN_HIDDEN_SIZE = 128
-MAX_HIDDEN_SIZE = 1024
+MAX_HIDDEN_SIZE = MAX_NATIVE_HIDDEN_SIZE
 
 IMPLEMENTATIONS = ("auto", TARGET_ARCHITECTURE, "gfx1010", "triton", "torch")
 BRANCH_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 NORMALIZED_DTYPES = (torch.float32, torch.float16, torch.bfloat16)
 _STRICT_NATIVE = frozenset({TARGET_ARCHITECTURE, "gfx1010"})
+_NATIVE_SIZES = frozenset(NATIVE_HIDDEN_SIZES)
 _UNAVAILABLE = f"{TARGET_ARCHITECTURE} native residual LayerNorm is unavailable"
 
 
@@ -151,7 +160,7 @@ def _input_reason(x, branch, weight, bias, dropout_p, eps):
 def can_use_residual_layer_norm(x, branch, weight, bias, dropout_p=0.0, eps=1e-5):
     """True when ``residual_layer_norm(..., implementation="auto")`` runs natively."""
     reason = _input_reason(x, branch, weight, bias, dropout_p, eps)
-    if reason is not None or x.shape[-1] not in NATIVE_HIDDEN_SIZES:
+    if reason is not None or x.shape[-1] not in _NATIVE_SIZES:
         return False
     return residual_layer_norm_status(x.device).available
 
@@ -161,9 +170,9 @@ def _strict_native(x, branch, weight, bias, dropout_p, eps, training, normalized
         raise RuntimeError(f"{_UNAVAILABLE}: x must be a HIP tensor")
     if x.ndim == 0:
         raise RuntimeError(f"{_UNAVAILABLE}: x must have at least two dimensions")
-    if x.shape[-1] not in NATIVE_HIDDEN_SIZES:
+    if x.shape[-1] not in _NATIVE_SIZES:
         raise RuntimeError(
-            f"{_UNAVAILABLE}: native hidden size must be one of {NATIVE_HIDDEN_SIZES}"
+            f"{_UNAVAILABLE}: native hidden size must be one of {NATIVE_HIDDEN_SIZES_TEXT}"
         )
     status = residual_layer_norm_status(x.device)
     if not status.available:
@@ -192,14 +201,14 @@ def _traced(x, branch, weight, bias, dropout_p, eps, training, normalized_dtype,
     the registered custom op (``gfx1010_kernels::rln_forward``) so the graph
     keeps them; the backend status is not queried (the op raises at run time
     if the extension is missing) and ``auto`` falls back without a warning."""
-    native = x.is_cuda and x.ndim >= 2 and x.shape[-1] in NATIVE_HIDDEN_SIZES
+    native = x.is_cuda and x.ndim >= 2 and x.shape[-1] in _NATIVE_SIZES
     args = (x, branch, weight, bias, dropout_p, eps, training, normalized_dtype)
     if implementation in _STRICT_NATIVE:
         if not x.is_cuda:
             raise RuntimeError(f"{_UNAVAILABLE}: x must be a HIP tensor")
         if not native:
             raise RuntimeError(
-                f"{_UNAVAILABLE}: native hidden size must be one of {NATIVE_HIDDEN_SIZES}"
+                f"{_UNAVAILABLE}: native hidden size must be one of {NATIVE_HIDDEN_SIZES_TEXT}"
             )
         return residual_layer_norm_op(*args)
     if implementation == "triton":
@@ -256,8 +265,8 @@ def residual_layer_norm(
         )
     if reason is not None:
         return _fall_back(reason, *args)
-    if x.shape[-1] not in NATIVE_HIDDEN_SIZES:
-        return _fall_back(f"native hidden size must be one of {NATIVE_HIDDEN_SIZES}", *args)
+    if x.shape[-1] not in _NATIVE_SIZES:
+        return _fall_back(f"native hidden size must be one of {NATIVE_HIDDEN_SIZES_TEXT}", *args)
     status = residual_layer_norm_status(x.device)
     if not status.available:
         if status.architecture == TARGET_ARCHITECTURE:

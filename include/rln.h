@@ -160,10 +160,14 @@ uint64_t rln_philox_increment(int64_t hidden);
 /* Number of uint32 dropout-mask words for [rows, hidden]. */
 int64_t rln_mask_words(int64_t rows, int64_t hidden);
 
-/* 1 if `hidden` has a compiled specialization, else 0. */
+/* 1 if the library serves rows of `hidden` values, else 0: the reference's
+ * sizes 128, 256, 384, 512, 768 and 1024 (specialized kernels) and every
+ * other multiple of 64 from 128 to 8192 (kernels with a run-time row length;
+ * the reference compiles only the six). */
 int rln_hidden_supported(int64_t hidden);
 
-/* Writes up to `capacity` supported hidden sizes; returns how many exist. */
+/* Writes up to `capacity` supported hidden sizes in ascending order; returns
+ * how many exist. */
 int rln_supported_hidden_sizes(int64_t* out, int capacity);
 
 /* Thread-local message for the last failed call on this thread. */

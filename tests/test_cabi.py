@@ -39,8 +39,9 @@ def test_library_metadata():
     assert _cabi.supported_hidden_sizes() == NATIVE_HIDDEN_SIZES
     for hidden in NATIVE_HIDDEN_SIZES:
         assert library.rln_hidden_supported(hidden) == 1
-    for hidden in (0, 64, 160, 2048):
+    for hidden in (0, 32, 64, 100, 160, 1000, 8256, 16384):
         assert library.rln_hidden_supported(hidden) == 0
+    assert NATIVE_HIDDEN_SIZES == tuple(range(128, 8193, 64))
 
 
 def test_philox_struct_layout():
@@ -59,6 +60,13 @@ def test_size_queries():
     assert _cabi.backward_workspace_bytes(37, 128, True) == 3 * 2 * 128 * 4
     assert _cabi.backward_workspace_bytes(41, 768, True) == 6 * 2 * 768 * 4
     assert _cabi.backward_workspace_bytes(1 << 20, 1024, True) == 256 * 2 * 1024 * 4
+    # Run-time row lengths: one wave per row up to 1024, else 2, 4 or 8 waves
+    # per row (4, 2 or 1 rows per 8-wave block).
+    assert _cabi.backward_workspace_bytes(41, 640, True) == 6 * 2 * 640 * 4
+    assert _cabi.backward_workspace_bytes(41, 2048, True) == 11 * 2 * 2048 * 4
+    assert _cabi.backward_workspace_bytes(41, 4096, True) == 21 * 2 * 4096 * 4
+    assert _cabi.backward_workspace_bytes(41, 8192, True) == 41 * 2 * 8192 * 4
+    assert _cabi.backward_workspace_bytes(8192, 8192, True) == 256 * 2 * 8192 * 4
 
 
 FAKE = 1 << 20  # a non-null address; validation fails before it is touched

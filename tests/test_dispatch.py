@@ -164,7 +164,7 @@ def test_auto_falls_back_for_non_native_hidden_size(monkeypatch):
         (lambda t: t.update(branch=t["branch"].double()), "float16, bfloat16 or float32"),
         (lambda t: t.update(weight=t["weight"][:-8]), "match the final tensor dimension"),
         (lambda t: t.update(x=t["x"][:, :120].contiguous(), branch=t["branch"][:, :120].contiguous(),
-                            weight=t["weight"][:120], bias=t["bias"][:120]), "between 128 and 1024"),
+                            weight=t["weight"][:120], bias=t["bias"][:120]), "between 128 and 8192"),
         (lambda t: t.update(x=t["x"].t().contiguous().t()), "contiguous"),
         (lambda t: t.update(dropout_p=1.0), r"\[0, 1\)"),
         (lambda t: t.update(eps=0.0), "eps must be positive"),

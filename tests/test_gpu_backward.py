@@ -14,7 +14,7 @@ import torch
 
 from gfx1010_kernels import _C, residual_layer_norm
 from parity import (
-    NATIVE_HIDDEN_SIZES,
+    SPECIALIZED_HIDDEN_SIZES,
     assert_bitwise,
     check_backward,
     check_forward,
@@ -50,7 +50,7 @@ def raw_backward(grad_updated, grad_normalized, outputs, weight, dropout_p, bran
         dropout_p, training, branch_is_half, 128, 64, 64, 1, parameters, **extra)
 
 
-@pytest.mark.parametrize("hidden", NATIVE_HIDDEN_SIZES)
+@pytest.mark.parametrize("hidden", SPECIALIZED_HIDDEN_SIZES)
 @pytest.mark.parametrize("branch_dtype", [torch.float16, torch.bfloat16, torch.float32],
                          ids=["f16", "bf16", "f32"])
 @pytest.mark.parametrize("dropout_p", [0.0, 0.15])

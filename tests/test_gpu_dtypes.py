@@ -12,7 +12,7 @@ import torch
 from gfx1010_kernels import _C, residual_layer_norm
 from oracle import rln_oracle as oracle
 from parity import (
-    NATIVE_HIDDEN_SIZES,
+    SPECIALIZED_HIDDEN_SIZES,
     assert_bitwise,
     check_backward,
     check_forward,
@@ -27,7 +27,7 @@ HALF = [torch.float16, torch.bfloat16]
 BRANCHES = [torch.float16, torch.bfloat16, torch.float32]
 
 
-@pytest.mark.parametrize("hidden", NATIVE_HIDDEN_SIZES)
+@pytest.mark.parametrize("hidden", SPECIALIZED_HIDDEN_SIZES)
 @pytest.mark.parametrize("normalized_dtype", HALF, ids=["f16", "bf16"])
 @pytest.mark.parametrize("branch_dtype", BRANCHES, ids=["b16", "bbf16", "b32"])
 def test_half_normalized_forward_and_backward(hidden, normalized_dtype, branch_dtype):

@@ -11,7 +11,7 @@ import torch
 
 from gfx1010_kernels import _C, residual_layer_norm
 from parity import (
-    NATIVE_HIDDEN_SIZES,
+    SPECIALIZED_HIDDEN_SIZES,
     assert_bitwise,
     check_forward,
     generator_state,
@@ -28,7 +28,7 @@ MODES = {
 }
 
 
-@pytest.mark.parametrize("hidden", NATIVE_HIDDEN_SIZES)
+@pytest.mark.parametrize("hidden", SPECIALIZED_HIDDEN_SIZES)
 @pytest.mark.parametrize("branch_dtype", [torch.float16, torch.bfloat16, torch.float32],
                          ids=["f16", "bf16", "f32"])
 @pytest.mark.parametrize("mode", list(MODES))
@@ -99,9 +99,10 @@ def test_raw_forward_rejects_invalid_inputs_on_gpu():
     x, branch, weight, bias = make_inputs((4, 768), torch.float16, seed=1)
     with pytest.raises(RuntimeError, match="empty tensors are unsupported"):
         _C.residual_layer_norm_forward(x[:0], branch[:0], weight, bias, 0.0, 1e-5, True, 128)
-    with pytest.raises(RuntimeError, match="unsupported native hidden size: 640"):
-        big = torch.zeros(4, 640, device=x.device)
-        _C.residual_layer_norm_forward(big, big, big[0], big[0], 0.0, 1e-5, True, 128)
+    for hidden in (96, 640 + 32, 8192 + 64):
+        with pytest.raises(RuntimeError, match=f"unsupported native hidden size: {hidden}"):
+            big = torch.zeros(4, hidden, device=x.device)
+            _C.residual_layer_norm_forward(big, big, big[0], big[0], 0.0, 1e-5, True, 128)
     with pytest.raises(RuntimeError, match="threads must be 128, 192 or 256"):
         _C.residual_layer_norm_forward(x, branch, weight, bias, 0.0, 1e-5, True, 64)
     with pytest.raises(RuntimeError, match="all tensors must be contiguous"):

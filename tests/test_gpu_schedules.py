@@ -2,7 +2,8 @@
 
 The library walks a launch's rows with one row of look-ahead when it is
 small and paced (each row's loads issued after the previous row is stored,
-slice by slice) from 2^23 elements at hidden >= 256. Every output of a row
+slice by slice) from 2^23 elements at hidden >= 256 (multi-wave rows
+included). Every output of a row
 except the weight/bias sums depends on that row alone, so the first rows of
 a paced launch must equal, bit for bit, a look-ahead launch over just those
 rows; the sums of the paced launch are checked against a float64 reduction
@@ -99,7 +100,7 @@ def check_parameter_sums(out, grad_normalized, rows, chunk=16384):
 ROW_OUTPUTS = ("updated", "normalized", "mean", "rstd", "grad_x", "grad_branch")
 
 
-@pytest.mark.parametrize("hidden", [256, 768, 1024])
+@pytest.mark.parametrize("hidden", [256, 768, 1024, 1280, 8192])
 @pytest.mark.parametrize("branch_dtype,normalized_dtype",
                          [(torch.float16, torch.float32), (torch.bfloat16, torch.bfloat16),
                           (torch.float32, torch.float16)], ids=["f16-f32", "bf16-bf16", "f32-f16"])
