@@ -35,6 +35,7 @@ def test_public_surface():
     assert set(gfx1010_kernels.__all__) == {
         "__version__", "BackendStatus", "can_use_residual_layer_norm",
         "residual_layer_norm", "residual_layer_norm_status",
+        "prenorm_forward", "residual_norm",
     }
     assert callable(gfx1010_kernels.residual_layer_norm_status)
     status = BackendStatus(True, "dev", "gfx950", "ready")
