@@ -24,6 +24,9 @@ Prints one JSON line:
                so that its saved forward state is no longer cache resident
   cpu_baseline the reference's CPU decomposition (F.dropout + add +
                F.layer_norm, forward + autograd) on this host's cores
+  step_us_spread  p20 / median / p80 of the step time over batches of 25
+  copy_ceiling    a plain device copy's GB/s at ~100 MB per launch, the
+               practical streaming ceiling on this box
 
 ``--sweep`` adds one JSON line per other BASELINE.json configuration (C0, the
 C2 hidden-size sweep, C3 deterministic, the C4 cases), each with the same
@@ -316,9 +319,15 @@ class Runner:
         base = warmup
         step_ms = self.timed(lambda i: self.step(base + i), steps)
         base += steps
+        # Spread: the same steps timed in batches of 25 (p20 / median / p80
+        # of the per-batch step time).
+        batches = []
+        for _ in range(max(steps // 25, 4)):
+            batches.append(self.timed(lambda i: self.step(base + i), 25))
+            base += 25
         forward_ms = self.timed(lambda i: self.forward(base + i), steps)
         base += steps
-        result = {"step_ms": step_ms, "forward_ms": forward_ms}
+        result = {"step_ms": step_ms, "forward_ms": forward_ms, "step_batches_ms": batches}
         if w.backward:
             # Every set now holds the saved state of a forward; re-running the
             # backward on it is the same work as the step's backward.
@@ -334,6 +343,41 @@ class Runner:
 
             result["cold_ms"] = self.timed(cold, steps)
         return result
+
+
+def copy_ceiling(torch, stream, mib: int = 50, copies: int = 200) -> dict:
+    """A plain device copy (torch copy_) of `mib` MiB, four buffer pairs in
+    rotation (400 MiB of sources, beyond the 256 MB MALL), back to back on
+    the bench stream: the streaming ceiling the op's kernels compare with."""
+    elements = mib * (1 << 20) // 4
+    pairs = [(torch.ones(elements, device="cuda"), torch.empty(elements, device="cuda"))
+             for _ in range(4)]
+    with torch.cuda.stream(stream):
+        for source, target in pairs:
+            target.copy_(source)
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record(stream)
+        for index in range(copies):
+            source, target = pairs[index % 4]
+            target.copy_(source)
+        end.record(stream)
+        end.synchronize()
+    us = start.elapsed_time(end) * 1e3 / copies
+    moved = 2 * elements * 4
+    return {"gbps": round(moved / (us * 1e-6) / 1e9, 1), "us_per_copy": round(us, 3),
+            "bytes_moved": moved, "kind": f"torch copy_ of {mib} MiB, 4 buffer pairs rotated"}
+
+
+def percentiles_us(batches_ms) -> dict:
+    ordered = sorted(batches_ms)
+
+    def pick(fraction):
+        return round(ordered[min(len(ordered) - 1, int(fraction * len(ordered)))] * 1e3, 3)
+
+    return {"p20": pick(0.2), "median": round(statistics.median(ordered) * 1e3, 3),
+            "p80": pick(0.8), "batches": len(ordered), "steps_per_batch": 25}
 
 
 def gbps(nbytes: int, ms: float) -> float:
@@ -394,6 +438,7 @@ def result_line(torch, workload: Workload, timing: dict, steps: int, warmup: int
             "parallelism": "single GPU",
         },
         "pct_of_peak": round(100.0 * value / HBM_PEAK_GBPS, 2),
+        "step_us_spread": percentiles_us(timing["step_batches_ms"]),
         "rows_per_s": round(workload.rows / (timing["step_ms"] * 1e-3), 1),
         "fwd_gbps": round(forward_gbps, 2),
         "fwd_pct_of_peak": round(100.0 * forward_gbps / HBM_PEAK_GBPS, 2),
@@ -462,6 +507,7 @@ def main() -> int:
               f"{timing['forward_ms'] * 1e3:.2f} us, backward {timing['backward_ms'] * 1e3:.2f} us, "
               f"cold step {timing['cold_ms'] * 1e3:.2f} us", flush=True)
     result = result_line(torch, C1, timing, args.steps, args.warmup, args.sets, traffic)
+    result["copy_ceiling"] = copy_ceiling(torch, stream)
     if not args.no_cpu_baseline:
         print(f"[bench] CPU baseline (~{args.cpu_seconds:.0f} s)", flush=True)
         result["cpu_baseline"] = cpu_baseline(torch, C1, args.cpu_seconds)
