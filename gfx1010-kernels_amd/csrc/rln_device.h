@@ -217,11 +217,28 @@ inline int64_t backward_blocks(int64_t rows, int64_t hidden) {
     return launch_blocks(rows, hidden, kBackwardThreads, kBackwardMaxBlocks, 1);
 }
 
-// 1 if a launch over rows x hidden walks its rows paced (measured on MI355X:
-// faster from about 8 M elements at hidden >= 256, neutral below, slower at
-// C1-sized launches), 0 for look-ahead.
-inline int paced_schedule(int64_t rows, int64_t hidden) {
-    return hidden >= kPacedMinHidden && rows * hidden >= kPacedElements ? 1 : 0;
+// 1 if a launch over rows x hidden walks its rows paced, 0 for look-ahead.
+// Measured on MI355X: paced is faster from about 8 M elements for one-wave
+// rows of 256 or more columns (backward up to 12 % at 200 M elements), and
+// slower at C1-sized launches. Multi-wave rows gain from it only in the
+// forward, from about 64 M elements, and not with 8 waves of 4 slots (one
+// block per CU, where look-ahead is up to 19 % faster); their backward is
+// faster with look-ahead at every size measured (up to 24 %).
+inline int forward_paced(int64_t rows, int64_t hidden) {
+    const ShapeInfo info = shape_info(hidden);
+    const int64_t elements = rows * hidden;
+    if (hidden < kPacedMinHidden || elements < kPacedElements) {
+        return 0;
+    }
+    if (info.parts == 1) {
+        return 1;
+    }
+    return elements >= 8 * kPacedElements && !(info.parts == 8 && info.vectors == 4) ? 1 : 0;
+}
+
+inline int backward_paced(int64_t rows, int64_t hidden) {
+    return hidden >= kPacedMinHidden && rows * hidden >= kPacedElements
+        && shape_info(hidden).parts == 1 ? 1 : 0;
 }
 
 // ----------------------------------------------------------------------------
@@ -594,13 +611,19 @@ void rln_forward_kernel(
     // past the end reads the last row instead, an idle slot its row's first
     // columns, and both are discarded), so the compiler can count them and
     // wait for exactly the ones a computation needs; a load under a branch
-    // makes it wait for all.
+    // makes it wait for all. Paced loads wait slice by slice anyway, so they
+    // skip idle slots (10 % faster at H = 896).
     auto load_row = [&](ForwardRow<V, B>& r, int64_t row, bool wait_slices) {
         const int64_t source = row < rows ? row : rows - 1;
         const float* x_row = x + source * hidden;
         const B* branch_row = branch + source * hidden;
 #pragma unroll
         for (int v = 0; v < V; ++v) {
+            if (wait_slices && !slots.active(v)) {
+                r.x[v] = zero4();
+                r.branch[v] = typename Vector4<B>::type{};
+                continue;
+            }
             const int column = slots.column(v);
             r.x[v] = load4<Aligned>(x_row + column);
             r.branch[v] = load_raw4<B, Aligned>(branch_row + column);
@@ -807,7 +830,8 @@ void rln_backward_kernel(
     // needs (a load under a branch makes it wait for all): an absent input
     // reads the row of `updated` in its place, a row past the end reads the
     // last row, an idle slot its row's first columns; process_row discards
-    // what it read.
+    // what it read. (Unlike the forward, skipping idle slots in paced loads
+    // measured slower here: 9 % at H = 640 and 896.)
     auto load_row = [&](BackwardRow<V, GY>& r, int64_t row, bool wait_slices) {
         const int64_t source = row < rows ? row : rows - 1;
         const int64_t base = source * hidden;
@@ -1046,7 +1070,7 @@ int launch_forward(const ForwardArgs& a, S shape) {
         a.scale,
         a.threshold,
         a.philox,
-        paced_schedule(a.rows, shape.hidden()));
+        forward_paced(a.rows, shape.hidden()));
     return check_launch("rln_forward_kernel");
 }
 
@@ -1070,7 +1094,7 @@ int launch_backward(const BackwardArgs& a, S shape) {
         shape,
         a.flags,
         a.scale,
-        paced_schedule(a.rows, shape.hidden()));
+        backward_paced(a.rows, shape.hidden()));
     return check_launch("rln_backward_kernel");
 }
 
