@@ -392,7 +392,10 @@ def kernel_name(kernel: str, workload: Workload) -> str:
     names it): its row shape, branch type, normalized / gradient type, and the
     aligned access path."""
     if workload.hidden in SPECIALIZED_HIDDEN:
-        shape = f"rln::FixedShape<{workload.hidden}>"
+        lanes = 64 if (workload.hidden // 4) % 64 == 0 else 32
+        if kernel == "rln_forward_kernel" and workload.hidden in (128, 256):
+            lanes = workload.hidden // 8
+        shape = f"rln::FixedShape<{workload.hidden}, {lanes}>"
     else:
         parts = 1 if workload.hidden <= 1024 else 2 if workload.hidden <= 2048 else (
             4 if workload.hidden <= 4096 else 8)

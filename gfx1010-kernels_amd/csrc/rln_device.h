@@ -112,9 +112,10 @@ int check_launch(const char* what);
 // team of lanes owns the row, and vector j of the row sits in slot v of lane
 // l of part p, with j = (v * kParts + p) * kLanes + l.
 //
-//  * FixedShape<H>: the reference's hidden sizes, known at compile time. One
-//    wave owns a row, or half a wave (32 lanes) when H/4 is not a multiple
-//    of 64 (H = 128, 384); every slot holds columns.
+//  * FixedShape<H, Lanes>: the reference's hidden sizes, known at compile
+//    time. A wave owns a row, or 32 or 16 lanes own it (two or four rows per
+//    wave); every slot holds columns. The forward and the backward may split
+//    a row differently (row_lanes): the layouts in memory do not depend on it.
 //  * WideShape<V, P>: every other multiple of 64 from kMinHidden to
 //    kMaxHidden, passed at run time. P waves own a row (P > 1 add their row
 //    sums through LDS), V slots per lane; slots past the end of the row
@@ -125,15 +126,30 @@ constexpr int64_t kMinHidden = 128;
 constexpr int64_t kMaxHidden = 8192;
 constexpr int64_t kHiddenMultiple = 64;
 
-template <int H>
+// Lanes per row of a specialized hidden size: a whole wave when H/4 is a
+// multiple of 64, else half a wave; the forward gives H = 128 and 256 two
+// slots per lane instead (16 and 32 lanes per row: 6-12 % faster on MI355X;
+// the backward is faster with one slot).
+constexpr int row_lanes(int64_t hidden, bool forward) {
+    if (forward && hidden == 128) {
+        return 16;
+    }
+    if (forward && hidden == 256) {
+        return 32;
+    }
+    return ((hidden / 4) % kWaveSize == 0) ? 64 : 32;
+}
+
+template <int H, int Lanes>
 struct FixedShape {
-    static constexpr int kLanes = ((H / 4) % kWaveSize == 0) ? 64 : 32;
+    static constexpr int kLanes = Lanes;
     static constexpr int kV = (H / 4) / kLanes;
     static constexpr int kParts = 1;
     static constexpr int kRowsPerWave = kWaveSize / kLanes;
     static constexpr bool kRagged = false;
     static constexpr int kForwardThreads = 256;
-    static_assert(H % 64 == 0 && (H / 4) % kLanes == 0, "row must split evenly over lanes");
+    static_assert(H % 64 == 0 && (H / 4) % kLanes == 0 && kLanes >= 16,
+                  "row must split evenly over lanes");
     __host__ __device__ constexpr int64_t hidden() const { return H; }
     __host__ __device__ constexpr float inv_hidden() const {
         return 1.0f / static_cast<float>(H);
@@ -178,11 +194,15 @@ struct ShapeInfo {
     int forward_threads;
 };
 
-inline ShapeInfo shape_info(int64_t hidden) {
+template <int H>
+using ForwardFixed = FixedShape<H, row_lanes(H, true)>;
+template <int H>
+using BackwardFixed = FixedShape<H, row_lanes(H, false)>;
+
+inline ShapeInfo shape_info(int64_t hidden, bool forward) {
     if (specialized_hidden(hidden)) {
-        const int rows_per_wave = ((hidden / 4) % kWaveSize == 0) ? 1 : 2;
-        return {rows_per_wave, 1, static_cast<int>(hidden / 4 / (kWaveSize / rows_per_wave)),
-                256};
+        const int lanes = row_lanes(hidden, forward);
+        return {kWaveSize / lanes, 1, static_cast<int>(hidden / 4 / lanes), 256};
     }
     const int parts = hidden <= 1024 ? 1 : hidden <= 2048 ? 2 : hidden <= 4096 ? 4 : 8;
     const int64_t per_slot = 4 * kWaveSize * parts;
@@ -194,9 +214,8 @@ inline ShapeInfo shape_info(int64_t hidden) {
 // (threads / 64) * rows_per_wave / parts rows at a time, and gets enough
 // blocks for `iterations` such steps, capped; a function of (rows, hidden)
 // only.
-inline int64_t launch_blocks(int64_t rows, int64_t hidden, int threads, int64_t cap,
+inline int64_t launch_blocks(int64_t rows, const ShapeInfo& info, int threads, int64_t cap,
                              int64_t iterations) {
-    const ShapeInfo info = shape_info(hidden);
     const int64_t rows_per_block = (threads / kWaveSize) * info.rows_per_wave / info.parts;
     const int64_t steps = (rows + rows_per_block - 1) / rows_per_block;
     const int64_t blocks = (steps + iterations - 1) / iterations;
@@ -207,14 +226,15 @@ inline int64_t launch_blocks(int64_t rows, int64_t hidden, int threads, int64_t 
 // look-ahead load overlaps a row's computation; with 256-thread blocks and
 // ~100 VGPRs per lane the cap of 2048 blocks is two waves of residency.
 inline int64_t forward_blocks(int64_t rows, int64_t hidden) {
-    return launch_blocks(rows, hidden, shape_info(hidden).forward_threads, kForwardMaxBlocks,
+    const ShapeInfo info = shape_info(hidden, true);
+    return launch_blocks(rows, info, info.forward_threads, kForwardMaxBlocks,
                          RLN_FWD_GROUPS_PER_WAVE);
 }
 
 // The backward's grid is also the number of weight/bias partials: at most
 // 256 blocks of 8 waves, one block per CU.
 inline int64_t backward_blocks(int64_t rows, int64_t hidden) {
-    return launch_blocks(rows, hidden, kBackwardThreads, kBackwardMaxBlocks, 1);
+    return launch_blocks(rows, shape_info(hidden, false), kBackwardThreads, kBackwardMaxBlocks, 1);
 }
 
 // 1 if a launch over rows x hidden walks its rows paced, 0 for look-ahead.
@@ -225,7 +245,7 @@ inline int64_t backward_blocks(int64_t rows, int64_t hidden) {
 // block per CU, where look-ahead is up to 19 % faster); their backward is
 // faster with look-ahead at every size measured (up to 24 %).
 inline int forward_paced(int64_t rows, int64_t hidden) {
-    const ShapeInfo info = shape_info(hidden);
+    const ShapeInfo info = shape_info(hidden, true);
     const int64_t elements = rows * hidden;
     if (hidden < kPacedMinHidden || elements < kPacedElements) {
         return 0;
@@ -238,7 +258,7 @@ inline int forward_paced(int64_t rows, int64_t hidden) {
 
 inline int backward_paced(int64_t rows, int64_t hidden) {
     return hidden >= kPacedMinHidden && rows * hidden >= kPacedElements
-        && shape_info(hidden).parts == 1 ? 1 : 0;
+        && shape_info(hidden, false).parts == 1 ? 1 : 0;
 }
 
 // ----------------------------------------------------------------------------
@@ -277,6 +297,9 @@ __device__ __forceinline__ float readlane_f32(float value, int lane) {
 template <int Lanes>
 __device__ __forceinline__ float row_sum(float value) {
     value = row16_sum(value);
+    if constexpr (Lanes == 16) {
+        return value;
+    }
     const float low = readlane_f32(value, 0) + readlane_f32(value, 16);
     const float high = readlane_f32(value, 32) + readlane_f32(value, 48);
     if constexpr (Lanes == 64) {
@@ -1040,8 +1063,8 @@ struct BackwardArgs {
 // hidden size, since the grid (and so the deterministic order) is computed
 // from the latter.
 template <typename S>
-int check_shape(const S& shape) {
-    const ShapeInfo info = shape_info(shape.hidden());
+int check_shape(const S& shape, bool forward) {
+    const ShapeInfo info = shape_info(shape.hidden(), forward);
     if (info.parts != S::kParts || info.rows_per_wave != S::kRowsPerWave
         || info.vectors != S::kV || info.forward_threads != S::kForwardThreads) {
         return fail(RLN_ERR_UNSUPPORTED, "shape mismatch for hidden size %lld",
@@ -1115,7 +1138,7 @@ int with_dtype(int dtype, Launch&& launch) {
 template <typename S>
 int launch_forward_shape(const ForwardArgs& a, S shape, int branch_dtype, int normalized_dtype,
                          bool aligned) {
-    const int status = check_shape(shape);
+    const int status = check_shape(shape, true);
     if (status != RLN_OK) {
         return status;
     }
@@ -1130,7 +1153,7 @@ int launch_forward_shape(const ForwardArgs& a, S shape, int branch_dtype, int no
 template <typename S>
 int launch_backward_shape(const BackwardArgs& a, S shape, int branch_dtype,
                           int grad_normalized_dtype, bool aligned) {
-    const int status = check_shape(shape);
+    const int status = check_shape(shape, false);
     if (status != RLN_OK) {
         return status;
     }
@@ -1142,23 +1165,24 @@ int launch_backward_shape(const BackwardArgs& a, S shape, int branch_dtype,
     });
 }
 
-// Calls `launch(shape)` with the row shape of a supported hidden size.
-template <typename Launch>
+// Calls `launch(shape)` with the forward's (Forward) or the backward's row
+// shape for a supported hidden size.
+template <bool Forward, typename Launch>
 int with_shape(int64_t hidden, Launch&& launch) {
     switch (hidden) {
-        case 128: return launch(FixedShape<128>{});
-        case 256: return launch(FixedShape<256>{});
-        case 384: return launch(FixedShape<384>{});
-        case 512: return launch(FixedShape<512>{});
-        case 768: return launch(FixedShape<768>{});
-        case 1024: return launch(FixedShape<1024>{});
+        case 128: return launch(FixedShape<128, row_lanes(128, Forward)>{});
+        case 256: return launch(FixedShape<256, row_lanes(256, Forward)>{});
+        case 384: return launch(FixedShape<384, row_lanes(384, Forward)>{});
+        case 512: return launch(FixedShape<512, row_lanes(512, Forward)>{});
+        case 768: return launch(FixedShape<768, row_lanes(768, Forward)>{});
+        case 1024: return launch(FixedShape<1024, row_lanes(1024, Forward)>{});
         default: break;
     }
     if (!hidden_supported(hidden)) {
         return fail(RLN_ERR_UNSUPPORTED, "unsupported native hidden size: %lld",
                     static_cast<long long>(hidden));
     }
-    const ShapeInfo info = shape_info(hidden);
+    const ShapeInfo info = shape_info(hidden, Forward);
     const float inv_hidden = 1.0f / static_cast<float>(hidden);
     switch (info.parts * 16 + info.vectors) {
         case 1 * 16 + 1: return launch(WideShape<1, 1>{hidden, inv_hidden});
@@ -1178,16 +1202,20 @@ int with_shape(int64_t hidden, Launch&& launch) {
 }
 
 // The row shapes, one translation unit each (rln_hidden.hip).
-#define RLN_FOR_EACH_SHAPE(X)                                                     \
-    X(FixedShape<128>) X(FixedShape<256>) X(FixedShape<384>) X(FixedShape<512>)   \
-    X(FixedShape<768>) X(FixedShape<1024>) X(RLN_WIDE(1, 1)) X(RLN_WIDE(2, 1))   \
-    X(RLN_WIDE(3, 1)) X(RLN_WIDE(4, 1)) X(RLN_WIDE(3, 2)) X(RLN_WIDE(4, 2))       \
-    X(RLN_WIDE(3, 4)) X(RLN_WIDE(4, 4)) X(RLN_WIDE(3, 8)) X(RLN_WIDE(4, 8))
-#define RLN_WIDE(V, P) WideShape<V, P>
+#define RLN_FOR_EACH_FIXED(X) X(128) X(256) X(384) X(512) X(768) X(1024)
+#define RLN_FOR_EACH_WIDE(X) \
+    X(1, 1) X(2, 1) X(3, 1) X(4, 1) X(3, 2) X(4, 2) X(3, 4) X(4, 4) X(3, 8) X(4, 8)
 
-#define RLN_DECLARE_SHAPE(S)                                                                  \
-    extern template int launch_forward_shape<S>(const ForwardArgs&, S, int, int, bool);      \
-    extern template int launch_backward_shape<S>(const BackwardArgs&, S, int, int, bool);
+#define RLN_DECLARE_FIXED(H)                                                              \
+    extern template int launch_forward_shape<ForwardFixed<H>>(                           \
+        const ForwardArgs&, ForwardFixed<H>, int, int, bool);                             \
+    extern template int launch_backward_shape<BackwardFixed<H>>(                         \
+        const BackwardArgs&, BackwardFixed<H>, int, int, bool);
+#define RLN_DECLARE_WIDE(V, P)                                                            \
+    extern template int launch_forward_shape<WideShape<V, P>>(                           \
+        const ForwardArgs&, WideShape<V, P>, int, int, bool);                             \
+    extern template int launch_backward_shape<WideShape<V, P>>(                          \
+        const BackwardArgs&, WideShape<V, P>, int, int, bool);
 
 }  // namespace rln
 

@@ -5,16 +5,20 @@
 #include "rln_device.h"
 
 #if defined(RLN_HIDDEN)
-#define RLN_SHAPE FixedShape<RLN_HIDDEN>
+#define RLN_FORWARD_SHAPE ForwardFixed<RLN_HIDDEN>
+#define RLN_BACKWARD_SHAPE BackwardFixed<RLN_HIDDEN>
 #elif defined(RLN_WIDE_V) && defined(RLN_WIDE_P)
-#define RLN_SHAPE WideShape<RLN_WIDE_V, RLN_WIDE_P>
+#define RLN_FORWARD_SHAPE WideShape<RLN_WIDE_V, RLN_WIDE_P>
+#define RLN_BACKWARD_SHAPE WideShape<RLN_WIDE_V, RLN_WIDE_P>
 #else
 #error "compile with -DRLN_HIDDEN=<H> or -DRLN_WIDE_V=<V> -DRLN_WIDE_P=<P>"
 #endif
 
 namespace rln {
 
-template int launch_forward_shape<RLN_SHAPE>(const ForwardArgs&, RLN_SHAPE, int, int, bool);
-template int launch_backward_shape<RLN_SHAPE>(const BackwardArgs&, RLN_SHAPE, int, int, bool);
+template int launch_forward_shape<RLN_FORWARD_SHAPE>(const ForwardArgs&, RLN_FORWARD_SHAPE, int,
+                                                     int, bool);
+template int launch_backward_shape<RLN_BACKWARD_SHAPE>(const BackwardArgs&, RLN_BACKWARD_SHAPE,
+                                                       int, int, bool);
 
 }  // namespace rln
