@@ -393,8 +393,9 @@ def kernel_name(kernel: str, workload: Workload) -> str:
     aligned access path."""
     if workload.hidden in SPECIALIZED_HIDDEN:
         lanes = 64 if (workload.hidden // 4) % 64 == 0 else 32
-        if kernel == "rln_forward_kernel" and workload.hidden in (128, 256):
-            lanes = workload.hidden // 8
+        if kernel == "rln_forward_kernel":
+            lanes = {128: 16, 768: 32 if workload.normalized == "f32" else 64, 1024: 64}.get(
+                workload.hidden, 32)
         shape = f"rln::FixedShape<{workload.hidden}, {lanes}>"
     else:
         parts = 1 if workload.hidden <= 1024 else 2 if workload.hidden <= 2048 else (

@@ -49,6 +49,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
 
 #include "rln.h"
 
@@ -114,8 +115,9 @@ int check_launch(const char* what);
 //
 //  * FixedShape<H, Lanes>: the reference's hidden sizes, known at compile
 //    time. A wave owns a row, or 32 or 16 lanes own it (two or four rows per
-//    wave); every slot holds columns. The forward and the backward may split
-//    a row differently (row_lanes): the layouts in memory do not depend on it.
+//    wave); every slot holds columns. The forward may split a row over fewer
+//    lanes than the backward (forward_lanes): the layouts in memory do not
+//    depend on the split.
 //  * WideShape<V, P>: every other multiple of 64 from kMinHidden to
 //    kMaxHidden, passed at run time. P waves own a row (P > 1 add their row
 //    sums through LDS), V slots per lane; slots past the end of the row
@@ -126,21 +128,33 @@ constexpr int64_t kMinHidden = 128;
 constexpr int64_t kMaxHidden = 8192;
 constexpr int64_t kHiddenMultiple = 64;
 
-// Lanes per row of a specialized hidden size: a whole wave when H/4 is a
-// multiple of 64, else half a wave; the forward gives H = 128 and 256 two
-// slots per lane instead (16 and 32 lanes per row: 6-12 % faster on MI355X;
-// the backward is faster with one slot).
-constexpr int row_lanes(int64_t hidden, bool forward) {
-    if (forward && hidden == 128) {
-        return 16;
-    }
-    if (forward && hidden == 256) {
-        return 32;
-    }
+// Lanes per row of a specialized hidden size in the backward, and in the
+// shape the C ABI dispatches on: a whole wave when H/4 is a multiple of 64,
+// else half a wave.
+constexpr int fixed_lanes(int64_t hidden) {
     return ((hidden / 4) % kWaveSize == 0) ? 64 : 32;
 }
 
-template <int H, int Lanes>
+// Lanes per row in the forward, whose normalized output has type N: fewer
+// lanes with more slots each where that measured faster on MI355X (H = 128:
+// 16 lanes, 12 % faster; H = 256 and 512: 32 lanes, 2-6 %; H = 768 with fp32
+// output: 32 lanes, 3 % at C1); H = 1024, and H = 768 with a 16-bit output,
+// are faster with a whole wave. The backward measured slower with more slots.
+template <typename N>
+constexpr int forward_lanes(int64_t hidden) {
+    if (hidden == 128) {
+        return 16;
+    }
+    if (hidden == 768) {
+        return std::is_same_v<N, float> ? 32 : 64;
+    }
+    if (hidden == 1024) {
+        return 64;
+    }
+    return 32;
+}
+
+template <int H, int Lanes = fixed_lanes(H)>
 struct FixedShape {
     static constexpr int kLanes = Lanes;
     static constexpr int kV = (H / 4) / kLanes;
@@ -194,14 +208,25 @@ struct ShapeInfo {
     int forward_threads;
 };
 
-template <int H>
-using ForwardFixed = FixedShape<H, row_lanes(H, true)>;
-template <int H>
-using BackwardFixed = FixedShape<H, row_lanes(H, false)>;
+// The forward's shape for dispatch shape S and normalized type N.
+template <typename S, typename N>
+struct ForwardShape {
+    using type = S;
+};
+template <int H, int Lanes, typename N>
+struct ForwardShape<FixedShape<H, Lanes>, N> {
+    using type = FixedShape<H, forward_lanes<N>(H)>;
+};
 
-inline ShapeInfo shape_info(int64_t hidden, bool forward) {
+template <typename S>
+constexpr ShapeInfo info_of() {
+    return {S::kRowsPerWave, S::kParts, S::kV, S::kForwardThreads};
+}
+
+// The dispatch (and backward) shape of a supported hidden size.
+inline ShapeInfo shape_info(int64_t hidden) {
     if (specialized_hidden(hidden)) {
-        const int lanes = row_lanes(hidden, forward);
+        const int lanes = fixed_lanes(hidden);
         return {kWaveSize / lanes, 1, static_cast<int>(hidden / 4 / lanes), 256};
     }
     const int parts = hidden <= 1024 ? 1 : hidden <= 2048 ? 2 : hidden <= 4096 ? 4 : 8;
@@ -223,18 +248,17 @@ inline int64_t launch_blocks(int64_t rows, const ShapeInfo& info, int threads, i
 }
 
 // The forward gives each team at least two row steps so that its
-// look-ahead load overlaps a row's computation; with 256-thread blocks and
-// ~100 VGPRs per lane the cap of 2048 blocks is two waves of residency.
-inline int64_t forward_blocks(int64_t rows, int64_t hidden) {
-    const ShapeInfo info = shape_info(hidden, true);
-    return launch_blocks(rows, info, info.forward_threads, kForwardMaxBlocks,
+// look-ahead load overlaps a row's computation, with at most 2048 blocks.
+template <typename S>
+int64_t forward_blocks(int64_t rows) {
+    return launch_blocks(rows, info_of<S>(), S::kForwardThreads, kForwardMaxBlocks,
                          RLN_FWD_GROUPS_PER_WAVE);
 }
 
 // The backward's grid is also the number of weight/bias partials: at most
 // 256 blocks of 8 waves, one block per CU.
 inline int64_t backward_blocks(int64_t rows, int64_t hidden) {
-    return launch_blocks(rows, shape_info(hidden, false), kBackwardThreads, kBackwardMaxBlocks, 1);
+    return launch_blocks(rows, shape_info(hidden), kBackwardThreads, kBackwardMaxBlocks, 1);
 }
 
 // 1 if a launch over rows x hidden walks its rows paced, 0 for look-ahead.
@@ -245,7 +269,7 @@ inline int64_t backward_blocks(int64_t rows, int64_t hidden) {
 // block per CU, where look-ahead is up to 19 % faster); their backward is
 // faster with look-ahead at every size measured (up to 24 %).
 inline int forward_paced(int64_t rows, int64_t hidden) {
-    const ShapeInfo info = shape_info(hidden, true);
+    const ShapeInfo info = shape_info(hidden);
     const int64_t elements = rows * hidden;
     if (hidden < kPacedMinHidden || elements < kPacedElements) {
         return 0;
@@ -258,7 +282,7 @@ inline int forward_paced(int64_t rows, int64_t hidden) {
 
 inline int backward_paced(int64_t rows, int64_t hidden) {
     return hidden >= kPacedMinHidden && rows * hidden >= kPacedElements
-        && shape_info(hidden, false).parts == 1 ? 1 : 0;
+        && shape_info(hidden).parts == 1 ? 1 : 0;
 }
 
 // ----------------------------------------------------------------------------
@@ -1059,12 +1083,12 @@ struct BackwardArgs {
     hipStream_t stream;
 };
 
-// The kernels' template shape must be the one shape_info() describes for the
-// hidden size, since the grid (and so the deterministic order) is computed
-// from the latter.
+// The dispatch shape must be the one shape_info() describes for the hidden
+// size, since the backward's grid (and so the deterministic order and the
+// workspace size) is computed from the latter.
 template <typename S>
-int check_shape(const S& shape, bool forward) {
-    const ShapeInfo info = shape_info(shape.hidden(), forward);
+int check_shape(const S& shape) {
+    const ShapeInfo info = shape_info(shape.hidden());
     if (info.parts != S::kParts || info.rows_per_wave != S::kRowsPerWave
         || info.vectors != S::kV || info.forward_threads != S::kForwardThreads) {
         return fail(RLN_ERR_UNSUPPORTED, "shape mismatch for hidden size %lld",
@@ -1075,7 +1099,7 @@ int check_shape(const S& shape, bool forward) {
 
 template <typename S, typename B, typename N, bool Aligned>
 int launch_forward(const ForwardArgs& a, S shape) {
-    const dim3 grid(static_cast<unsigned>(forward_blocks(a.rows, shape.hidden())));
+    const dim3 grid(static_cast<unsigned>(forward_blocks<S>(a.rows)));
     rln_forward_kernel<S, B, N, Aligned><<<grid, S::kForwardThreads, 0, a.stream>>>(
         a.x,
         static_cast<const B*>(a.branch),
@@ -1138,14 +1162,19 @@ int with_dtype(int dtype, Launch&& launch) {
 template <typename S>
 int launch_forward_shape(const ForwardArgs& a, S shape, int branch_dtype, int normalized_dtype,
                          bool aligned) {
-    const int status = check_shape(shape, true);
+    const int status = check_shape(shape);
     if (status != RLN_OK) {
         return status;
     }
     return with_dtype(branch_dtype, [&]<typename B>() {
         return with_dtype(normalized_dtype, [&]<typename N>() {
-            return aligned ? launch_forward<S, B, N, true>(a, shape)
-                           : launch_forward<S, B, N, false>(a, shape);
+            using F = typename ForwardShape<S, N>::type;
+            F forward_shape{};
+            if constexpr (std::is_same_v<F, S>) {
+                forward_shape = shape;
+            }
+            return aligned ? launch_forward<F, B, N, true>(a, forward_shape)
+                           : launch_forward<F, B, N, false>(a, forward_shape);
         });
     });
 }
@@ -1153,7 +1182,7 @@ int launch_forward_shape(const ForwardArgs& a, S shape, int branch_dtype, int no
 template <typename S>
 int launch_backward_shape(const BackwardArgs& a, S shape, int branch_dtype,
                           int grad_normalized_dtype, bool aligned) {
-    const int status = check_shape(shape, false);
+    const int status = check_shape(shape);
     if (status != RLN_OK) {
         return status;
     }
@@ -1165,24 +1194,23 @@ int launch_backward_shape(const BackwardArgs& a, S shape, int branch_dtype,
     });
 }
 
-// Calls `launch(shape)` with the forward's (Forward) or the backward's row
-// shape for a supported hidden size.
-template <bool Forward, typename Launch>
+// Calls `launch(shape)` with the dispatch shape of a supported hidden size.
+template <typename Launch>
 int with_shape(int64_t hidden, Launch&& launch) {
     switch (hidden) {
-        case 128: return launch(FixedShape<128, row_lanes(128, Forward)>{});
-        case 256: return launch(FixedShape<256, row_lanes(256, Forward)>{});
-        case 384: return launch(FixedShape<384, row_lanes(384, Forward)>{});
-        case 512: return launch(FixedShape<512, row_lanes(512, Forward)>{});
-        case 768: return launch(FixedShape<768, row_lanes(768, Forward)>{});
-        case 1024: return launch(FixedShape<1024, row_lanes(1024, Forward)>{});
+        case 128: return launch(FixedShape<128>{});
+        case 256: return launch(FixedShape<256>{});
+        case 384: return launch(FixedShape<384>{});
+        case 512: return launch(FixedShape<512>{});
+        case 768: return launch(FixedShape<768>{});
+        case 1024: return launch(FixedShape<1024>{});
         default: break;
     }
     if (!hidden_supported(hidden)) {
         return fail(RLN_ERR_UNSUPPORTED, "unsupported native hidden size: %lld",
                     static_cast<long long>(hidden));
     }
-    const ShapeInfo info = shape_info(hidden, Forward);
+    const ShapeInfo info = shape_info(hidden);
     const float inv_hidden = 1.0f / static_cast<float>(hidden);
     switch (info.parts * 16 + info.vectors) {
         case 1 * 16 + 1: return launch(WideShape<1, 1>{hidden, inv_hidden});
@@ -1207,10 +1235,10 @@ int with_shape(int64_t hidden, Launch&& launch) {
     X(1, 1) X(2, 1) X(3, 1) X(4, 1) X(3, 2) X(4, 2) X(3, 4) X(4, 4) X(3, 8) X(4, 8)
 
 #define RLN_DECLARE_FIXED(H)                                                              \
-    extern template int launch_forward_shape<ForwardFixed<H>>(                           \
-        const ForwardArgs&, ForwardFixed<H>, int, int, bool);                             \
-    extern template int launch_backward_shape<BackwardFixed<H>>(                         \
-        const BackwardArgs&, BackwardFixed<H>, int, int, bool);
+    extern template int launch_forward_shape<FixedShape<H>>(                             \
+        const ForwardArgs&, FixedShape<H>, int, int, bool);                               \
+    extern template int launch_backward_shape<FixedShape<H>>(                            \
+        const BackwardArgs&, FixedShape<H>, int, int, bool);
 #define RLN_DECLARE_WIDE(V, P)                                                            \
     extern template int launch_forward_shape<WideShape<V, P>>(                           \
         const ForwardArgs&, WideShape<V, P>, int, int, bool);                             \

@@ -5,8 +5,8 @@
 #include "rln_device.h"
 
 #if defined(RLN_HIDDEN)
-#define RLN_FORWARD_SHAPE ForwardFixed<RLN_HIDDEN>
-#define RLN_BACKWARD_SHAPE BackwardFixed<RLN_HIDDEN>
+#define RLN_FORWARD_SHAPE FixedShape<RLN_HIDDEN>
+#define RLN_BACKWARD_SHAPE FixedShape<RLN_HIDDEN>
 #elif defined(RLN_WIDE_V) && defined(RLN_WIDE_P)
 #define RLN_FORWARD_SHAPE WideShape<RLN_WIDE_V, RLN_WIDE_P>
 #define RLN_BACKWARD_SHAPE WideShape<RLN_WIDE_V, RLN_WIDE_P>
