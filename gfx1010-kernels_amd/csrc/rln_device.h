@@ -1,16 +1,17 @@
 // Fused residual-add + dropout + LayerNorm for MI355X (gfx950, CDNA4): the
-// device kernels and their launchers, shared by the per-hidden-size
+// device kernels and their launchers, shared by the per-row-shape
 // translation units (rln_hidden.hip) and the C ABI (rln_api.hip, declared in
 // include/rln.h). The operator is the
 // one implemented by the reference's csrc/residual_layer_norm_kernel.hip
 // (forward :425-545, input backward :548-618, parameter backward :727-869);
 // the kernels here are organised for wave64 CDNA hardware instead:
 //
-//  * One wavefront owns one row (two rows when H/4 is not a multiple of 64,
-//    i.e. H = 128 and 384: each half-wave of 32 lanes owns a row). A lane
-//    holds kV four-element vectors of its row in registers, so both row
-//    reductions run inside the wave with DPP row operations plus
-//    v_readlane - no LDS, no barriers.
+//  * Up to 1024 columns, one wavefront, or a group of 16 or 32 of its lanes,
+//    owns a row. A lane holds kV four-element vectors of its row in
+//    registers, so both row reductions run inside the wave with DPP row
+//    operations plus v_readlane - no LDS, no barriers. Longer rows (up to
+//    8192) are split over 2, 4 or 8 waves of a block, which add their
+//    per-wave sums through LDS.
 //  * Loads and stores are 128-bit (64-bit for four fp16 values) and marked
 //    non-temporal: every byte of the op is touched exactly once per kernel,
 //    so the accesses stream through the caches instead of displacing lines
@@ -316,8 +317,9 @@ __device__ __forceinline__ float readlane_f32(float value, int lane) {
         float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, value), lane));
 }
 
-// Sum over the lanes that own one row: 64 lanes, or the 32-lane half of the
-// wave that the calling lane belongs to. Must be called by all 64 lanes.
+// Sum over the lanes that own one row: 64 lanes, the 32-lane half of the
+// wave that the calling lane belongs to, or its 16-lane DPP row. Must be
+// called by all 64 lanes.
 template <int Lanes>
 __device__ __forceinline__ float row_sum(float value) {
     value = row16_sum(value);
@@ -440,21 +442,6 @@ template <>
 struct Vector4<bf16_t> {
     using type = bf16x4;
 };
-
-// Four consecutive elements of type T (fp32, fp16 or bf16), widened to fp32.
-template <typename T, bool Aligned>
-__device__ __forceinline__ f32x4 load_convert4(const T* __restrict__ pointer) {
-    if constexpr (Aligned) {
-        return __builtin_convertvector(
-            stream_load(reinterpret_cast<const typename Vector4<T>::type*>(pointer)), f32x4);
-    } else {
-        return f32x4{
-            static_cast<float>(stream_load(pointer)),
-            static_cast<float>(stream_load(pointer + 1)),
-            static_cast<float>(stream_load(pointer + 2)),
-            static_cast<float>(stream_load(pointer + 3))};
-    }
-}
 
 // Four consecutive elements of type T in their storage type, unconverted.
 // Row loads keep this form so that no arithmetic (and hence no wait for the
