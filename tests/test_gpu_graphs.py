@@ -1,0 +1,57 @@
+"""A whole training step of the op (forward + backward) under HIP graph capture.
+
+The captured graph holds the forward, the weight/bias zeroing kernel (atomic
+mode) or the fixed-order reduce kernel (deterministic mode) and the backward;
+no memset node. Each replay, with eager work and synchronizations between
+replays, draws a fresh dropout mask from the generator and must match the
+oracle for the RNG state it consumed (the reference rejects capture,
+csrc/residual_layer_norm_kernel.hip:1758-1777).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from gfx1010_kernels import _C
+from parity import check_backward, check_forward, generator_state, host, make_grads, make_inputs
+from test_gpu_backward import deterministic_algorithms, raw_backward
+
+pytestmark = pytest.mark.gpu
+EPS = 1e-5
+
+
+@pytest.mark.parametrize("hidden", [768, 2048])
+@pytest.mark.parametrize("deterministic", [False, True], ids=["atomic", "deterministic"])
+def test_captured_training_step_replays(hidden, deterministic):
+    rows = 300
+    inputs = make_inputs((rows, hidden), torch.float16, seed=hidden)
+    grad_updated, grad_normalized = make_grads((rows, hidden), seed=hidden + 1)
+    torch.cuda.manual_seed(7)
+
+    def step():
+        outputs = _C.residual_layer_norm_forward(*inputs, 0.1, EPS, True, 128)
+        gradients = raw_backward(grad_updated, grad_normalized, outputs, inputs[2], 0.1, True)
+        return outputs, gradients
+
+    with deterministic_algorithms(deterministic):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            step()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            outputs, gradients = step()
+        masks = []
+        for replay in range(3):
+            seed, offset = generator_state()
+            graph.replay()
+            torch.cuda.synchronize()
+            keep, scale = check_forward(outputs, inputs, 0.1, True, EPS, seed, offset,
+                                        f"replay {replay}")
+            check_backward(gradients, grad_updated, grad_normalized, outputs[0], inputs[2], EPS,
+                           keep, scale, f"replay {replay}")
+            masks.append(host(outputs[4]).copy())
+            step()  # eager work between replays
+            torch.cuda.synchronize()
+    assert not np.array_equal(masks[0], masks[1]) and not np.array_equal(masks[1], masks[2])
