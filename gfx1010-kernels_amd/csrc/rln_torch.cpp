@@ -10,10 +10,10 @@
 // csrc/residual_layer_norm_kernel.hip:26-166. Two optional trailing keyword
 // arguments extend them: `normalized_dtype` (forward; float32, float16 or
 // bfloat16 normalized output) and `branch_dtype` (backward; names a bfloat16
-// branch, which the reference's `branch_is_half` flag cannot express). The reference's launch hints
-// (threads, block_rows, parameter_threads, parameter_groups) are validated
-// with the reference's messages and otherwise ignored: the MI355X library
-// picks its own launch shape.
+// branch, which the reference's `branch_is_half` flag cannot express). The
+// reference's launch hints (threads, block_rows, parameter_threads,
+// parameter_groups) are validated with the reference's messages and otherwise
+// ignored: the MI355X library picks its own launch shape.
 //
 // This file owns what the C ABI leaves to the caller: tensor allocation on
 // the caching allocator, the device guard, the current HIP stream, the
