@@ -27,6 +27,9 @@ Prints one JSON line:
   step_us_spread  p20 / median / p80 of the step time over batches of 25
   copy_ceiling    a plain device copy's GB/s at ~100 MB per launch, the
                practical streaming ceiling on this box
+  public_api      whole autograd steps through the public Python API on this
+               GPU: these kernels (implementation="gfx950") and the
+               reference's decomposition run by PyTorch-ROCm ("torch")
 
 ``--sweep`` adds one JSON line per other BASELINE.json configuration (C0, the
 C2 hidden-size sweep, C3 deterministic, the C4 cases), each with the same
@@ -162,6 +165,65 @@ def parse_args():
     return parser.parse_args()
 
 
+def public_api_steps(torch, workload: Workload, stream, steps: int = 100) -> dict:
+    """Whole autograd steps through the public API on this GPU, as a user runs
+    them: `implementation="gfx950"` (these kernels) and
+    `implementation="torch"` (the reference's decomposition, F.dropout + add +
+    F.layer_norm, run by PyTorch-ROCm on the same GPU). `eager` includes
+    Python dispatch, autograd and allocation per step; `graph` replays the
+    same step captured in a HIP graph (the op draws a fresh dropout mask on
+    every replay)."""
+    from gfx1010_kernels import residual_layer_norm
+
+    generator = torch.Generator(device="cuda").manual_seed(workload.seed)
+    shape = (workload.rows, workload.hidden)
+    branch_type = getattr(torch, DTYPE_NAMES[workload.branch])
+    x = torch.randn(shape, device="cuda", generator=generator).requires_grad_(True)
+    branch = (workload.branch_std * torch.randn(shape, device="cuda", generator=generator)).to(
+        branch_type).requires_grad_(True)
+    weight = (1.0 + 0.02 * torch.randn(workload.hidden, device="cuda",
+                                       generator=generator)).requires_grad_(True)
+    bias = (0.02 * torch.randn(workload.hidden, device="cuda",
+                               generator=generator)).requires_grad_(True)
+    grads = [torch.randn(shape, device="cuda", generator=generator) for _ in range(2)]
+    leaves = (x, branch, weight, bias)
+    total = workload.forward_bytes() + workload.backward_bytes()
+
+    def timed(body):
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record(stream)
+        for _ in range(steps):
+            body()
+        end.record(stream)
+        end.synchronize()
+        ms = start.elapsed_time(end) / steps
+        return {"us_per_step": round(ms * 1e3, 3), "gbps": round(total / (ms * 1e-3) / 1e9, 1)}
+
+    result = {}
+    with torch.cuda.stream(stream):
+        for implementation in ("gfx950", "torch"):
+            def step():
+                updated, normalized = residual_layer_norm(
+                    x, branch, weight, bias, dropout_p=workload.dropout_p, eps=EPS,
+                    training=workload.training, implementation=implementation)
+                return torch.autograd.grad((updated, normalized), leaves, grads)
+
+            for _ in range(10):
+                step()
+            eager = timed(step)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                step()
+            graph.replay()
+            result[implementation] = {"eager": eager, "graph": timed(graph.replay)}
+            del graph
+    result["kind"] = ("fwd+bwd through residual_layer_norm(..., implementation=...) and "
+                      f"torch.autograd.grad, {steps} steps back to back, one input set")
+    return result
+
+
 def cpu_baseline(torch, workload: Workload, budget_seconds: float) -> dict:
     """The reference's CPU path on this host, on a bounded sample of steps."""
     from oracle.torch_path import fwd_bwd_step
@@ -272,7 +334,7 @@ class Runner:
             t["x"].data_ptr(), t["branch"].data_ptr(), self.code(w.branch), self.weight.data_ptr(),
             self.bias.data_ptr(), t["updated"].data_ptr(), t["normalized"].data_ptr(),
             self.code(w.normalized), t["mean"].data_ptr(), t["rstd"].data_ptr(),
-            t["mask"].data_ptr(), w.rows, w.hidden,
+            t["mask"].data_ptr(), None, None, w.rows, w.hidden,
             w.dropout_p, EPS, int(w.training), philox, self.handle)
         if status:
             raise RuntimeError(self.cabi.last_error())
@@ -512,6 +574,7 @@ def main() -> int:
               f"cold step {timing['cold_ms'] * 1e3:.2f} us", flush=True)
     result = result_line(torch, C1, timing, args.steps, args.warmup, args.sets, traffic)
     result["copy_ceiling"] = copy_ceiling(torch, stream)
+    result["public_api"] = public_api_steps(torch, C1, stream)
     if not args.no_cpu_baseline:
         print(f"[bench] CPU baseline (~{args.cpu_seconds:.0f} s)", flush=True)
         result["cpu_baseline"] = cpu_baseline(torch, C1, args.cpu_seconds)

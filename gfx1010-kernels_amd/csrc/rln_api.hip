@@ -183,6 +183,8 @@ int rln_forward(
     float* mean,
     float* rstd,
     uint32_t* dropout_mask,
+    float* zero_grad_weight,
+    float* zero_grad_bias,
     int64_t rows,
     int64_t hidden,
     double dropout_p,
@@ -204,6 +206,10 @@ int rln_forward(
     if (!(eps > 0.0)) {
         return fail(RLN_ERR_INVALID, "eps must be positive");
     }
+    if ((zero_grad_weight == nullptr) != (zero_grad_bias == nullptr)) {
+        return fail(RLN_ERR_INVALID,
+                    "zero_grad_weight and zero_grad_bias must both be given or both be null");
+    }
     DropoutConstants drop{};
     status = dropout_constants(dropout_p, training, &drop);
     if (status != RLN_OK) {
@@ -219,6 +225,8 @@ int rln_forward(
     a.mean = mean;
     a.rstd = rstd;
     a.mask = dropout_mask;
+    a.zero_weight = zero_grad_weight;
+    a.zero_bias = zero_grad_bias;
     a.rows = rows;
     a.eps = static_cast<float>(eps);
     a.dropout = drop.active ? 1 : 0;
@@ -406,7 +414,7 @@ const char* rln_target_arch(void) {
 }
 
 const char* rln_version(void) {
-    return "0.2.0";
+    return "0.3.0";
 }
 
 }  // extern "C"

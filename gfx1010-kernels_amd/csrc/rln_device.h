@@ -598,6 +598,8 @@ void rln_forward_kernel(
     float* __restrict__ mean_out,
     float* __restrict__ rstd_out,
     uint32_t* __restrict__ mask,
+    float* __restrict__ zero_weight,
+    float* __restrict__ zero_bias,
     int64_t rows,
     S shape,
     float eps,
@@ -625,6 +627,16 @@ void rln_forward_kernel(
     for (int v = 0; v < V; ++v) {
         w[v] = load_parameter4<Aligned>(weight + slots.column(v));
         b[v] = load_parameter4<Aligned>(bias + slots.column(v));
+    }
+
+    // Zero the weight/bias gradient sums a later backward accumulates into.
+    if (zero_weight != nullptr) {
+        const int64_t threads = static_cast<int64_t>(gridDim.x) * S::kForwardThreads;
+        for (int64_t i = static_cast<int64_t>(blockIdx.x) * S::kForwardThreads + threadIdx.x;
+             i < hidden; i += threads) {
+            zero_weight[i] = 0.0f;
+            zero_bias[i] = 0.0f;
+        }
     }
 
     uint32_t key0 = 0;
@@ -1042,6 +1054,8 @@ struct ForwardArgs {
     float* mean;
     float* rstd;
     uint32_t* mask;
+    float* zero_weight;  // optional: zeroed by the launch (hidden floats each)
+    float* zero_bias;
     int64_t rows;
     float eps;
     int dropout;
@@ -1097,6 +1111,8 @@ int launch_forward(const ForwardArgs& a, S shape) {
         a.mean,
         a.rstd,
         a.mask,
+        a.zero_weight,
+        a.zero_bias,
         a.rows,
         shape,
         a.eps,

@@ -209,7 +209,9 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> forward_i
     double eps,
     bool training,
     int64_t threads,
-    std::optional<at::ScalarType> normalized_dtype) {
+    std::optional<at::ScalarType> normalized_dtype,
+    at::Tensor* zeroed_grad_weight = nullptr,
+    at::Tensor* zeroed_grad_bias = nullptr) {
     check_forward_inputs(x, branch, weight, bias, dropout_p, eps, threads);
     const at::ScalarType output_type = normalized_dtype.value_or(at::kFloat);
     TORCH_CHECK(supported_dtype(output_type),
@@ -227,6 +229,13 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> forward_i
     if (dropout) {
         philox = reserve_philox(x, hidden);
     }
+    // Optional weight/bias gradient sums for the backward of this call,
+    // zeroed by the forward launch itself.
+    const bool zero_sums = zeroed_grad_weight != nullptr && zeroed_grad_bias != nullptr;
+    if (zero_sums) {
+        *zeroed_grad_weight = at::empty({hidden}, x.options());
+        *zeroed_grad_bias = at::empty({hidden}, x.options());
+    }
     const auto stream = c10::hip::getCurrentHIPStreamMasqueradingAsCUDA(x.device().index()).stream();
     check_status(rln_forward(
         x.data_ptr<float>(),
@@ -240,6 +249,8 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> forward_i
         mean.data_ptr<float>(),
         rstd.data_ptr<float>(),
         dropout ? reinterpret_cast<uint32_t*>(mask.data_ptr<int32_t>()) : nullptr,
+        zero_sums ? zeroed_grad_weight->data_ptr<float>() : nullptr,
+        zero_sums ? zeroed_grad_bias->data_ptr<float>() : nullptr,
         rows,
         hidden,
         dropout_p,
@@ -266,7 +277,9 @@ std::vector<at::Tensor> backward_impl(
     int64_t parameter_threads,
     int64_t parameter_groups,
     bool compute_parameter_gradients,
-    std::optional<at::ScalarType> branch_dtype) {
+    std::optional<at::ScalarType> branch_dtype,
+    const at::Tensor* zeroed_grad_weight = nullptr,
+    const at::Tensor* zeroed_grad_bias = nullptr) {
     // Undefined tensors arrive from autograd as nullopt-equivalents.
     std::optional<at::Tensor> grad_updated;
     std::optional<at::Tensor> grad_normalized;
@@ -306,14 +319,22 @@ std::vector<at::Tensor> backward_impl(
     at::Tensor grad_bias;
     at::Tensor workspace;
     const bool launch_parameters = compute_parameter_gradients && grad_normalized.has_value();
+    // Sums the forward already zeroed: accumulate into them, no zeroing launch.
+    const bool zeroed = zeroed_grad_weight != nullptr && zeroed_grad_bias != nullptr
+        && zeroed_grad_weight->defined() && zeroed_grad_bias->defined();
     if (compute_parameter_gradients) {
         // Without grad_normalized the parameter gradients are exactly zero.
         // Two separate tensors (not views of one), so that no two returned
         // gradients alias each other.
-        grad_weight = launch_parameters ? at::empty({hidden}, updated.options())
-                                        : at::zeros({hidden}, updated.options());
-        grad_bias = launch_parameters ? at::empty({hidden}, updated.options())
-                                      : at::zeros({hidden}, updated.options());
+        if (zeroed) {
+            grad_weight = *zeroed_grad_weight;
+            grad_bias = *zeroed_grad_bias;
+        } else {
+            grad_weight = launch_parameters ? at::empty({hidden}, updated.options())
+                                            : at::zeros({hidden}, updated.options());
+            grad_bias = launch_parameters ? at::empty({hidden}, updated.options())
+                                          : at::zeros({hidden}, updated.options());
+        }
     }
     if (launch_parameters) {
         const size_t bytes = rln_backward_workspace_bytes(rows, hidden, deterministic ? 1 : 0);
@@ -343,7 +364,7 @@ std::vector<at::Tensor> backward_impl(
         dropout_p,
         training ? 1 : 0,
         deterministic ? 1 : 0,
-        0,
+        zeroed ? 1 : 0,
         workspace.defined() ? workspace.data_ptr() : nullptr,
         workspace.defined() ? static_cast<size_t>(workspace.numel()) * sizeof(float) : 0,
         stream));
@@ -371,8 +392,17 @@ class ResidualLayerNormFunction : public torch::autograd::Function<ResidualLayer
         int64_t parameter_threads,
         int64_t parameter_groups,
         std::optional<at::ScalarType> normalized_dtype) {
+        // The first backward of this call accumulates the weight/bias
+        // gradients into sums the forward launch zeroes (one launch fewer per
+        // training step); a repeated backward (retain_graph) allocates anew.
+        at::Tensor grad_weight_sum;
+        at::Tensor grad_bias_sum;
+        const bool parameters = weight.requires_grad() || bias.requires_grad();
         auto result = forward_impl(
-            x, branch, weight, bias, dropout_p, eps, training, threads, normalized_dtype);
+            x, branch, weight, bias, dropout_p, eps, training, threads, normalized_dtype,
+            parameters ? &grad_weight_sum : nullptr, parameters ? &grad_bias_sum : nullptr);
+        ctx->saved_data["grad_weight_sum"] = grad_weight_sum;
+        ctx->saved_data["grad_bias_sum"] = grad_bias_sum;
         auto updated = std::get<0>(result);
         auto normalized = std::get<1>(result);
         ctx->save_for_backward(
@@ -407,6 +437,11 @@ class ResidualLayerNormFunction : public torch::autograd::Function<ResidualLayer
                 at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor(),
                 at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor()};
         }
+        // Sums zeroed by the forward serve the first backward only.
+        at::Tensor grad_weight_sum = ctx->saved_data["grad_weight_sum"].toTensor();
+        at::Tensor grad_bias_sum = ctx->saved_data["grad_bias_sum"].toTensor();
+        ctx->saved_data["grad_weight_sum"] = at::Tensor();
+        ctx->saved_data["grad_bias_sum"] = at::Tensor();
         auto gradients = backward_impl(
             grad_updated,
             grad_normalized,
@@ -423,7 +458,9 @@ class ResidualLayerNormFunction : public torch::autograd::Function<ResidualLayer
             ctx->saved_data["parameter_threads"].toInt(),
             ctx->saved_data["parameter_groups"].toInt(),
             has_grad_normalized,
-            static_cast<at::ScalarType>(ctx->saved_data["branch_dtype"].toInt()));
+            static_cast<at::ScalarType>(ctx->saved_data["branch_dtype"].toInt()),
+            &grad_weight_sum,
+            &grad_bias_sum);
         return {
             gradients[0],
             gradients[1],
@@ -490,7 +527,12 @@ PYBIND11_MODULE(_C, module) {
         pybind11::arg("normalized_dtype") = pybind11::none());
     module.def(
         "residual_layer_norm_forward",
-        &forward_impl,
+        [](const at::Tensor& x, const at::Tensor& branch, const at::Tensor& weight,
+           const at::Tensor& bias, double dropout_p, double eps, bool training, int64_t threads,
+           std::optional<at::ScalarType> normalized_dtype) {
+            return forward_impl(
+                x, branch, weight, bias, dropout_p, eps, training, threads, normalized_dtype);
+        },
         pybind11::arg("x"),
         pybind11::arg("branch"),
         pybind11::arg("weight"),
@@ -502,7 +544,18 @@ PYBIND11_MODULE(_C, module) {
         pybind11::arg("normalized_dtype") = pybind11::none());
     module.def(
         "residual_layer_norm_backward",
-        &backward_impl,
+        [](const std::optional<at::Tensor>& grad_updated,
+           const std::optional<at::Tensor>& grad_normalized, const at::Tensor& updated,
+           const at::Tensor& weight, const at::Tensor& mean, const at::Tensor& rstd,
+           const at::Tensor& dropout_mask, double dropout_p, bool training, bool branch_is_half,
+           int64_t threads, int64_t block_rows, int64_t parameter_threads,
+           int64_t parameter_groups, bool compute_parameter_gradients,
+           std::optional<at::ScalarType> branch_dtype) {
+            return backward_impl(
+                grad_updated, grad_normalized, updated, weight, mean, rstd, dropout_mask,
+                dropout_p, training, branch_is_half, threads, block_rows, parameter_threads,
+                parameter_groups, compute_parameter_gradients, branch_dtype);
+        },
         pybind11::arg("grad_updated"),
         pybind11::arg("grad_normalized"),
         pybind11::arg("updated"),

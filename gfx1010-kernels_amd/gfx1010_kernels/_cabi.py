@@ -52,7 +52,7 @@ _I64 = ctypes.c_int64
 SIGNATURES = {
     "rln_forward": (
         ctypes.c_int,
-        [_P, _P, ctypes.c_int, _P, _P, _P, _P, ctypes.c_int, _P, _P, _P, _I64, _I64,
+        [_P, _P, ctypes.c_int, _P, _P, _P, _P, ctypes.c_int, _P, _P, _P, _P, _P, _I64, _I64,
          ctypes.c_double, ctypes.c_double, ctypes.c_int, ctypes.POINTER(RlnPhilox), _P],
     ),
     "rln_backward": (
@@ -106,15 +106,15 @@ def supported_hidden_sizes() -> tuple[int, ...]:
 def forward(
     x, branch, branch_dtype, weight, bias, updated, normalized, mean, rstd, mask,
     rows, hidden, dropout_p, eps, training, philox=None, stream=None,
-    normalized_dtype=RLN_DTYPE_F32,
+    normalized_dtype=RLN_DTYPE_F32, zero_grad_weight=None, zero_grad_bias=None,
 ):
     """Call ``rln_forward`` with integer device addresses; raises RlnError."""
     pointer = ctypes.byref(philox) if philox is not None else None
     _check(
         library().rln_forward(
             x, branch, branch_dtype, weight, bias, updated, normalized, normalized_dtype,
-            mean, rstd, mask, rows, hidden, dropout_p, eps, int(bool(training)), pointer,
-            stream,
+            mean, rstd, mask, zero_grad_weight, zero_grad_bias, rows, hidden, dropout_p, eps,
+            int(bool(training)), pointer, stream,
         )
     )
 

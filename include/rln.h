@@ -82,6 +82,12 @@ typedef struct rln_philox {
  * training && dropout_p > 0 (may be NULL otherwise). `philox` is read only in
  * that case (may be NULL otherwise). The call consumes
  * rln_philox_increment(hidden) offset units of the Philox stream.
+ * zero_grad_weight, zero_grad_bias: both NULL, or fp32 [hidden] each, set to
+ * zero by this launch: the weight/bias gradient sums of a later
+ * rln_backward(..., accumulate_parameters = 1), which then needs no zeroing
+ * launch of its own (the reference memsets them in its backward,
+ * csrc/residual_layer_norm_kernel.hip:1870-1880; one launch fewer per
+ * training step here).
  */
 int rln_forward(
     const float* x,
@@ -95,6 +101,8 @@ int rln_forward(
     float* mean,
     float* rstd,
     uint32_t* dropout_mask,
+    float* zero_grad_weight,
+    float* zero_grad_bias,
     int64_t rows,
     int64_t hidden,
     double dropout_p,

@@ -97,6 +97,8 @@ def _forward(**overrides):
         (dict(mask=None), _cabi.RLN_ERR_INVALID, "dropout_mask must not be null"),
         (dict(philox=None), _cabi.RLN_ERR_INVALID, "philox must not be null"),
         (dict(rows=1 << 62), _cabi.RLN_ERR_INVALID, "overflows"),
+        (dict(zero_grad_weight=FAKE), _cabi.RLN_ERR_INVALID,
+         "zero_grad_weight and zero_grad_bias must both be given or both be null"),
     ],
 )
 def test_forward_rejects_invalid_arguments(overrides, status, message):

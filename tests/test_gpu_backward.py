@@ -207,3 +207,26 @@ def test_atomic_mode_is_close_to_deterministic_mode():
         scale = float(b.abs().max())
         assert float((a - b).abs().max()) <= 1e-5 * scale
     assert np.isfinite(host(fixed[2])).all()
+
+
+@pytest.mark.parametrize("deterministic", [False, True], ids=["atomic", "deterministic"])
+def test_repeated_backward_of_one_forward(deterministic):
+    """The first backward of a call accumulates into sums its forward zeroed;
+    a second backward of the same graph (retain_graph) must give the same
+    gradients, not twice them."""
+    rows, hidden = 129, 768
+    leaves = [t.requires_grad_(True) for t in make_inputs((rows, hidden), torch.float16, seed=5)]
+    grad_updated, grad_normalized = make_grads((rows, hidden), seed=6)
+    with deterministic_algorithms(deterministic):
+        updated, normalized = residual_layer_norm(*leaves, dropout_p=0.1, eps=1e-5,
+                                                  training=True, implementation="gfx950")
+        first = torch.autograd.grad((updated, normalized), leaves,
+                                    (grad_updated, grad_normalized), retain_graph=True)
+        second = torch.autograd.grad((updated, normalized), leaves,
+                                     (grad_updated, grad_normalized))
+    for name, a, b in zip(("x", "branch", "weight", "bias"), first, second):
+        if deterministic:
+            assert_bitwise(host(a), host(b), name)
+        else:
+            assert torch.allclose(a.float(), b.float(), rtol=1e-5, atol=1e-5), name
+    assert first[2].data_ptr() != second[2].data_ptr()

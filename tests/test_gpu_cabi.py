@@ -138,3 +138,38 @@ def test_backward_without_parameter_gradients():
                                  out["mask"]), inputs, 0.2, True, EPS, 77, 8)
     check_backward((grad_x, grad_branch, None, None), grads[0], grads[1], out["updated"],
                    inputs[2], EPS, keep, scale, "no parameters", parameters=False)
+
+
+@pytest.mark.parametrize("hidden", [768, 1600])
+@pytest.mark.parametrize("deterministic", [False, True], ids=["atomic", "deterministic"])
+def test_forward_zeroes_the_parameter_sums_of_the_next_backward(hidden, deterministic):
+    """rln_forward with zero_grad_weight / zero_grad_bias clears them (they
+    start as NaN here); a backward that accumulates into them then yields the
+    parameter gradients alone."""
+    rows = 300
+    inputs = make_inputs((rows, hidden), torch.float16, seed=hidden + 9)
+    grads = make_grads((rows, hidden), seed=hidden + 10)
+    x, branch, weight, bias = inputs
+    sums = torch.full((2, hidden), float("nan"), device="cuda")
+    out = dict(
+        updated=torch.empty_like(x), normalized=torch.empty_like(x),
+        mean=torch.empty(rows, device="cuda"), rstd=torch.empty(rows, device="cuda"),
+        mask=torch.zeros(_cabi.mask_words(rows, hidden), device="cuda", dtype=torch.int32),
+    )
+    seed, offset = 99, 4 * rows
+    _cabi.forward(x.data_ptr(), branch.data_ptr(), _cabi.RLN_DTYPE_F16, weight.data_ptr(),
+                  bias.data_ptr(), out["updated"].data_ptr(), out["normalized"].data_ptr(),
+                  out["mean"].data_ptr(), out["rstd"].data_ptr(), out["mask"].data_ptr(), rows,
+                  hidden, 0.1, EPS, True, _cabi.RlnPhilox(seed, offset, None, None),
+                  torch.cuda.current_stream().cuda_stream, zero_grad_weight=sums[0].data_ptr(),
+                  zero_grad_bias=sums[1].data_ptr())
+    torch.cuda.synchronize()
+    assert torch.count_nonzero(sums).item() == 0 and not torch.isnan(sums).any()
+    keep, scale = check_forward((out["updated"], out["normalized"], out["mean"], out["rstd"],
+                                 out["mask"]), inputs, 0.1, True, EPS, seed, offset, "zeroing")
+    workspace = new_workspace(rows, hidden) if deterministic else None
+    grad_x, grad_branch = backward(out, grads, weight, torch.float16, 0.1, deterministic, True,
+                                   sums, workspace)
+    torch.cuda.synchronize()
+    check_backward((grad_x, grad_branch, sums[0], sums[1]), grads[0], grads[1], out["updated"],
+                   weight, EPS, keep, scale, f"H={hidden}")
