@@ -86,7 +86,7 @@ typedef struct rln_philox {
  * zero by this launch: the weight/bias gradient sums of a later
  * rln_backward(..., accumulate_parameters = 1), which then needs no zeroing
  * launch of its own (the reference memsets them in its backward,
- * csrc/residual_layer_norm_kernel.hip:1870-1880; one launch fewer per
+ * csrc/residual_layer_norm_kernel.hip:1895-1901; one launch fewer per
  * training step here).
  */
 int rln_forward(
