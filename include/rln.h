@@ -129,7 +129,7 @@ int rln_forward(
  * already in grad_weight / grad_bias (gradient accumulation across calls, one
  * kernel launch in atomic mode); 0 overwrites them.
  * workspace: device scratch of at least
- * rln_backward_workspace_bytes(rows, hidden, deterministic) bytes, 256-byte
+ * rln_backward_workspace_bytes(rows, hidden, deterministic) bytes, 16-byte
  * aligned (may be NULL when that size is 0).
  */
 int rln_backward(
@@ -156,35 +156,43 @@ int rln_backward(
     size_t workspace_bytes,
     void* stream);
 
-/* Workspace bytes rln_backward needs (0 in atomic mode). */
+/* Workspace bytes rln_backward needs (0 in atomic mode): the per-block
+ * weight/bias partials of the deterministic reduction, which the reference
+ * allocates itself (csrc/residual_layer_norm_kernel.hip:1870-1872). */
 size_t rln_backward_workspace_bytes(
     int64_t rows,
     int64_t hidden,
     int deterministic);
 
-/* Philox offset units one dropout forward consumes (torch's `increment`). */
+/* Philox offset units one dropout forward consumes (torch's `increment`;
+ * the reference computes its own at csrc/residual_layer_norm_kernel.hip:1766-1770). */
 uint64_t rln_philox_increment(int64_t hidden);
 
-/* Number of uint32 dropout-mask words for [rows, hidden]. */
+/* Number of uint32 dropout-mask words for [rows, hidden] (the reference's
+ * mask size, csrc/residual_layer_norm_kernel.hip:1750-1753, :162-164). */
 int64_t rln_mask_words(int64_t rows, int64_t hidden);
 
 /* 1 if the library serves rows of `hidden` values, else 0: the reference's
  * sizes 128, 256, 384, 512, 768 and 1024 (specialized kernels) and every
  * other multiple of 64 from 128 to 8192 (kernels with a run-time row length;
- * the reference compiles only the six). */
+ * the reference compiles only the six, gfx1010_kernels/normalization.py:12). */
 int rln_hidden_supported(int64_t hidden);
 
 /* Writes up to `capacity` supported hidden sizes in ascending order; returns
- * how many exist. */
+ * how many exist (the reference's NATIVE_HIDDEN_SIZES,
+ * gfx1010_kernels/normalization.py:12). */
 int rln_supported_hidden_sizes(int64_t* out, int capacity);
 
-/* Thread-local message for the last failed call on this thread. */
+/* Thread-local message for the last failed call on this thread (the text of
+ * the reference's TORCH_CHECK messages, csrc/residual_layer_norm_kernel.hip:26-166). */
 const char* rln_last_error(void);
 
-/* GPU architecture the device code was built for ("gfx950"). */
+/* GPU architecture the device code was built for ("gfx950"; the reference
+ * gates on "gfx1010", gfx1010_kernels/normalization.py:57). */
 const char* rln_target_arch(void);
 
-/* Library version string. */
+/* Library version string (the reference's package version is
+ * gfx1010_kernels/__init__.py:22). */
 const char* rln_version(void);
 
 #ifdef __cplusplus
