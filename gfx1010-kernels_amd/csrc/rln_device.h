@@ -1022,42 +1022,44 @@ void rln_backward_kernel(
 
     // Combine the block's sums in a fixed order. A column is owned by one
     // (part, lane) pair; for each, the block adds groups 0..kGroups-1 and,
-    // within a wave, row slots 0..kRowsPerWave-1.
-    __shared__ f32x4 staging[kWaves][kWaveSize][2];
+    // within a wave, row slots 0..kRowsPerWave-1. All slots are staged at
+    // once (16 KiB of LDS per slot), so one barrier serves the whole combine.
+    __shared__ f32x4 staging[V][kWaves][kWaveSize][2];
     const bool write_partials = flags & kPartials;
 #pragma unroll
     for (int v = 0; v < V; ++v) {
-        staging[wave_in_block][lane][0] = acc_w[v];
-        staging[wave_in_block][lane][1] = acc_b[v];
-        __syncthreads();
-        // P x L owners x 8 floats to produce; the block's threads share them.
-        for (int entry = threadIdx.x; entry < P * L * 8; entry += kBackwardThreads) {
-            const int owner = entry / 8;
-            const int owner_part = owner / L;
-            const int slot = owner % L;
-            const int which = (entry / 4) & 1;  // 0 = weight, 1 = bias
-            const int component = entry & 3;
-            const int64_t column = static_cast<int64_t>((v * P + owner_part) * L + slot) * 4
-                + component;
-            if (S::kRagged && column >= hidden) {
-                continue;
-            }
-            float total = 0.0f;
+        staging[v][wave_in_block][lane][0] = acc_w[v];
+        staging[v][wave_in_block][lane][1] = acc_b[v];
+    }
+    __syncthreads();
+    // V x P x L owners x 8 floats to produce; the block's threads share them.
+    constexpr int kPerSlot = P * L * 8;
+    for (int entry = threadIdx.x; entry < V * kPerSlot; entry += kBackwardThreads) {
+        const int v = entry / kPerSlot;
+        const int owner = (entry % kPerSlot) / 8;
+        const int owner_part = owner / L;
+        const int slot = owner % L;
+        const int which = (entry / 4) & 1;  // 0 = weight, 1 = bias
+        const int component = entry & 3;
+        const int64_t column = static_cast<int64_t>((v * P + owner_part) * L + slot) * 4
+            + component;
+        if (S::kRagged && column >= hidden) {
+            continue;
+        }
+        float total = 0.0f;
 #pragma unroll
-            for (int group = 0; group < T::kGroups; ++group) {
+        for (int group = 0; group < T::kGroups; ++group) {
 #pragma unroll
-                for (int source_sub = 0; source_sub < S::kRowsPerWave; ++source_sub) {
-                    total += staging[group * P + owner_part][source_sub * L + slot][which]
-                                    [component];
-                }
-            }
-            if (write_partials) {
-                partials[(static_cast<int64_t>(blockIdx.x) * 2 + which) * hidden + column] = total;
-            } else {
-                unsafeAtomicAdd((which ? grad_bias : grad_weight) + column, total);
+            for (int source_sub = 0; source_sub < S::kRowsPerWave; ++source_sub) {
+                total += staging[v][group * P + owner_part][source_sub * L + slot][which]
+                                [component];
             }
         }
-        __syncthreads();
+        if (write_partials) {
+            partials[(static_cast<int64_t>(blockIdx.x) * 2 + which) * hidden + column] = total;
+        } else {
+            unsafeAtomicAdd((which ? grad_bias : grad_weight) + column, total);
+        }
     }
 }
 
