@@ -1,0 +1,57 @@
+"""Seeded random configurations across the whole supported range.
+
+Each case draws a hidden size (any multiple of 64 from 128 to 8192), a row
+count, branch and normalized dtypes, dropout, training mode and reduction
+mode, then checks the forward and the backward against the fp64 oracle. The
+draws are fixed by the case index, so every run checks the same cases.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from gfx1010_kernels import _C
+from gfx1010_kernels._normalization_native import NATIVE_HIDDEN_SIZES
+from parity import check_backward, check_forward, generator_state, make_grads, make_inputs
+from test_gpu_backward import deterministic_algorithms, raw_backward
+
+pytestmark = pytest.mark.gpu
+EPS = 1e-5
+DTYPES = (torch.float32, torch.float16, torch.bfloat16)
+
+
+def draw(case):
+    rng = np.random.default_rng(1000 + case)
+    hidden = int(rng.choice(NATIVE_HIDDEN_SIZES))
+    max_rows = max(1, (1 << 20) // hidden)
+    rows = int(min(max_rows, rng.choice([1, 2, 3, 7, 31, 64, 255, 513, 1024, 2047, 4099])))
+    return dict(
+        hidden=hidden,
+        rows=rows,
+        branch=DTYPES[int(rng.integers(3))],
+        normalized=DTYPES[int(rng.integers(3))],
+        dropout_p=float(rng.choice([0.0, 0.1, 0.5])),
+        training=bool(rng.integers(4) != 0),
+        deterministic=bool(rng.integers(2)),
+        x_mean=float(rng.choice([0.0, 3.0, 100.0])),
+    )
+
+
+@pytest.mark.parametrize("case", range(32))
+def test_random_configuration_matches_oracle(case):
+    c = draw(case)
+    print(f"[random] case {case}: {c}", flush=True)
+    inputs = make_inputs((c["rows"], c["hidden"]), c["branch"], seed=case, x_mean=c["x_mean"])
+    grad_updated, grad_normalized = make_grads((c["rows"], c["hidden"]), seed=case + 500)
+    grad_normalized = grad_normalized.to(c["normalized"])
+    torch.cuda.manual_seed(case)
+    seed, offset = generator_state()
+    outputs = _C.residual_layer_norm_forward(*inputs, c["dropout_p"], EPS, c["training"], 128,
+                                             normalized_dtype=c["normalized"])
+    keep, scale = check_forward(outputs, inputs, c["dropout_p"], c["training"], EPS, seed,
+                                offset, f"case {case}")
+    with deterministic_algorithms(c["deterministic"]):
+        gradients = raw_backward(grad_updated, grad_normalized, outputs, inputs[2],
+                                 c["dropout_p"], c["branch"], training=c["training"])
+    check_backward(gradients, grad_updated, grad_normalized, outputs[0], inputs[2], EPS, keep,
+                   scale, f"case {case}")
