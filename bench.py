@@ -225,8 +225,9 @@ def public_api_steps(torch, workload: Workload, stream, steps: int = 100) -> dic
 
 
 def cpu_baseline(torch, workload: Workload, budget_seconds: float) -> dict:
-    """The reference's CPU path on this host, on a bounded sample of steps."""
-    from oracle.torch_path import fwd_bwd_step
+    """The reference's CPU path on this host, on a bounded sample of steps
+    (forward plus autograd backward; forward only for a forward workload)."""
+    from oracle.torch_path import fwd_bwd_step, residual_layer_norm_torch
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
@@ -239,8 +240,14 @@ def cpu_baseline(torch, workload: Workload, budget_seconds: float) -> dict:
     bias = (0.02 * torch.randn(workload.hidden, generator=generator)).requires_grad_(True)
     grad_updated = torch.randn(shape, generator=generator)
     grad_normalized = torch.randn(shape, generator=generator)
-    step = lambda: fwd_bwd_step(x, branch, weight, bias, grad_updated,  # noqa: E731
-                                grad_normalized, workload.dropout_p, EPS)
+    if workload.backward:
+        step = lambda: fwd_bwd_step(x, branch, weight, bias, grad_updated,  # noqa: E731
+                                    grad_normalized, workload.dropout_p, EPS)
+    else:
+        def step():
+            with torch.no_grad():
+                residual_layer_norm_torch(x, branch, weight, bias, workload.dropout_p, EPS,
+                                          workload.training)
     for _ in range(2):
         step()
     samples = []
@@ -264,10 +271,10 @@ def cpu_baseline(torch, workload: Workload, budget_seconds: float) -> dict:
         "unit": "GB/s",
         "cores": cores,
         "kind": "port",
-        "sample": (f"{len(samples)} fwd+bwd steps of {workload.name} "
-                   f"[{workload.rows},{workload.hidden}] (F.dropout + add + F.layer_norm, "
-                   f"autograd.grad), median {median * 1e3:.2f} ms/step, "
-                   f"torch {torch.__version__} on {model}"),
+        "sample": (f"{len(samples)} {'fwd+bwd' if workload.backward else 'fwd'} steps of "
+                   f"{workload.name} [{workload.rows},{workload.hidden}] (F.dropout + add + "
+                   f"F.layer_norm{', autograd.grad' if workload.backward else ''}), "
+                   f"median {median * 1e3:.2f} ms/step, torch {torch.__version__} on {model}"),
         "rows_per_s": round(workload.rows / median, 1),
         "ms_per_step": round(median * 1e3, 3),
     }
@@ -592,6 +599,9 @@ def main() -> int:
                 del runner
             line = result_line(torch, workload, timing, steps, args.warmup, sets, None)
             line["sweep"] = True
+            if not workload.backward and not args.no_cpu_baseline:
+                # C0's forward-only CPU path is cheap to sample (~0.5 ms per step).
+                line["cpu_baseline"] = cpu_baseline(torch, workload, min(args.cpu_seconds, 5.0))
             print(json.dumps(line), flush=True)
     return 0
 
