@@ -189,3 +189,32 @@ def test_input_reasons(mutate, reason):
     finally:
         del Cuda.is_cuda
     assert found is not None and __import__("re").search(reason, found), found
+
+
+@pytest.mark.parametrize("hidden,native", [(128, True), (192, True), (1600, True), (8192, True),
+                                           (136, False), (160, False), (1000, False),
+                                           (8256, False)])
+def test_native_hidden_sizes_are_the_multiples_of_64_up_to_8192(monkeypatch, hidden, native):
+    """can_use_residual_layer_norm accepts every multiple of 64 from 128 to
+    8192 when the inputs are otherwise eligible and the backend is ready."""
+    _eligible(monkeypatch, BackendStatus(True, "MI355X", "gfx950", "ready"))
+    x = torch.randn(2, hidden)
+    assert can_use_residual_layer_norm(x, x, torch.ones(hidden), torch.zeros(hidden)) is native
+
+
+def test_auto_eligibility_range_reaches_8192():
+    x = torch.zeros(2, 8256)
+    reason = normalization._input_reason(x, x, torch.ones(8256), torch.zeros(8256), 0.0, 1e-5)
+    assert reason == "x must be a HIP tensor"  # checked before the size on CPU tensors
+
+    class Cuda:
+        is_cuda = True
+        ndim = 2
+        device = torch.device("cpu")
+
+        def __init__(self, shape):
+            self.shape = torch.Size(shape)
+
+    wide = Cuda((2, 8256))
+    assert "between 128 and 8192" in normalization._input_reason(
+        wide, wide, wide, wide, 0.0, 1e-5)
