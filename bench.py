@@ -162,7 +162,76 @@ def parse_args():
                         help="also print one line per other BASELINE.json configuration")
     parser.add_argument("--calibrate-copy-mib", type=int, default=0,
                         help="also launch one device copy of this many MiB (PMC calibration)")
+    parser.add_argument("--prenorm", action="store_true",
+                        help="also time a pre-norm transformer stack, fused vs unfused")
     return parser.parse_args()
+
+
+def prenorm_stack(torch, stream, depth: int = 12, hidden: int = 768, tokens: int = 8192,
+                  dropout_p: float = 0.1, steps: int = 20) -> dict:
+    """A GPT-2-small-shaped pre-norm stack (12 blocks, H = 768, 8 x 1024 tokens;
+    attention replaced by one H x H projection, MLP H -> 4H -> H with GELU;
+    bf16 sublayers, fp32 residual stream and LayerNorm parameters), one
+    training step = forward + backward of the whole stack. "unfused" runs
+    `x = x + dropout(sublayer(ln(x)))` in PyTorch; "fused" runs
+    prenorm_forward, every residual add fused into the LayerNorm after it
+    (normalized output in bf16 for the sublayers)."""
+    from torch import nn
+    from torch.nn import functional as F
+
+    from gfx1010_kernels import prenorm_forward
+
+    torch.manual_seed(0)
+
+    class Block(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.ln_1 = nn.LayerNorm(hidden)
+            self.attn = nn.Linear(hidden, hidden, dtype=torch.bfloat16)
+            self.ln_2 = nn.LayerNorm(hidden)
+            self.mlp = nn.Sequential(nn.Linear(hidden, 4 * hidden, dtype=torch.bfloat16),
+                                     nn.GELU(),
+                                     nn.Linear(4 * hidden, hidden, dtype=torch.bfloat16))
+
+    blocks = nn.ModuleList(Block() for _ in range(depth)).cuda()
+    final = nn.LayerNorm(hidden).cuda()
+    x = torch.randn(tokens, hidden, device="cuda", requires_grad=True)
+    grad = torch.randn(tokens, hidden, device="cuda", dtype=torch.bfloat16)
+    half = torch.bfloat16
+
+    def unfused():
+        h = x
+        for block in blocks:
+            h = h + F.dropout(block.attn(block.ln_1(h).to(half)).float(), dropout_p, True)
+            h = h + F.dropout(block.mlp(block.ln_2(h).to(half)).float(), dropout_p, True)
+        return final(h).to(half)
+
+    def fused():
+        _, out = prenorm_forward(x, blocks, final, dropout_p=dropout_p, training=True,
+                                 implementation="gfx950", normalized_dtype=half)
+        return out
+
+    result = {}
+    with torch.cuda.stream(stream):
+        for name, forward in (("unfused", unfused), ("fused", fused)):
+            def step():
+                torch.autograd.backward(forward(), grad)
+
+            for _ in range(3):
+                step()
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            start.record(stream)
+            for _ in range(steps):
+                step()
+            end.record(stream)
+            end.synchronize()
+            result[name] = {"ms_per_step": round(start.elapsed_time(end) / steps, 3)}
+    result["speedup"] = round(result["unfused"]["ms_per_step"] / result["fused"]["ms_per_step"], 3)
+    result["config"] = {"depth": depth, "hidden": hidden, "tokens": tokens,
+                        "dropout_p": dropout_p, "sublayers": "bf16", "steps": steps}
+    return result
 
 
 def public_api_steps(torch, workload: Workload, stream, steps: int = 100) -> dict:
@@ -586,6 +655,11 @@ def main() -> int:
         print(f"[bench] CPU baseline (~{args.cpu_seconds:.0f} s)", flush=True)
         result["cpu_baseline"] = cpu_baseline(torch, C1, args.cpu_seconds)
     print(json.dumps(result), flush=True)
+
+    if args.prenorm:
+        line = {"metric": "pre-norm stack fwd+bwd step time (ms)", "higher_is_better": False,
+                **prenorm_stack(torch, stream)}
+        print(json.dumps(line), flush=True)
 
     if args.sweep:
         for workload in sweep_workloads():
