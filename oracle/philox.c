@@ -14,10 +14,9 @@
  *    numbers: as easy as 1, 2, 3", SC'11), one block per four consecutive
  *    columns, counter = (offset/4 low, offset/4 high, g low, g high) with
  *    g = (r * H + c) / 4, key = (seed low, seed high); output word c % 4.
- *    This counter assignment is the MI355X build's own: the reference draws
- *    from hipRAND's Philox with a launch-shape-dependent subsequence
- *    (csrc/residual_layer_norm_kernel.hip:449-480), which no test of the
- *    reference pins bit for bit.
+ *    This counter assignment is the MI355X build's own layout; the
+ *    reference's hipRAND layout (csrc/residual_layer_norm_kernel.hip:449-480)
+ *    is restated at the end of this file (oracle_reference_mask_rows).
  *
  * Pinned by: the Random123 known-answer vectors for philox4x32_10
  * (tests/golden/philox4x32_10_kat.json, tests/test_oracle.py) and a
@@ -98,4 +97,87 @@ void oracle_dropout_mask(
     int64_t rows, int64_t hidden, uint64_t seed, uint64_t offset, uint32_t threshold,
     uint32_t* words) {
     oracle_dropout_mask_rows(0, rows, hidden, seed, offset, threshold, words);
+}
+
+/* ------------------------------------------------------------------------
+ * The reference's own dropout stream: hipRAND's Philox4x32-10, which on ROCm
+ * is rocRAND's engine (third-party dependency of the reference, not vendored
+ * in it: rocRAND 4.2.0 of ROCm 7.2.0, rocrand/rocrand_philox4x32_10.h;
+ * hiprand_init / hiprand4 forward to rocrand_init / rocrand4,
+ * hiprand/hiprand_kernel_rocm.h:201-222, :377-380). Restated from its
+ * published behaviour:
+ *
+ *  - rocrand_init(seed, subsequence, offset): key = (seed low, seed high);
+ *    128-bit counter = subsequence * 2^64 + offset / 4; substate = offset % 4;
+ *  - the n-th rocrand4 call (n = 0, 1, ...) returns words substate ..
+ *    substate + 3 of the 8-word sequence philox(counter + n) ||
+ *    philox(counter + n + 1) (for substate 0 that is philox(counter + n)).
+ *
+ * Pinned by vectors that tests/golden/make_hiprand_vectors.py writes by
+ * calling rocRAND's rocrand_init / rocrand4 themselves
+ * (tests/golden/hiprand_philox_vectors.json, tests/test_oracle.py).
+ */
+
+/* Philox block of the 128-bit counter (high:low) + n. */
+static void philox_at(uint64_t low, uint64_t high, uint64_t n, const uint32_t key[2],
+                      uint32_t out[4]) {
+    const uint64_t sum = low + n;
+    const uint64_t carry = sum < low ? 1u : 0u;
+    const uint64_t top = high + carry;
+    const uint32_t counter[4] = {(uint32_t)sum, (uint32_t)(sum >> 32), (uint32_t)top,
+                                 (uint32_t)(top >> 32)};
+    oracle_philox4x32_10(counter, key, out);
+}
+
+/* `calls` consecutive rocrand4 results after rocrand_init(seed, subsequence,
+ * offset); out holds 4 * calls words. */
+void oracle_hiprand_philox4(uint64_t seed, uint64_t subsequence, uint64_t offset, int calls,
+                            uint32_t* out) {
+    const uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+    const unsigned substate = (unsigned)(offset % 4);
+    uint32_t current[4];
+    philox_at(offset / 4, subsequence, 0, key, current);
+    for (int n = 0; n < calls; ++n) {
+        uint32_t next[4];
+        philox_at(offset / 4, subsequence, (uint64_t)n + 1, key, next);
+        for (unsigned j = 0; j < 4; ++j) {
+            const unsigned word = substate + j;
+            out[4 * n + j] = word < 4 ? current[word] : next[word - 4];
+        }
+        memcpy(current, next, sizeof(current));
+    }
+}
+
+/* The reference's keep mask for rows [first_row, first_row + rows) of a
+ * [*, hidden] tensor launched with `threads` threads per row
+ * (csrc/residual_layer_norm_kernel.hip:449-511): thread t of row r draws
+ * items = ceil(hidden / threads) values, random_values[0..3] from the first
+ * hiprand4 of hiprand_init(seed, r * threads + t, offset) and [4..7] from the
+ * second; column c = t + item * threads (< hidden) keeps iff
+ * random_values[item] >= threshold; bit c % 32 of word c / 32. Returns 0, or
+ * -1 when a thread would need more than the reference's 8 values. */
+int oracle_reference_mask_rows(int64_t first_row, int64_t rows, int64_t hidden, int64_t threads,
+                               uint64_t seed, uint64_t offset, uint32_t threshold,
+                               uint32_t* words) {
+    const int64_t items = (hidden + threads - 1) / threads;
+    if (threads <= 0 || items > 8 || hidden % 32 != 0) {
+        return -1;
+    }
+    const int calls = (int)((items + 3) / 4);
+    memset(words, 0, (size_t)(rows * hidden / 32) * sizeof(uint32_t));
+    for (int64_t local = 0; local < rows; ++local) {
+        const uint64_t row = (uint64_t)(first_row + local);
+        for (int64_t t = 0; t < threads; ++t) {
+            uint32_t values[8];
+            oracle_hiprand_philox4(seed, row * (uint64_t)threads + (uint64_t)t, offset, calls,
+                                   values);
+            for (int64_t item = 0; item < items; ++item) {
+                const int64_t column = t + item * threads;
+                if (column < hidden && values[item] >= threshold) {
+                    words[local * (hidden / 32) + column / 32] |= 1u << (column % 32);
+                }
+            }
+        }
+    }
+    return 0;
 }

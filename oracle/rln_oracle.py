@@ -22,11 +22,17 @@ Restatement of the reference's algorithm, in numpy:
   fp64 (csrc/residual_layer_norm_kernel.hip:548-618, :727-786;
   docs/residual_layer_norm.md:111-160).
 * dropout mask: Philox4x32-10 stream and the reference's int32 word layout,
-  in C (oracle/philox.c).
+  in C (oracle/philox.c): this build's own counter layout
+  (``dropout_mask_words``), and the reference's hipRAND layout of a
+  ``threads``-wide launch (``reference_mask_words``,
+  csrc/residual_layer_norm_kernel.hip:449-511).
 
 How each function is pinned (tests/test_oracle.py):
 
 * Philox4x32-10: Random123 known-answer vectors (tests/golden/philox4x32_10_kat.json).
+* hipRAND stream and the reference's mask: vectors from rocRAND's own
+  rocrand_init / rocrand4 (tests/golden/hiprand_philox_vectors.json, written by
+  tests/golden/make_hiprand_vectors.py).
 * mask layout / decode: per-element pure-Python restatement on small shapes,
   and the byte identity with a little-endian uint64 word layout.
 * dropout constants: closed forms (p = 0.5, 0.25, 0.75 give exact powers of
@@ -79,6 +85,13 @@ def _library() -> ctypes.CDLL:
         ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_uint64, ctypes.c_uint64,
         ctypes.c_uint32, u32p]
     library.oracle_dropout_mask_rows.restype = None
+    library.oracle_hiprand_philox4.argtypes = [
+        ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int, u32p]
+    library.oracle_hiprand_philox4.restype = None
+    library.oracle_reference_mask_rows.argtypes = [
+        ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_uint64,
+        ctypes.c_uint64, ctypes.c_uint32, u32p]
+    library.oracle_reference_mask_rows.restype = ctypes.c_int
     return library
 
 
@@ -131,6 +144,44 @@ def dropout_mask_rows(first_row: int, rows: int, hidden: int, seed: int, offset:
     _library().oracle_dropout_mask_rows(first_row, rows, hidden, seed, offset, threshold,
                                         _u32_pointer(words))
     return words
+
+
+# The reference's own stream: hipRAND (rocRAND) Philox, one state per
+# (row, thread) of a `threads`-wide launch (oracle/philox.c).
+REFERENCE_THREADS = (128, 192, 256)
+
+
+def hiprand_philox4(seed: int, subsequence: int, offset: int, calls: int) -> list[int]:
+    """``calls`` rocrand4 results after rocrand_init(seed, subsequence, offset), flattened."""
+    out = np.zeros(4 * calls, dtype=np.uint32)
+    _library().oracle_hiprand_philox4(seed, subsequence, offset, calls, _u32_pointer(out))
+    return [int(value) for value in out]
+
+
+def reference_philox_increment(hidden: int, threads: int) -> int:
+    """Offset units the reference reserves per call: 4 * ceil(ceil(H / T) / 4)
+    (csrc/residual_layer_norm_kernel.hip:1766-1770)."""
+    items = -(-hidden // threads)
+    return 4 * (-(-items // 4))
+
+
+def reference_mask_rows(first_row: int, rows: int, hidden: int, threads: int, seed: int,
+                        offset: int, threshold: int) -> np.ndarray:
+    """The reference's keep mask for rows [first_row, first_row + rows), as
+    drawn by its ``threads``-wide forward launch."""
+    words = np.zeros(rows * hidden // 32, dtype=np.uint32)
+    status = _library().oracle_reference_mask_rows(first_row, rows, hidden, threads, seed,
+                                                   offset, threshold, _u32_pointer(words))
+    if status != 0:
+        raise ValueError(f"the reference draws at most 8 values per thread "
+                         f"(hidden={hidden}, threads={threads})")
+    return words
+
+
+def reference_mask_words(rows: int, hidden: int, threads: int, seed: int, offset: int,
+                         threshold: int) -> np.ndarray:
+    """The reference's keep mask for a whole [rows, hidden] tensor."""
+    return reference_mask_rows(0, rows, hidden, threads, seed, offset, threshold)
 
 
 def decode_mask(words: np.ndarray, rows: int, hidden: int) -> np.ndarray:

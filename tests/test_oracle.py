@@ -99,6 +99,71 @@ def test_offsets_select_disjoint_streams():
     assert (a != b).mean() > 0.99 and (a != c).mean() > 0.99
 
 
+# ---------------------------------------------------------------------------
+# The reference's own stream: hipRAND (rocRAND) Philox per (row, thread).
+
+def _hiprand_vectors():
+    return json.loads((GOLDEN / "hiprand_philox_vectors.json").read_text())
+
+
+def test_hiprand_stream_matches_rocrand():
+    """rocrand_init / rocrand4 outputs, from rocRAND itself, for both key
+    words, subsequences past 2^32, every substate and carrying counters."""
+    streams = _hiprand_vectors()["streams"]
+    assert {vector["offset"] % 4 for vector in streams} == {0, 1, 2, 3}
+    for vector in streams:
+        actual = oracle.hiprand_philox4(vector["seed"], vector["subsequence"],
+                                        vector["offset"], vector["calls"])
+        assert actual == vector["words"], vector
+
+
+def test_hiprand_stream_with_zero_substate_is_plain_philox():
+    """For offset % 4 == 0 the n-th rocrand4 is one Philox block of counter
+    (offset/4 + n, subsequence) - the Random123-pinned function."""
+    seed, subsequence, offset = 0xDEADBEEF_00C0FFEE, (3 << 32) + 11, 4 * ((1 << 33) + 5)
+    words = oracle.hiprand_philox4(seed, subsequence, offset, 2)
+    key = [seed & 0xFFFFFFFF, seed >> 32]
+    for n in range(2):
+        position = offset // 4 + n
+        counter = [position & 0xFFFFFFFF, position >> 32, subsequence & 0xFFFFFFFF,
+                   subsequence >> 32]
+        assert tuple(words[4 * n: 4 * n + 4]) == oracle.philox4x32_10(counter, key)
+
+
+def test_reference_mask_matches_rocrand():
+    """The reference kernel's keep masks, drawn through rocRAND, on its six
+    hidden sizes with thread counts 128 / 192 / 256 (ragged last items, one
+    and two hiprand4 calls, a subsequence past 2^32)."""
+    for vector in _hiprand_vectors()["masks"]:
+        words = oracle.reference_mask_rows(
+            vector["first_row"], vector["rows"], vector["hidden"], vector["threads"],
+            vector["seed"], vector["offset"], vector["threshold"])
+        assert words.tolist() == vector["words"], {k: vector[k] for k in vector if k != "words"}
+        _, _, threshold = oracle.dropout_constants(vector["dropout_p"])
+        assert threshold == vector["threshold"]
+
+
+@pytest.mark.parametrize("hidden,threads,increment", [
+    (128, 128, 4), (256, 128, 4), (384, 128, 4), (512, 128, 4), (768, 128, 8),
+    (1024, 128, 8), (1024, 192, 8), (768, 256, 4), (128, 256, 4)])
+def test_reference_philox_increment(hidden, threads, increment):
+    assert oracle.reference_philox_increment(hidden, threads) == increment
+
+
+def test_reference_mask_rejects_more_than_eight_values_per_thread():
+    with pytest.raises(ValueError, match="at most 8 values"):
+        oracle.reference_mask_words(1, 2048, 128, 1, 0, 1 << 30)
+
+
+def test_reference_mask_keep_ratio_is_binomial():
+    rows, hidden, p = 64, 768, 0.1
+    _, _, threshold = oracle.dropout_constants(p)
+    keep = oracle.decode_mask(
+        oracle.reference_mask_words(rows, hidden, 128, 11, 0, threshold), rows, hidden)
+    n = keep.size
+    assert abs(keep.sum() - n * (1 - p)) < 6 * np.sqrt(n * p * (1 - p))
+
+
 def test_dropout_constants_closed_forms():
     assert oracle.dropout_constants(0.0) == (False, np.float32(1.0), 0)
     assert oracle.dropout_constants(0.7, training=False)[0] is False
