@@ -64,6 +64,9 @@ EPS = 1e-5
 TRAFFIC_FILE = REPO / "profiles" / "rln_backward_c1_traffic.json"
 
 
+# The reference's threads per row (reference _normalization_native.py:5-12),
+# which fix its dropout stream; the public API passes the same table.
+REFERENCE_THREADS = {128: 128, 256: 128, 384: 128, 512: 128, 768: 128, 1024: 192}
 DTYPE_BYTES = {"f32": 4, "f16": 2, "bf16": 2}
 DTYPE_NAMES = {"f32": "float32", "f16": "float16", "bf16": "bfloat16"}
 
@@ -82,6 +85,16 @@ class Workload:
     x_mean: float = 0.0
     seed: int = 1001
     normalized: str = "f32"  # dtype of normalized and of its upstream gradient
+    # Dropout stream layout (rln_philox_t.threads): None = what the public API
+    # draws (the reference's hipRAND stream with its threads table on its
+    # hidden sizes, else the library's own layout); 0 = the library's layout.
+    threads: int | None = None
+
+    @property
+    def stream_threads(self) -> int:
+        if self.threads is not None:
+            return self.threads
+        return REFERENCE_THREADS.get(self.hidden, 0)
 
     @property
     def branch_bytes(self) -> int:
@@ -113,8 +126,13 @@ class Workload:
         reduction = "deterministic" if self.deterministic else "atomic"
         suffix = f", {reduction} dW/db" if self.backward else ""
         output = "" if self.normalized == "f32" else f", normalized {self.normalized}"
+        stream = ""
+        if self.dropping:
+            stream = (f", reference hipRAND stream (threads={self.stream_threads})"
+                      if self.stream_threads else ", library Philox layout")
         return (f"{self.name} {mode}: x fp32 [{self.rows},{self.hidden}], branch {self.branch}"
-                f"{output}, dropout_p={self.dropout_p}, training={self.training}{suffix}")
+                f"{output}, dropout_p={self.dropout_p}, training={self.training}{stream}"
+                f"{suffix}")
 
 
 C1 = Workload("C1", 8 * 1024, 768, "f16", 0.5, 0.1, seed=1001)
@@ -137,6 +155,12 @@ def sweep_workloads() -> list[Workload]:
     # normalized output and upstream gradient, at the C1 and C2 H=768 shapes.
     workloads.append(Workload("C1 bf16-out", 8 * 1024, 768, "bf16", 0.5, 0.1, seed=1001,
                               normalized="bf16"))
+    # The library's own Philox layout (a quarter fewer Philox blocks than the
+    # reference's stream at H = 768) at the C1 and C2 H=768 shapes.
+    workloads.append(Workload("C1 own-stream", 8 * 1024, 768, "f16", 0.5, 0.1, seed=1001,
+                              threads=0))
+    workloads.append(Workload("C2 H=768 own-stream", 262144, 768, "f16", 1.0, 0.15,
+                              seed=1002 + 768, threads=0))
     workloads.append(Workload("C2 H=768 bf16-out", 262144, 768, "bf16", 1.0, 0.15,
                               seed=1770, normalized="bf16"))
     # Hidden sizes the reference does not serve natively (run-time row length,
@@ -369,6 +393,7 @@ class Runner:
         if workload.backward and workspace_bytes:
             self.workspace = torch.empty(workspace_bytes, device="cuda", dtype=torch.uint8)
         self.seed = 0x5EED_0000 + workload.seed
+        self.increment = max(cabi.philox_increment(workload.hidden, workload.stream_threads), 4)
 
     def _make_set(self, seed: int) -> dict:
         torch, w = self.torch, self.w
@@ -405,7 +430,8 @@ class Runner:
 
     def forward(self, step: int):
         t, w = self.sets[step % len(self.sets)], self.w
-        philox = self.cabi.RlnPhilox(self.seed, 4 * step, None, None)
+        philox = self.cabi.RlnPhilox(self.seed, self.increment * step, None, None,
+                                     w.stream_threads)
         status = self.library.rln_forward(
             t["x"].data_ptr(), t["branch"].data_ptr(), self.code(w.branch), self.weight.data_ptr(),
             self.bias.data_ptr(), t["updated"].data_ptr(), t["normalized"].data_ptr(),

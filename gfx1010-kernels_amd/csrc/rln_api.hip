@@ -155,6 +155,27 @@ int check_common(int64_t rows, int64_t hidden, int branch_dtype) {
     return RLN_OK;
 }
 
+// The dropout layout `threads` selects: 0 for this library's; 128, 192 or
+// 256 for the reference's stream of a launch with that many threads per row
+// (reference csrc/residual_layer_norm_kernel.hip:68-72 accepts the same three
+// values), which exists for the reference's hidden sizes only and draws at
+// most 8 values per thread (its two hiprand4 calls, :449-480).
+int check_philox_threads(int64_t hidden, int64_t threads) {
+    if (threads == 0) {
+        return RLN_OK;
+    }
+    if (threads != 128 && threads != 192 && threads != 256) {
+        return fail(RLN_ERR_INVALID, "threads must be 0, 128, 192 or 256");
+    }
+    if (!specialized_hidden(hidden) || (hidden + threads - 1) / threads > 8) {
+        return fail(RLN_ERR_UNSUPPORTED,
+                    "the reference's dropout stream exists for hidden sizes 128, 256, 384, "
+                    "512, 768 and 1024 only, not %lld",
+                    static_cast<long long>(hidden));
+    }
+    return RLN_OK;
+}
+
 // Whether the parameter gradients of this call go through per-block partials
 // (and therefore the workspace and the reduce kernel).
 bool uses_partials(int deterministic) {
@@ -240,10 +261,20 @@ int rln_forward(
         if (!philox) {
             return fail(RLN_ERR_INVALID, "philox must not be null when dropout is active");
         }
+        status = check_philox_threads(hidden, philox->threads);
+        if (status != RLN_OK) {
+            return status;
+        }
+        if (philox->threads != 0 && philox->offset % 4 != 0) {
+            return fail(RLN_ERR_INVALID,
+                        "the reference's dropout stream needs a Philox offset that is a "
+                        "multiple of 4");
+        }
         a.philox.seed = philox->seed;
         a.philox.offset = philox->offset;
         a.philox.seed_ptr = philox->seed_ptr;
         a.philox.offset_ptr = philox->offset_ptr;
+        a.philox.threads = static_cast<int>(philox->threads);
     }
     const bool aligned = aligned_to(x, 16) && aligned_to(weight, 16) && aligned_to(bias, 16)
         && aligned_to(updated, 16)
@@ -375,9 +406,20 @@ int rln_backward(
     return status;
 }
 
-uint64_t rln_philox_increment(int64_t hidden) {
-    (void)hidden;
-    return 4;
+uint64_t rln_philox_increment(int64_t hidden, int64_t threads) {
+    rln::t_last_error.clear();
+    if (!hidden_supported(hidden)) {
+        fail(RLN_ERR_UNSUPPORTED, "unsupported hidden size %lld", static_cast<long long>(hidden));
+        return 0;
+    }
+    if (check_philox_threads(hidden, threads) != RLN_OK) {
+        return 0;
+    }
+    if (threads == 0) {
+        return 4;
+    }
+    const int64_t items = (hidden + threads - 1) / threads;
+    return static_cast<uint64_t>(4 * ((items + 3) / 4));
 }
 
 int64_t rln_mask_words(int64_t rows, int64_t hidden) {
@@ -414,7 +456,7 @@ const char* rln_target_arch(void) {
 }
 
 const char* rln_version(void) {
-    return "0.3.0";
+    return "0.4.0";
 }
 
 }  // extern "C"

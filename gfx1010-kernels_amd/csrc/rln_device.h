@@ -21,11 +21,17 @@
 //  * Waves walk rows with a grid-stride loop over a grid that depends only on
 //    (rows, H), never on the device, so the dropout stream and the
 //    deterministic parameter-gradient order are reproducible anywhere.
-//  * Dropout draws one Philox4x32-10 block (Salmon et al., SC'11) per four
-//    consecutive columns: counter = (offset/4, column-group index), key =
-//    seed. The keep mask depends only on (seed, offset, row, column), not on
-//    the launch shape. Keep bits are OR-combined across 8 lanes with DPP
-//    into the reference's int32 word layout (bit c%32 of word c/32).
+//  * Dropout draws from Philox4x32-10 (Salmon et al., SC'11) in one of two
+//    layouts. The reference's (hidden sizes 128-1024): its hipRAND stream,
+//    one Philox state per (row, thread) of a launch with 128, 192 or 256
+//    threads per row, so masks equal the reference's bit for bit
+//    (reference_keep_bits). This library's own (every hidden size): one
+//    Philox block per four consecutive columns, counter = (offset/4,
+//    column-group index), key = seed, a quarter of the reference's Philox
+//    work at H = 128 and three quarters at H = 768. Either way the mask
+//    depends on (seed, offset, row, column) and not on this build's launch
+//    shape. Keep bits are OR-combined across 8 lanes with DPP into the
+//    reference's int32 word layout (bit c%32 of word c/32).
 //  * The backward kernel produces grad_x and grad_branch AND accumulates
 //    the weight/bias gradients from the same registers, so g_y and updated
 //    are read once (the reference reads them a second time in its separate
@@ -138,18 +144,17 @@ constexpr int fixed_lanes(int64_t hidden) {
 
 // Lanes per row in the forward, whose normalized output has type N: fewer
 // lanes with more slots each where that measured faster on MI355X (H = 128:
-// 16 lanes, 12 % faster; H = 256 and 512: 32 lanes, 2-6 %; H = 768 with fp32
-// output: 32 lanes, 3 % at C1); H = 1024, and H = 768 with a 16-bit output,
-// are faster with a whole wave. The backward measured slower with more slots.
+// 16 lanes, 12 % faster; H = 256 and 512: 32 lanes, 2-6 %); H = 768 and 1024
+// are faster with a whole wave. (H = 768 with an fp32 output was 3 % faster
+// with 32 lanes in the library's own dropout layout at [8192, 768], but 2-14 %
+// slower drawing the reference's stream, whose extra Philox work then runs
+// at half the occupancy.) The backward measured slower with more slots.
 template <typename N>
 constexpr int forward_lanes(int64_t hidden) {
     if (hidden == 128) {
         return 16;
     }
-    if (hidden == 768) {
-        return std::is_same_v<N, float> ? 32 : 64;
-    }
-    if (hidden == 1024) {
+    if (hidden == 768 || hidden == 1024) {
         return 64;
     }
     return 32;
@@ -157,6 +162,7 @@ constexpr int forward_lanes(int64_t hidden) {
 
 template <int H, int Lanes = fixed_lanes(H)>
 struct FixedShape {
+    static constexpr int kHidden = H;
     static constexpr int kLanes = Lanes;
     static constexpr int kV = (H / 4) / kLanes;
     static constexpr int kParts = 1;
@@ -173,6 +179,7 @@ struct FixedShape {
 
 template <int V, int P>
 struct WideShape {
+    static constexpr int kHidden = 0;  // run-time
     static constexpr int kLanes = kWaveSize;
     static constexpr int kV = V;
     static constexpr int kParts = P;
@@ -371,6 +378,7 @@ struct PhiloxArgs {
     uint64_t offset;
     const int64_t* seed_ptr;
     const int64_t* offset_ptr;
+    int threads;  // 0: this library's layout; else the reference's, per rln_philox_t
 };
 
 // ----------------------------------------------------------------------------
@@ -550,6 +558,73 @@ __device__ __forceinline__ float team_sum(float value, float (*exchange)[S::kPar
     }
 }
 
+// Keep bits of the reference's own dropout stream for one row of a fixed
+// shape (reference csrc/residual_layer_norm_kernel.hip:449-511). The
+// reference launches `threads` threads per row; thread t of row r seeds
+// hipRAND's Philox with hiprand_init(seed, r * threads + t, offset) - key =
+// seed, 128-bit counter = (r * threads + t) * 2^64 + offset / 4, plus n for
+// its n-th hiprand4 - and draws items = ceil(H / threads) values, four per
+// call; column t + item * threads keeps iff value[item] >= threshold.
+//
+// Here the row's L lanes stand in for those threads, L at a time
+// (t = k * L + l), and compute the same ceil(items / 4) Philox blocks per
+// thread. Item `item` of threads k * L .. k * L + L - 1 covers the L
+// consecutive columns of chunk item * (threads / L) + k; one ballot
+// collects their keep flags, which the row's first L / 16 lanes stage in
+// LDS as 16-bit pieces (a ballot carries the chunks of all rows of the
+// wave). Each lane then reads the 4 bits of each of its slots and returns
+// them packed, slot v in bits 4v .. 4v + 3. `stage` is the row's H / 16
+// pieces, used by this wave only: LDS accesses of one wave complete in
+// order, so no barrier is needed. Requires offset % 4 == 0 and at most 8
+// items (the reference's two hiprand4 calls), checked on the host.
+template <typename S>
+__device__ __forceinline__ uint32_t reference_keep_bits(
+    uint16_t* stage, int64_t row, int lane, int group, int threads, uint64_t position,
+    uint32_t key0, uint32_t key1, uint32_t threshold) {
+    constexpr int L = S::kLanes;
+    constexpr int kChunks = S::kHidden / L;
+    static_assert(S::kParts == 1 && S::kHidden > 0 && L % 16 == 0 && S::kV <= 8,
+                  "fixed one-part rows of at most 8 slots");
+    const int per_item = threads / L;
+    const int items = (S::kHidden + threads - 1) / threads;
+    const int calls = (items + 3) / 4;
+    // Threads k * L + l with k >= H / L own no column (item 0 is already past
+    // the row), so their draws are skipped.
+    const int k_end = per_item < kChunks ? per_item : kChunks;
+    for (int k = 0; k < k_end; ++k) {
+        const uint64_t subsequence = static_cast<uint64_t>(row) * threads + k * L + lane;
+        for (int n = 0; n < calls; ++n) {
+            const uint64_t low = position + n;
+            const uint64_t high = subsequence + (low < position ? 1 : 0);
+            const uint4 random = philox4x32_10(
+                make_uint4(static_cast<uint32_t>(low), static_cast<uint32_t>(low >> 32),
+                           static_cast<uint32_t>(high), static_cast<uint32_t>(high >> 32)),
+                key0, key1);
+            const uint32_t draws[4] = {random.x, random.y, random.z, random.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int item = 4 * n + e;
+                const int chunk = item * per_item + k;
+                if (item < items && chunk < kChunks) {
+                    const uint64_t ballot = __ballot(draws[e] >= threshold);
+                    if (lane < L / 16) {
+                        stage[chunk * (L / 16) + lane] =
+                            static_cast<uint16_t>(ballot >> (group * L + 16 * lane));
+                    }
+                }
+            }
+        }
+    }
+    uint32_t keep = 0;
+#pragma unroll
+    for (int v = 0; v < S::kV; ++v) {
+        const int vector = v * L + lane;
+        keep |= ((static_cast<uint32_t>(stage[vector / 4]) >> (4 * (vector % 4))) & 0xFu)
+            << (4 * v);
+    }
+    return keep;
+}
+
 // Rows are walked by teams: a wave (one or two rows at a time) when a row
 // fits one wave, else the whole block (kWaves / P rows at a time), so that
 // every wave of a block meets the same barriers.
@@ -620,6 +695,10 @@ void rln_forward_kernel(
     // arrays and a barrier per sum keep a wave that runs ahead from
     // overwriting a value another wave has yet to read.
     __shared__ float exchange[2][T::kGroups][S::kParts];
+    // Keep bits of the reference's stream, staged per row (fixed shapes).
+    constexpr bool kReferenceStream = S::kHidden > 0;
+    constexpr int kStagePieces = kReferenceStream ? S::kHidden / 16 : 1;
+    __shared__ uint16_t stage[kReferenceStream ? T::kWaves * S::kRowsPerWave : 1][kStagePieces];
 
     f32x4 w[V];
     f32x4 b[V];
@@ -652,6 +731,7 @@ void rln_forward_kernel(
         key1 = static_cast<uint32_t>(seed >> 32);
         position = offset / 4;
     }
+    const bool reference_stream = kReferenceStream && dropout && philox.threads != 0;
 
     // Loads x and the branch of one row. The loads are unconditional (a row
     // past the end reads the last row instead, an idle slot its row's first
@@ -679,7 +759,23 @@ void rln_forward_kernel(
         }
     };
 
-    auto process_row = [&](const ForwardRow<V, B>& r, int64_t row) {
+    // The reference stream's keep bits of a row (0 in the library's layout,
+    // whose draws happen slot by slot in process_row). They depend on the
+    // row index only, so the loops below compute them a row ahead, while
+    // that row's loads or the previous row's stores are in flight.
+    auto reference_keep = [&](int64_t row) -> uint32_t {
+        if constexpr (kReferenceStream) {
+            if (reference_stream) {
+                const int wave = threadIdx.x / kWaveSize;
+                return reference_keep_bits<S>(stage[wave * S::kRowsPerWave + team.offset], row,
+                                              l, team.offset, philox.threads, position, key0,
+                                              key1, threshold);
+            }
+        }
+        return 0u;
+    };
+
+    auto process_row = [&](const ForwardRow<V, B>& r, int64_t row, uint32_t reference_bits) {
         const bool valid = row < rows;
         const int64_t base = row * hidden;
         f32x4 u[V];
@@ -687,26 +783,37 @@ void rln_forward_kernel(
 #pragma unroll
         for (int v = 0; v < V; ++v) {
             f32x4 bv = widen4<B>(r.branch[v]);
-            keep_bits[v] = 0;
             if (dropout) {
-                const uint64_t group = static_cast<uint64_t>(row) * (hidden / 4) + slots.vector(v);
-                const uint4 random = philox4x32_10(
-                    make_uint4(
-                        static_cast<uint32_t>(position),
-                        static_cast<uint32_t>(position >> 32),
-                        static_cast<uint32_t>(group),
-                        static_cast<uint32_t>(group >> 32)),
-                    key0,
-                    key1);
-                const uint32_t k0 = random.x >= threshold;
-                const uint32_t k1 = random.y >= threshold;
-                const uint32_t k2 = random.z >= threshold;
-                const uint32_t k3 = random.w >= threshold;
+                uint32_t k0, k1, k2, k3;
+                if (reference_stream) {
+                    const uint32_t bits = reference_bits >> (4 * v);
+                    k0 = bits & 1u;
+                    k1 = (bits >> 1) & 1u;
+                    k2 = (bits >> 2) & 1u;
+                    k3 = (bits >> 3) & 1u;
+                } else {
+                    const uint64_t group =
+                        static_cast<uint64_t>(row) * (hidden / 4) + slots.vector(v);
+                    const uint4 random = philox4x32_10(
+                        make_uint4(
+                            static_cast<uint32_t>(position),
+                            static_cast<uint32_t>(position >> 32),
+                            static_cast<uint32_t>(group),
+                            static_cast<uint32_t>(group >> 32)),
+                        key0,
+                        key1);
+                    k0 = random.x >= threshold;
+                    k1 = random.y >= threshold;
+                    k2 = random.z >= threshold;
+                    k3 = random.w >= threshold;
+                }
                 bv.x = round_to_branch<B>(bv.x * static_cast<float>(k0) * scale);
                 bv.y = round_to_branch<B>(bv.y * static_cast<float>(k1) * scale);
                 bv.z = round_to_branch<B>(bv.z * static_cast<float>(k2) * scale);
                 bv.w = round_to_branch<B>(bv.w * static_cast<float>(k3) * scale);
                 keep_bits[v] = k0 | (k1 << 1) | (k2 << 2) | (k3 << 3);
+            } else {
+                keep_bits[v] = 0;
             }
             u[v] = r.x[v] + bv;
             if (valid && slots.active(v)) {
@@ -781,20 +888,23 @@ void rln_forward_kernel(
     }
     ForwardRow<V, B> current;
     load_row(current, first + team.offset, false);
+    uint32_t keep = reference_keep(first + team.offset);
     if (paced) {
         for (; first + stride < rows; first += stride) {
-            process_row(current, first + team.offset);
+            process_row(current, first + team.offset, keep);
+            keep = reference_keep(first + stride + team.offset);
             load_row(current, first + stride + team.offset, true);
         }
     } else {
         for (; first + stride < rows; first += stride) {
             ForwardRow<V, B> next;
             load_row(next, first + stride + team.offset, false);
-            process_row(current, first + team.offset);
+            process_row(current, first + team.offset, keep);
+            keep = reference_keep(first + stride + team.offset);
             current = next;
         }
     }
-    process_row(current, first + team.offset);
+    process_row(current, first + team.offset, keep);
 }
 
 // ----------------------------------------------------------------------------

@@ -12,8 +12,12 @@
 // bfloat16 normalized output) and `branch_dtype` (backward; names a bfloat16
 // branch, which the reference's `branch_is_half` flag cannot express). The
 // reference's launch hints (threads, block_rows, parameter_threads,
-// parameter_groups) are validated with the reference's messages and otherwise
-// ignored: the MI355X library picks its own launch shape.
+// parameter_groups) are validated with the reference's messages; the MI355X
+// library picks its own launch shape. `threads` keeps one meaning: on the
+// reference's hidden sizes (128-1024) dropout draws the reference's hipRAND
+// stream of a `threads`-wide launch, so the masks equal the reference's for
+// the same generator state; other hidden sizes, which the reference does not
+// run natively, use the library's own stream layout.
 //
 // This file owns what the C ABI leaves to the caller: tensor allocation on
 // the caching allocator, the device guard, the current HIP stream, the
@@ -165,20 +169,28 @@ void check_backward_inputs(
     }
 }
 
+// The dropout layout for `threads` (rln_philox_t::threads): the reference's
+// where it exists for this hidden size, else the library's own (0).
+int64_t layout_threads(int64_t hidden, int64_t threads) {
+    return rln_philox_increment(hidden, threads) != 0 ? threads : 0;
+}
+
 // Reserves rln_philox_increment() offset units from the device's default
 // generator (the reference does the same at
 // csrc/residual_layer_norm_kernel.hip:1762-1779). Under HIP graph capture the
 // generator hands out device pointers that the kernel reads at replay time,
 // so captured graphs draw fresh masks on every replay.
-rln_philox_t reserve_philox(const at::Tensor& x, int64_t hidden) {
+rln_philox_t reserve_philox(const at::Tensor& x, int64_t hidden, int64_t threads) {
+    const uint64_t increment = rln_philox_increment(hidden, threads);
+    check_status(increment != 0 ? RLN_OK : RLN_ERR_INVALID);
     auto generator = at::cuda::detail::getDefaultCUDAGenerator(x.device().index());
     at::PhiloxCudaState state;
     {
         std::lock_guard<std::mutex> lock(generator.mutex());
-        state = generator.get<at::CUDAGeneratorImpl>()->philox_cuda_state(
-            rln_philox_increment(hidden));
+        state = generator.get<at::CUDAGeneratorImpl>()->philox_cuda_state(increment);
     }
     rln_philox_t philox{};
+    philox.threads = threads;
     if (state.captured_) {
         philox.seed_ptr = state.seed_.ptr;
         philox.offset_ptr = state.offset_.ptr;
@@ -227,7 +239,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> forward_i
     auto mask = at::empty({dropout ? rln_mask_words(rows, hidden) : 0}, x.options().dtype(at::kInt));
     rln_philox_t philox{};
     if (dropout) {
-        philox = reserve_philox(x, hidden);
+        philox = reserve_philox(x, hidden, layout_threads(hidden, threads));
     }
     // Optional weight/bias gradient sums for the backward of this call,
     // zeroed by the forward launch itself.

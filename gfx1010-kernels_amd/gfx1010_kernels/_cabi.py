@@ -29,13 +29,15 @@ RLN_ERR_HIP = 3
 
 
 class RlnPhilox(ctypes.Structure):
-    """``rln_philox_t``."""
+    """``rln_philox_t``; ``threads`` 0 selects the library's dropout layout,
+    128 / 192 / 256 the reference's hipRAND stream of that launch width."""
 
     _fields_ = [
         ("seed", ctypes.c_uint64),
         ("offset", ctypes.c_uint64),
         ("seed_ptr", ctypes.c_void_p),
         ("offset_ptr", ctypes.c_void_p),
+        ("threads", ctypes.c_int64),
     ]
 
 
@@ -61,7 +63,7 @@ SIGNATURES = {
          ctypes.c_double, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P, ctypes.c_size_t, _P],
     ),
     "rln_backward_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, ctypes.c_int]),
-    "rln_philox_increment": (ctypes.c_uint64, [_I64]),
+    "rln_philox_increment": (ctypes.c_uint64, [_I64, _I64]),
     "rln_mask_words": (_I64, [_I64, _I64]),
     "rln_hidden_supported": (ctypes.c_int, [_I64]),
     "rln_supported_hidden_sizes": (ctypes.c_int, [ctypes.POINTER(_I64), ctypes.c_int]),
@@ -140,8 +142,8 @@ def backward_workspace_bytes(rows: int, hidden: int, deterministic: bool) -> int
     return int(library().rln_backward_workspace_bytes(rows, hidden, int(bool(deterministic))))
 
 
-def philox_increment(hidden: int) -> int:
-    return int(library().rln_philox_increment(hidden))
+def philox_increment(hidden: int, threads: int = 0) -> int:
+    return int(library().rln_philox_increment(hidden, threads))
 
 
 def mask_words(rows: int, hidden: int) -> int:

@@ -3,9 +3,12 @@
 Mirrors gfx1010_kernels/_normalization_native.py of the reference (lazy ``_C``
 import :57-63, ``native_extension_status`` :66-68, ``native_residual_layer_norm``
 :71-99). The reference chooses gfx1010-tuned launch hints here (:5-54); the
-MI355X library chooses its own launch shape from (rows, hidden), so this
-module forwards fixed, valid hint values that the extension range-checks and
-otherwise ignores.
+MI355X library chooses its own launch shape from (rows, hidden). Of the
+hints, only ``threads`` still matters: it names the reference launch whose
+hipRAND dropout stream the kernels reproduce, so this module passes the
+reference's own table (:5-12) and the masks equal the reference package's
+for the same generator state. The other hints are fixed, valid values that
+the extension range-checks and otherwise ignores.
 """
 
 from __future__ import annotations
@@ -30,9 +33,19 @@ NATIVE_HIDDEN_SIZES_TEXT = (
     f"to {MAX_NATIVE_HIDDEN_SIZE}")
 TARGET_ARCHITECTURE = "gfx950"
 
-# Interface-compatibility launch hints (threads, block_rows, parameter_threads,
-# parameter_groups); parameter_groups=1 is valid for every row count.
-_LAUNCH_HINTS = (128, 64, 64, 1)
+# The reference's threads per row (reference _normalization_native.py:5-12),
+# which fix its dropout stream; 128 for the sizes it does not run natively.
+_THREADS = {128: 128, 256: 128, 384: 128, 512: 128, 768: 128, 1024: 192}
+
+
+def launch_threads(hidden_size: int) -> int:
+    """The ``threads`` hint the reference passes for ``hidden_size``."""
+    return _THREADS.get(hidden_size, 128)
+
+
+# The remaining launch hints (block_rows, parameter_threads, parameter_groups);
+# parameter_groups=1 is valid for every row count.
+_LAUNCH_HINTS = (64, 64, 1)
 
 
 @lru_cache(maxsize=1)
@@ -73,6 +86,7 @@ def native_residual_layer_norm(
             float(dropout_p),
             float(eps),
             bool(training),
+            launch_threads(x.shape[-1]),
             *_LAUNCH_HINTS,
             normalized_dtype=normalized_dtype,
         )
@@ -81,6 +95,7 @@ def native_residual_layer_norm(
 
 __all__ = [
     "NATIVE_HIDDEN_SIZES",
+    "launch_threads",
     "SPECIALIZED_HIDDEN_SIZES",
     "TARGET_ARCHITECTURE",
     "native_extension_status",

@@ -10,10 +10,10 @@ fused op instead of breaking around it (the reference does not support
 
 * ``gfx1010_kernels::rln_forward(x, branch, weight, bias, dropout_p, eps, training,
   normalized_dtype) -> (updated, normalized, mean, rstd, mask)`` runs
-  ``_C.residual_layer_norm_forward``; with dropout it reserves its Philox
-  offsets from the device's default generator when it executes, exactly as
-  the eager path does, so compiled and eager runs draw the same masks from the
-  same RNG state.
+  ``_C.residual_layer_norm_forward`` with the eager path's ``threads``; with
+  dropout it reserves its Philox offsets from the device's default generator
+  when it executes, exactly as the eager path does, so compiled and eager runs
+  draw the same masks from the same RNG state.
 * ``gfx1010_kernels::rln_backward(grad_updated, grad_normalized, updated, weight,
   mean, rstd, mask, dropout_p, training, branch_dtype)
   -> (grad_x, grad_branch, grad_weight, grad_bias)`` runs
@@ -28,13 +28,12 @@ from typing import Optional
 import torch
 from torch import Tensor
 
-from ._normalization_native import TARGET_ARCHITECTURE, _extension
+from ._normalization_native import TARGET_ARCHITECTURE, _extension, launch_threads
 
 _NAMESPACE = "gfx1010_kernels"
 
-# Interface-compatibility launch hints the raw entry points range-check
+# Interface-compatibility launch hints the raw backward range-checks
 # (threads, block_rows, parameter_threads, parameter_groups).
-_THREADS = 128
 _BACKWARD_HINTS = (128, 64, 64, 1)
 
 
@@ -58,7 +57,8 @@ def rln_forward(
 ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     return tuple(
         _native().residual_layer_norm_forward(
-            x, branch, weight, bias, float(dropout_p), float(eps), bool(training), _THREADS,
+            x, branch, weight, bias, float(dropout_p), float(eps), bool(training),
+            launch_threads(x.shape[-1]),
             normalized_dtype=normalized_dtype,
         )
     )

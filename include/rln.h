@@ -62,12 +62,25 @@ enum rln_status {
  * are read when the kernel runs (effective offset = *offset_ptr + offset).
  * Replaces the seed/offset reservation at
  * csrc/residual_layer_norm_kernel.hip:1755-1780.
+ *
+ * `threads` selects the layout of the stream over the tensor:
+ *  - 128, 192 or 256: the reference's own, the hipRAND Philox stream of its
+ *    forward launched with that many threads per row (reference
+ *    csrc/residual_layer_norm_kernel.hip:449-511; the reference's Python
+ *    passes 128, or 192 for hidden 1024, gfx1010_kernels/_normalization_native.py:5-12).
+ *    Same (seed, offset, threads) => the reference's mask, bit for bit.
+ *    Hidden sizes 128, 256, 384, 512, 768 and 1024 only, and the offset
+ *    (offset, plus *offset_ptr under capture) must be a multiple of 4, as
+ *    torch's generator hands out.
+ *  - 0: this library's layout, one Philox block per four consecutive columns
+ *    (counter = (offset / 4, (row * hidden + column) / 4)); every hidden size.
  */
 typedef struct rln_philox {
     uint64_t seed;             /* used when seed_ptr == NULL            */
     uint64_t offset;           /* absolute offset, or intra-graph delta */
     const int64_t* seed_ptr;   /* device pointer or NULL                */
     const int64_t* offset_ptr; /* device pointer or NULL                */
+    int64_t threads;           /* 0, or 128 / 192 / 256 (see above)     */
 } rln_philox_t;
 
 /*
@@ -81,7 +94,8 @@ typedef struct rln_philox {
  * dropout_mask: rln_mask_words(rows, hidden) uint32 words, written only when
  * training && dropout_p > 0 (may be NULL otherwise). `philox` is read only in
  * that case (may be NULL otherwise). The call consumes
- * rln_philox_increment(hidden) offset units of the Philox stream.
+ * rln_philox_increment(hidden, philox->threads) offset units of the Philox
+ * stream.
  * zero_grad_weight, zero_grad_bias: both NULL, or fp32 [hidden] each, set to
  * zero by this launch: the weight/bias gradient sums of a later
  * rln_backward(..., accumulate_parameters = 1), which then needs no zeroing
@@ -164,9 +178,11 @@ size_t rln_backward_workspace_bytes(
     int64_t hidden,
     int deterministic);
 
-/* Philox offset units one dropout forward consumes (torch's `increment`;
- * the reference computes its own at csrc/residual_layer_norm_kernel.hip:1766-1770). */
-uint64_t rln_philox_increment(int64_t hidden);
+/* Philox offset units one dropout forward consumes (torch's `increment`):
+ * 4 for threads == 0; for the reference's layout its own
+ * 4 * ceil(ceil(hidden / threads) / 4) (csrc/residual_layer_norm_kernel.hip:1766-1770).
+ * 0 (with rln_last_error set) for an unsupported hidden / threads pair. */
+uint64_t rln_philox_increment(int64_t hidden, int64_t threads);
 
 /* Number of uint32 dropout-mask words for [rows, hidden] (the reference's
  * mask size, csrc/residual_layer_norm_kernel.hip:1750-1753, :162-164). */

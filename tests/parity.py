@@ -118,22 +118,53 @@ def generator_state(device=DEVICE):
     return generator.initial_seed(), generator.get_offset()
 
 
-def oracle_keep(rows, hidden, dropout_p, training, seed, offset):
+# The reference's threads per row (reference _normalization_native.py:5-12),
+# which the public API passes too. On these hidden sizes a call's `threads`
+# selects the reference's hipRAND dropout stream; on the others (and with
+# threads = 0 through the C ABI) the library's own layout is drawn.
+REFERENCE_THREADS = {128: 128, 256: 128, 384: 128, 512: 128, 768: 128, 1024: 192}
+API = "api"  # the `threads` the public API passes for the hidden size
+
+
+def stream_threads(hidden, threads):
+    """The dropout layout of a call: the reference's launch width, or 0."""
+    if threads == API:
+        threads = REFERENCE_THREADS.get(hidden, 0)
+    return threads if hidden in REFERENCE_THREADS else 0
+
+
+def oracle_mask_rows(first_row, rows, hidden, seed, offset, threshold, threads=128):
+    """Oracle mask words of rows [first_row, first_row + rows) for a call with `threads`."""
+    layout = stream_threads(hidden, threads)
+    if layout:
+        return oracle.reference_mask_rows(first_row, rows, hidden, layout, seed, offset, threshold)
+    return oracle.dropout_mask_rows(first_row, rows, hidden, seed, offset, threshold)
+
+
+def philox_increment(hidden, threads=128):
+    """Offset units a call with `threads` reserves."""
+    layout = stream_threads(hidden, threads)
+    return oracle.reference_philox_increment(hidden, layout) if layout else 4
+
+
+def oracle_keep(rows, hidden, dropout_p, training, seed, offset, threads=128):
     active, scale, threshold = oracle.dropout_constants(dropout_p, training)
     if not active:
         return None, scale, None
-    words = oracle.dropout_mask_words(rows, hidden, seed, offset, threshold)
+    words = oracle_mask_rows(0, rows, hidden, seed, offset, threshold, threads)
     return oracle.decode_mask(words, rows, hidden), scale, words
 
 
-def check_forward(outputs, inputs, dropout_p, training, eps, seed, offset, what=""):
-    """Compare raw forward outputs (updated, normalized, mean, rstd, mask) to the oracle."""
+def check_forward(outputs, inputs, dropout_p, training, eps, seed, offset, what="", threads=128):
+    """Compare raw forward outputs (updated, normalized, mean, rstd, mask) to the
+    oracle; `threads` is the call's (0 for the C ABI's own layout, API for the
+    public API's)."""
     updated, normalized, mean, rstd, mask = outputs
     branch_kind = kind(inputs[1])
     x, branch, weight, bias = (host(t) for t in inputs)
     hidden = x.shape[-1]
     rows = x.size // hidden
-    keep, scale, words = oracle_keep(rows, hidden, dropout_p, training, seed, offset)
+    keep, scale, words = oracle_keep(rows, hidden, dropout_p, training, seed, offset, threads)
     if words is not None:
         assert_bitwise(host(mask).view(np.uint32), words, f"{what} mask")
     else:

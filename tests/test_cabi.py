@@ -45,11 +45,25 @@ def test_library_metadata():
 
 
 def test_philox_struct_layout():
-    assert ctypes.sizeof(_cabi.RlnPhilox) == 32
+    assert ctypes.sizeof(_cabi.RlnPhilox) == 40
+    assert _cabi.RlnPhilox.threads.offset == 32
+    assert _cabi.RlnPhilox(1, 2, None, None).threads == 0
+
+
+@pytest.mark.parametrize("hidden,threads,increment", [
+    (768, 0, 4), (1600, 0, 4), (8192, 0, 4),
+    # The reference's 4 * ceil(ceil(H / threads) / 4)
+    # (csrc/residual_layer_norm_kernel.hip:1766-1770).
+    (128, 128, 4), (512, 128, 4), (768, 128, 8), (1024, 128, 8), (1024, 192, 8),
+    (1024, 256, 4), (768, 256, 4), (384, 192, 4),
+    # No reference layout: other sizes, other widths.
+    (1600, 128, 0), (640, 256, 0), (768, 64, 0), (768, 512, 0), (100, 0, 0),
+])
+def test_philox_increment(hidden, threads, increment):
+    assert _cabi.philox_increment(hidden, threads) == increment
 
 
 def test_size_queries():
-    assert _cabi.philox_increment(768) == 4
     assert _cabi.mask_words(8192, 768) == 8192 * 24
     assert _cabi.mask_words(0, 768) == 0
     assert _cabi.backward_workspace_bytes(8192, 768, False) == 0
@@ -99,6 +113,12 @@ def _forward(**overrides):
         (dict(rows=1 << 62), _cabi.RLN_ERR_INVALID, "overflows"),
         (dict(zero_grad_weight=FAKE), _cabi.RLN_ERR_INVALID,
          "zero_grad_weight and zero_grad_bias must both be given or both be null"),
+        (dict(philox=_cabi.RlnPhilox(1, 0, None, None, 64)), _cabi.RLN_ERR_INVALID,
+         "threads must be 0, 128, 192 or 256"),
+        (dict(hidden=1600, philox=_cabi.RlnPhilox(1, 0, None, None, 128)),
+         _cabi.RLN_ERR_UNSUPPORTED, "reference's dropout stream exists for hidden sizes"),
+        (dict(philox=_cabi.RlnPhilox(1, 6, None, None, 128)), _cabi.RLN_ERR_INVALID,
+         "offset that is a multiple of 4"),
     ],
 )
 def test_forward_rejects_invalid_arguments(overrides, status, message):

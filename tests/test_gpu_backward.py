@@ -168,8 +168,8 @@ def test_autograd_matches_oracle_through_public_api():
                                               implementation="gfx950")
     grad_updated, grad_normalized = make_grads((rows, hidden), seed=4)
     torch.autograd.backward((updated, normalized), (grad_updated, grad_normalized))
-    from parity import oracle_keep
-    keep, scale, _ = oracle_keep(rows, hidden, 0.1, True, seed, offset)
+    from parity import API, oracle_keep
+    keep, scale, _ = oracle_keep(rows, hidden, 0.1, True, seed, offset, API)
     check_backward((x.grad, branch.grad, weight.grad, bias.grad), grad_updated, grad_normalized,
                    updated, weight, 1e-5, keep, scale, "autograd")
 

@@ -80,7 +80,8 @@ def test_parameter_gradients_and_accumulation(rows, hidden, deterministic):
     out = forward(inputs, 0.1, seed, offset)
     torch.cuda.synchronize()
     keep, scale = check_forward((out["updated"], out["normalized"], out["mean"], out["rstd"],
-                                 out["mask"]), inputs, 0.1, True, EPS, seed, offset, "c-abi")
+                                 out["mask"]), inputs, 0.1, True, EPS, seed, offset, "c-abi",
+                                threads=0)
     parameters = torch.full((2, hidden), float("nan"), device="cuda")
     workspace = new_workspace(rows, hidden) if deterministic else None
     grad_x, grad_branch = backward(out, grads, inputs[2], torch.float16, 0.1, deterministic,
@@ -135,7 +136,7 @@ def test_backward_without_parameter_gradients():
         None, None, rows, hidden, 0.2, True, True, None, 0, stream)
     torch.cuda.synchronize()
     keep, scale = check_forward((out["updated"], out["normalized"], out["mean"], out["rstd"],
-                                 out["mask"]), inputs, 0.2, True, EPS, 77, 8)
+                                 out["mask"]), inputs, 0.2, True, EPS, 77, 8, threads=0)
     check_backward((grad_x, grad_branch, None, None), grads[0], grads[1], out["updated"],
                    inputs[2], EPS, keep, scale, "no parameters", parameters=False)
 
@@ -166,7 +167,8 @@ def test_forward_zeroes_the_parameter_sums_of_the_next_backward(hidden, determin
     torch.cuda.synchronize()
     assert torch.count_nonzero(sums).item() == 0 and not torch.isnan(sums).any()
     keep, scale = check_forward((out["updated"], out["normalized"], out["mean"], out["rstd"],
-                                 out["mask"]), inputs, 0.1, True, EPS, seed, offset, "zeroing")
+                                 out["mask"]), inputs, 0.1, True, EPS, seed, offset, "zeroing",
+                                threads=0)
     workspace = new_workspace(rows, hidden) if deterministic else None
     grad_x, grad_branch = backward(out, grads, weight, torch.float16, 0.1, deterministic, True,
                                    sums, workspace)

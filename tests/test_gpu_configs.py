@@ -29,6 +29,7 @@ from parity import (
     host,
     make_grads,
     make_inputs,
+    oracle_mask_rows,
 )
 
 pytestmark = pytest.mark.gpu
@@ -68,7 +69,8 @@ def keep_count(mask):
     return int(table[mask.view(torch.uint8).long()].sum())
 
 
-def check_sampled_rows(inputs, grads, outputs, gradients, dropout_p, seed, offset, sample=24):
+def check_sampled_rows(inputs, grads, outputs, gradients, dropout_p, seed, offset, sample=24,
+                       threads=128):
     x, branch, weight, bias = inputs
     rows, hidden = x.shape
     rng = np.random.default_rng(rows + hidden)
@@ -78,7 +80,8 @@ def check_sampled_rows(inputs, grads, outputs, gradients, dropout_p, seed, offse
     keep = None
     if active:
         words = np.concatenate([
-            oracle.dropout_mask_rows(int(r), 1, hidden, seed, offset, threshold) for r in picked])
+            oracle_mask_rows(int(r), 1, hidden, seed, offset, threshold, threads)
+            for r in picked])
         gpu_words = host(outputs[4].view(rows, hidden // 32).index_select(0, index)).view(np.uint32)
         assert_bitwise(gpu_words.ravel(), words, "sampled mask")
         keep = oracle.decode_mask(words, len(picked), hidden)

@@ -14,20 +14,35 @@ import torch
 
 from gfx1010_kernels import _C, _cabi, residual_layer_norm
 from oracle import rln_oracle as oracle
-from parity import assert_bitwise, check_forward, generator_state, host, make_inputs
+from parity import (
+    API,
+    REFERENCE_THREADS,
+    assert_bitwise,
+    check_forward,
+    generator_state,
+    host,
+    make_inputs,
+    philox_increment,
+)
 
 pytestmark = pytest.mark.gpu
 
 
-def test_call_reserves_four_offset_units_only_when_dropout_is_active():
-    inputs = make_inputs((8, 768), torch.float16, seed=1)
+@pytest.mark.parametrize("hidden,increment", [(128, 4), (512, 4), (768, 8), (1024, 8),
+                                              (1600, 4)])
+def test_call_reserves_the_reference_increment_only_when_dropout_is_active(hidden, increment):
+    """The reference reserves 4 * ceil(ceil(H / threads) / 4) offset units per
+    dropout call (csrc/residual_layer_norm_kernel.hip:1766-1770) with its
+    threads table: 8 at H = 768 and 1024, 4 below; sizes the reference does
+    not run natively reserve the library layout's 4."""
+    inputs = make_inputs((8, hidden), torch.float16, seed=1)
     torch.cuda.manual_seed(5)
     _, start = generator_state()
     residual_layer_norm(*inputs, dropout_p=0.1, implementation="gfx950")
-    assert generator_state()[1] == start + _cabi.philox_increment(768) == start + 4
+    assert generator_state()[1] == start + philox_increment(hidden, API) == start + increment
     residual_layer_norm(*inputs, dropout_p=0.1, training=False, implementation="gfx950")
     residual_layer_norm(*inputs, dropout_p=0.0, training=True, implementation="gfx950")
-    assert generator_state()[1] == start + 4
+    assert generator_state()[1] == start + increment
 
 
 def test_eval_bypasses_dropout_without_consuming_rng():
@@ -47,7 +62,8 @@ def test_consecutive_calls_draw_the_next_disjoint_streams():
     first = _C.residual_layer_norm_forward(*inputs, 0.5, 1e-5, True, 128)
     second = _C.residual_layer_norm_forward(*inputs, 0.5, 1e-5, True, 128)
     check_forward(first, inputs, 0.5, True, 1e-5, seed, offset, "first")
-    check_forward(second, inputs, 0.5, True, 1e-5, seed, offset + 4, "second")
+    check_forward(second, inputs, 0.5, True, 1e-5, seed, offset + philox_increment(768),
+                  "second")
     assert not torch.equal(first[4], second[4])
     # The reference's overlap probe (edge_cases:339-375).
     x = torch.zeros(3, 768, device="cuda")
@@ -119,7 +135,7 @@ def test_explicit_seed_and_offset_through_the_c_abi():
                   _cabi.RlnPhilox(seed, offset, None, None), stream)
     torch.cuda.synchronize()
     check_forward((updated, normalized, mean, rstd, mask), (x, branch, weight, bias), 0.3, True,
-                  1e-5, seed, offset, "c-abi")
+                  1e-5, seed, offset, "c-abi", threads=0)
 
 
 def test_graph_replays_draw_fresh_masks_from_the_generator():

@@ -12,6 +12,7 @@ import torch
 from gfx1010_kernels import _C, residual_layer_norm
 from oracle import rln_oracle as oracle
 from parity import (
+    REFERENCE_THREADS,
     SPECIALIZED_HIDDEN_SIZES,
     assert_bitwise,
     check_backward,
@@ -65,8 +66,8 @@ def test_public_api_autograd_with_half_output(normalized_dtype):
     grad_normalized = grad_normalized.to(normalized.dtype)
     torch.autograd.backward((updated, normalized), (grad_updated, grad_normalized))
     torch.cuda.synchronize()
-    keep_words = oracle.dropout_mask_words(
-        rows, hidden, seed, offset, oracle.dropout_constants(0.2)[2])
+    keep_words = oracle.reference_mask_words(
+        rows, hidden, REFERENCE_THREADS[hidden], seed, offset, oracle.dropout_constants(0.2)[2])
     keep = oracle.decode_mask(keep_words, rows, hidden)
     _, scale, _ = oracle.dropout_constants(0.2)
     expected = oracle.forward(host(inputs[0]), host(inputs[1]), host(inputs[2]),

@@ -11,6 +11,7 @@ import torch
 
 from gfx1010_kernels import _C, residual_layer_norm
 from parity import (
+    REFERENCE_THREADS,
     SPECIALIZED_HIDDEN_SIZES,
     assert_bitwise,
     check_forward,
@@ -37,8 +38,10 @@ def test_forward_matches_oracle(hidden, branch_dtype, mode):
     inputs = make_inputs((37, hidden), branch_dtype, seed=17 + hidden)
     torch.cuda.manual_seed(2026 + hidden)
     seed, offset = generator_state()
-    outputs = _C.residual_layer_norm_forward(*inputs, dropout_p, 1e-5, training, 128)
-    check_forward(outputs, inputs, dropout_p, training, 1e-5, seed, offset, f"H={hidden} {mode}")
+    threads = REFERENCE_THREADS[hidden]  # what the public API passes
+    outputs = _C.residual_layer_norm_forward(*inputs, dropout_p, 1e-5, training, threads)
+    check_forward(outputs, inputs, dropout_p, training, 1e-5, seed, offset, f"H={hidden} {mode}",
+                  threads=threads)
 
     # The public strict API runs the same computation for the same RNG state.
     torch.cuda.manual_seed(2026 + hidden)
