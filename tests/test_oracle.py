@@ -1,8 +1,8 @@
 """Pins the CPU oracle (oracle/) before it is trusted as the GPU checker.
 
 Every oracle function is checked against something that does not restate it:
-published known-answer vectors, PyTorch float64 golden vectors, closed forms,
-invariants and finite differences.
+published known-answer vectors, rocRAND's own outputs, PyTorch float64 golden
+vectors, closed forms, invariants and finite differences.
 """
 
 import json
@@ -153,6 +153,23 @@ def test_reference_philox_increment(hidden, threads, increment):
 def test_reference_mask_rejects_more_than_eight_values_per_thread():
     with pytest.raises(ValueError, match="at most 8 values"):
         oracle.reference_mask_words(1, 2048, 128, 1, 0, 1 << 30)
+
+
+@pytest.mark.skipif(not Path("/opt/rocm/include/rocrand/rocrand_philox4x32_10.h").exists(),
+                    reason="rocRAND headers are not installed")
+def test_hiprand_fixtures_regenerate_from_rocrand(tmp_path, monkeypatch):
+    """The committed fixtures are exactly what rocRAND's own engine outputs:
+    rebuilding the generator against the installed headers reproduces them."""
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location(
+        "make_hiprand_vectors", GOLDEN / "make_hiprand_vectors.py")
+    generator = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(generator)
+    monkeypatch.setattr(generator, "OUT", tmp_path / "vectors.json")
+    generator.main()
+    fresh = json.loads((tmp_path / "vectors.json").read_text())
+    assert fresh == _hiprand_vectors()
 
 
 def test_reference_mask_keep_ratio_is_binomial():
