@@ -356,6 +356,13 @@ __device__ __forceinline__ uint32_t or8(uint32_t value) {
 // Shaw, "Parallel random numbers: as easy as 1, 2, 3", SC'11):
 //   (hi0, lo0) = M0 * c0; (hi1, lo1) = M1 * c2
 //   c' = (hi1 ^ c1 ^ k0, lo1, hi0 ^ c3 ^ k1, lo0);  k += (W0, W1)
+// A round is two v_mad_u64_u32 (quarter rate) and two three-input XORs, each
+// one gfx950 v_bitop3_b32 (truth table 0x96) instead of two v_xor_b32; the
+// compiler does not form it from the XOR chain itself.
+
+__device__ __forceinline__ uint32_t xor3(uint32_t a, uint32_t b, uint32_t c) {
+    return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96);
+}
 
 __device__ __forceinline__ uint4 philox4x32_10(uint4 counter, uint32_t k0, uint32_t k1) {
 #pragma unroll
@@ -363,9 +370,9 @@ __device__ __forceinline__ uint4 philox4x32_10(uint4 counter, uint32_t k0, uint3
         const uint64_t product0 = static_cast<uint64_t>(0xD2511F53u) * counter.x;
         const uint64_t product1 = static_cast<uint64_t>(0xCD9E8D57u) * counter.z;
         counter = make_uint4(
-            static_cast<uint32_t>(product1 >> 32) ^ counter.y ^ k0,
+            xor3(static_cast<uint32_t>(product1 >> 32), counter.y, k0),
             static_cast<uint32_t>(product1),
-            static_cast<uint32_t>(product0 >> 32) ^ counter.w ^ k1,
+            xor3(static_cast<uint32_t>(product0 >> 32), counter.w, k1),
             static_cast<uint32_t>(product0));
         k0 += 0x9E3779B9u;
         k1 += 0xBB67AE85u;
@@ -762,7 +769,9 @@ void rln_forward_kernel(
     // The reference stream's keep bits of a row (0 in the library's layout,
     // whose draws happen slot by slot in process_row). They depend on the
     // row index only, so the loops below compute them a row ahead, while
-    // that row's loads or the previous row's stores are in flight.
+    // that row's loads or the previous row's stores are in flight. (Drawing
+    // the library's layout a row ahead too measured within +-2 %, either
+    // way, by hidden size.)
     auto reference_keep = [&](int64_t row) -> uint32_t {
         if constexpr (kReferenceStream) {
             if (reference_stream) {
