@@ -156,11 +156,14 @@ def sweep_workloads() -> list[Workload]:
     workloads.append(Workload("C1 bf16-out", 8 * 1024, 768, "bf16", 0.5, 0.1, seed=1001,
                               normalized="bf16"))
     # The library's own Philox layout (a quarter fewer Philox blocks than the
-    # reference's stream at H = 768) at the C1 and C2 H=768 shapes.
+    # reference's stream at H = 768, three quarters fewer at H = 128) at the
+    # C1, C2 H=768 and C2 H=128 shapes.
     workloads.append(Workload("C1 own-stream", 8 * 1024, 768, "f16", 0.5, 0.1, seed=1001,
                               threads=0))
     workloads.append(Workload("C2 H=768 own-stream", 262144, 768, "f16", 1.0, 0.15,
                               seed=1002 + 768, threads=0))
+    workloads.append(Workload("C2 H=128 own-stream", 262144, 128, "f16", 1.0, 0.15,
+                              seed=1002 + 128, threads=0))
     workloads.append(Workload("C2 H=768 bf16-out", 262144, 768, "bf16", 1.0, 0.15,
                               seed=1770, normalized="bf16"))
     # Hidden sizes the reference does not serve natively (run-time row length,
