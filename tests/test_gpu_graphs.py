@@ -13,7 +13,15 @@ import pytest
 import torch
 
 from gfx1010_kernels import _C
-from parity import check_backward, check_forward, generator_state, host, make_grads, make_inputs
+from parity import (
+    check_backward,
+    check_forward,
+    generator_state,
+    host,
+    make_grads,
+    make_inputs,
+    philox_increment,
+)
 from test_gpu_backward import deterministic_algorithms, raw_backward
 
 pytestmark = pytest.mark.gpu
@@ -55,3 +63,36 @@ def test_captured_training_step_replays(hidden, deterministic):
             step()  # eager work between replays
             torch.cuda.synchronize()
     assert not np.array_equal(masks[0], masks[1]) and not np.array_equal(masks[1], masks[2])
+
+
+@pytest.mark.parametrize("hidden,threads", [(1024, 192), (128, 256), (384, 128)])
+def test_captured_calls_draw_the_reference_stream_at_consecutive_offsets(hidden, threads):
+    """Two forwards captured in one graph draw the reference's stream at the
+    replay's base offset and at base + the reference's increment (8 at
+    H = 1024 with 192 threads, 4 below), read from the generator's device
+    pointers at replay time."""
+    rows = 97
+    inputs = make_inputs((rows, hidden), torch.float16, seed=hidden + threads)
+    torch.cuda.manual_seed(11)
+
+    def calls():
+        return [_C.residual_layer_norm_forward(*inputs, 0.2, EPS, True, threads)
+                for _ in range(2)]
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        calls()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outputs = calls()
+    increment = philox_increment(hidden, threads)
+    for replay in range(2):
+        seed, offset = generator_state()
+        graph.replay()
+        torch.cuda.synchronize()
+        for index, output in enumerate(outputs):
+            check_forward(output, inputs, 0.2, True, EPS, seed, offset + index * increment,
+                          f"replay {replay} call {index}", threads=threads)
+        assert generator_state()[1] == offset + 2 * increment
