@@ -58,6 +58,17 @@ MASKS = [
     (0, 2, 1024, 128, 5, 40, 0.1),
     (0, 2, 768, 256, 77, 24, 0.2),
     (40_000_000, 1, 768, 128, 3, 8, 0.1),
+    # Rows on either side of subsequence 2^32 (row * threads + t), a 64-bit
+    # seed, an offset past 2^32 * 4, and the rest of the size x threads grid.
+    ((1 << 25) - 1, 2, 768, 128, 0xFEDCBA9876543210, 4 * ((1 << 32) + 3), 0.1),
+    ((1 << 24) - 1, 2, 1024, 256, 0x0123456789ABCDEF, 4 * 17, 0.3),
+    (5, 3, 256, 256, 2024, 4 * 9, 0.1),
+    (1, 2, 384, 256, 99, 0, 0.05),
+    (0, 2, 512, 192, 1234, 4 * 3, 0.7),
+    (0, 1, 512, 256, 5, 4, 0.1),
+    (0, 2, 128, 192, 42, 4 * 100, 0.1),
+    (0, 2, 768, 192, 42, 4 * 101, 0.1),
+    (3, 2, 1024, 192, 0xFFFFFFFFFFFFFFFF, 8, 0.1),
 ]
 
 
