@@ -46,7 +46,8 @@ def test_opcheck_forward_and_backward():
 
 
 @pytest.mark.parametrize("implementation", ["gfx950", "auto"])
-@pytest.mark.parametrize("shape,dropout_p", [((4, 64, 768), 0.1), ((3, 97, 384), 0.0)])
+@pytest.mark.parametrize("shape,dropout_p", [((4, 64, 768), 0.1), ((3, 97, 384), 0.0),
+                                             ((2, 40, 1024), 0.2), ((2, 33, 1600), 0.1)])
 def test_compiled_step_matches_eager_bitwise(implementation, shape, dropout_p):
     inputs = make_inputs(shape, torch.float16, seed=11)
     grads = make_grads(shape, seed=12)
