@@ -33,7 +33,10 @@ Prints one JSON line:
 
 ``--sweep`` adds one JSON line per other BASELINE.json configuration (C0, the
 C2 hidden-size sweep, C3 deterministic, the C4 cases), each with the same
-fields for its own shape.
+fields for its own shape. ``--reference-table`` adds the reference's own
+published measurement, run on this GPU: public-API forward and training-step
+speedups over the PyTorch decomposition at B = 1, H = 384, T = 128 .. 4096,
+beside the speedups the reference publishes for gfx1010.
 
 Algorithmic bytes per row (H = hidden, bb = branch bytes, mask H/8 bytes when
 dropping):
@@ -191,7 +194,81 @@ def parse_args():
                         help="also launch one device copy of this many MiB (PMC calibration)")
     parser.add_argument("--prenorm", action="store_true",
                         help="also time a pre-norm transformer stack, fused vs unfused")
+    parser.add_argument("--reference-table", action="store_true",
+                        help="also print the reference's published speedup table, measured here")
     return parser.parse_args()
+
+
+# The reference's published speedups over its PyTorch decomposition on the
+# RX 5600 XT (gfx1010): B = 1, H = 384, fp32 x, fp16 branch, p = 0.15, median
+# of 1000 event-timed calls after 100 warmup calls (reference README.md:403-416).
+REFERENCE_SPEEDUPS = {128: (1.273, 1.269), 256: (1.262, 1.265), 512: (1.303, 1.292),
+                      1024: (1.242, 1.299), 2048: (1.792, 1.846), 4096: (1.839, 2.021)}
+# Sequence lengths added on MI355X, where the reference's ones are host-bound
+# (a call is done before its launch overhead): the same measurement where
+# the GPU work dominates.
+EXTRA_SEQUENCES = (16384, 65536, 262144)
+
+
+def reference_table(torch, warmup: int = 100, reps: int = 1000) -> list[dict]:
+    """The reference's own headline measurement, on this GPU: the public
+    forward and forward + backward (autograd.grad) call, fused native path
+    against implementation="torch" (the decomposition), one CUDA-event pair
+    around each call on the current stream, median / p20 / p80 of `reps`
+    calls after `warmup` (as the reference's
+    benchmarks/benchmark_residual_layer_norm.py:30-44, :213-264 measures)."""
+    from gfx1010_kernels import residual_layer_norm
+
+    def timed(call):
+        for _ in range(warmup):
+            call()
+        torch.cuda.synchronize()
+        events = []
+        for _ in range(reps):
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record()
+            call()
+            end.record()
+            events.append((start, end))
+        torch.cuda.synchronize()
+        samples = sorted(start.elapsed_time(end) for start, end in events)
+        pick = lambda fraction: samples[round(fraction * (len(samples) - 1))]  # noqa: E731
+        return {"median_ms": round(pick(0.5), 5), "p20_ms": round(pick(0.2), 5),
+                "p80_ms": round(pick(0.8), 5)}
+
+    hidden, dropout_p = 384, 0.15
+    lines = []
+    cases = [*REFERENCE_SPEEDUPS.items(), *((sequence, (None, None)) for sequence in EXTRA_SEQUENCES)]
+    for sequence, published in cases:
+        generator = torch.Generator(device="cuda").manual_seed(sequence)
+        shape = (1, sequence, hidden)
+        inputs = (
+            torch.randn(shape, device="cuda", generator=generator).requires_grad_(True),
+            torch.randn(shape, device="cuda", generator=generator).half().requires_grad_(True),
+            torch.randn(hidden, device="cuda", generator=generator).requires_grad_(True),
+            torch.randn(hidden, device="cuda", generator=generator).requires_grad_(True),
+        )
+        grads = tuple(torch.randn(shape, device="cuda", generator=generator) for _ in range(2))
+        line = {"kind": "reference_table", "B": 1, "T": sequence, "C": hidden,
+                "dropout_p": dropout_p, "branch": "float16", "warmup": warmup, "reps": reps}
+        for mode, index in (("forward", 0), ("train", 1)):
+            results = {}
+            for implementation in ("torch", "gfx950"):
+                def call(implementation=implementation, mode=mode):
+                    outputs = residual_layer_norm(*inputs, dropout_p=dropout_p, training=True,
+                                                  implementation=implementation)
+                    if mode == "train":
+                        torch.autograd.grad(outputs, inputs, grads)
+
+                results[implementation] = timed(call)
+            line[mode] = {
+                **results,
+                "speedup": round(results["torch"]["median_ms"] / results["gfx950"]["median_ms"], 3),
+                "reference_speedup_gfx1010": published[index],
+            }
+        lines.append(line)
+    return lines
 
 
 def prenorm_stack(torch, stream, depth: int = 12, hidden: int = 768, tokens: int = 8192,
@@ -689,6 +766,10 @@ def main() -> int:
         line = {"metric": "pre-norm stack fwd+bwd step time (ms)", "higher_is_better": False,
                 **prenorm_stack(torch, stream)}
         print(json.dumps(line), flush=True)
+
+    if args.reference_table:
+        for line in reference_table(torch):
+            print(json.dumps(line), flush=True)
 
     if args.sweep:
         for workload in sweep_workloads():
