@@ -40,6 +40,7 @@ from ._normalization_native import (
     NATIVE_HIDDEN_SIZES,
     NATIVE_HIDDEN_SIZES_TEXT,
     TARGET_ARCHITECTURE,
+    native_residual_layer_norm,
 )
 from ._ops import residual_layer_norm_op
 from ._status import BackendStatus
@@ -109,6 +110,10 @@ def _native_status(device_index):
 
 def residual_layer_norm_status(device=None):
     """Return the cached ``BackendStatus`` of the native backend on ``device``."""
+    if isinstance(device, torch.device) and device.type == "cuda" and device.index is not None:
+        # A HIP tensor's device (the per-call case): _native_status checks
+        # availability itself, once per device.
+        return _native_status(device.index)
     if not torch.cuda.is_available():
         return BackendStatus(False, None, None, "PyTorch CUDA/HIP is unavailable")
     if device is None:
@@ -177,8 +182,6 @@ def _strict_native(x, branch, weight, bias, dropout_p, eps, training, normalized
     status = residual_layer_norm_status(x.device)
     if not status.available:
         raise RuntimeError(f"{_UNAVAILABLE}: {status.reason}")
-    from ._normalization_native import native_residual_layer_norm
-
     return native_residual_layer_norm(
         x, branch, weight, bias, float(dropout_p), float(eps), bool(training),
         normalized_dtype=normalized_dtype,
@@ -272,8 +275,6 @@ def residual_layer_norm(
         if status.architecture == TARGET_ARCHITECTURE:
             raise RuntimeError(f"{_UNAVAILABLE}: {status.reason}")
         return _fall_back(status.reason, *args)
-    from ._normalization_native import native_residual_layer_norm
-
     with torch.cuda.device(x.device):
         return native_residual_layer_norm(
             x, branch, weight, bias, float(dropout_p), float(eps), bool(training),
