@@ -420,14 +420,12 @@ class ResidualLayerNormFunction : public torch::autograd::Function<ResidualLayer
         ctx->save_for_backward(
             {updated, weight, std::get<2>(result), std::get<3>(result), std::get<4>(result)});
         ctx->set_materialize_grads(false);
+        // The scalars the backward needs, in one entry (each saved_data entry
+        // costs a hash-map insertion on every forward call).
         ctx->saved_data["dropout_p"] = dropout_p;
-        ctx->saved_data["training"] = training;
-        ctx->saved_data["branch_is_half"] = branch.scalar_type() == at::kHalf;
-        ctx->saved_data["branch_dtype"] = static_cast<int64_t>(branch.scalar_type());
-        ctx->saved_data["threads"] = threads;
-        ctx->saved_data["block_rows"] = block_rows;
-        ctx->saved_data["parameter_threads"] = parameter_threads;
-        ctx->saved_data["parameter_groups"] = parameter_groups;
+        ctx->saved_data["state"] = std::vector<int64_t>{
+            training ? 1 : 0, static_cast<int64_t>(branch.scalar_type()), threads, block_rows,
+            parameter_threads, parameter_groups};
         return {updated, normalized};
     }
 
@@ -454,6 +452,8 @@ class ResidualLayerNormFunction : public torch::autograd::Function<ResidualLayer
         at::Tensor grad_bias_sum = ctx->saved_data["grad_bias_sum"].toTensor();
         ctx->saved_data["grad_weight_sum"] = at::Tensor();
         ctx->saved_data["grad_bias_sum"] = at::Tensor();
+        const std::vector<int64_t> state = ctx->saved_data["state"].toIntVector();
+        const auto branch_dtype = static_cast<at::ScalarType>(state[1]);
         auto gradients = backward_impl(
             grad_updated,
             grad_normalized,
@@ -463,14 +463,14 @@ class ResidualLayerNormFunction : public torch::autograd::Function<ResidualLayer
             saved[3],
             saved[4],
             ctx->saved_data["dropout_p"].toDouble(),
-            ctx->saved_data["training"].toBool(),
-            ctx->saved_data["branch_is_half"].toBool(),
-            ctx->saved_data["threads"].toInt(),
-            ctx->saved_data["block_rows"].toInt(),
-            ctx->saved_data["parameter_threads"].toInt(),
-            ctx->saved_data["parameter_groups"].toInt(),
+            state[0] != 0,
+            branch_dtype == at::kHalf,
+            state[2],
+            state[3],
+            state[4],
+            state[5],
             has_grad_normalized,
-            static_cast<at::ScalarType>(ctx->saved_data["branch_dtype"].toInt()),
+            branch_dtype,
             &grad_weight_sum,
             &grad_bias_sum);
         return {
