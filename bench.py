@@ -30,6 +30,10 @@ Prints one JSON line:
   public_api      whole autograd steps through the public Python API on this
                GPU: these kernels (implementation="gfx950") and the
                reference's decomposition run by PyTorch-ROCm ("torch")
+  reference_method  the reference's own published metric, speedup of the
+               public call over the PyTorch decomposition on the same GPU
+               (B = 1, H = 384), at T = 262144 where the GPU work dominates,
+               beside the best ratios the reference publishes for gfx1010
 
 ``--sweep`` adds one JSON line per other BASELINE.json configuration (C0, the
 C2 hidden-size sweep, C3 deterministic, the C4 cases), each with the same
@@ -210,13 +214,15 @@ REFERENCE_SPEEDUPS = {128: (1.273, 1.269), 256: (1.262, 1.265), 512: (1.303, 1.2
 EXTRA_SEQUENCES = (16384, 65536, 262144)
 
 
-def reference_table(torch, warmup: int = 100, reps: int = 1000) -> list[dict]:
+def reference_table(torch, warmup: int = 100, reps: int = 1000,
+                    sequences: tuple[int, ...] | None = None) -> list[dict]:
     """The reference's own headline measurement, on this GPU: the public
     forward and forward + backward (autograd.grad) call, fused native path
     against implementation="torch" (the decomposition), one CUDA-event pair
     around each call on the current stream, median / p20 / p80 of `reps`
     calls after `warmup` (as the reference's
-    benchmarks/benchmark_residual_layer_norm.py:30-44, :213-264 measures)."""
+    benchmarks/benchmark_residual_layer_norm.py:30-44, :213-264 measures).
+    `sequences` picks some of the sequence lengths (default: all)."""
     from gfx1010_kernels import residual_layer_norm
 
     def timed(call):
@@ -240,6 +246,8 @@ def reference_table(torch, warmup: int = 100, reps: int = 1000) -> list[dict]:
     hidden, dropout_p = 384, 0.15
     lines = []
     cases = [*REFERENCE_SPEEDUPS.items(), *((sequence, (None, None)) for sequence in EXTRA_SEQUENCES)]
+    if sequences is not None:
+        cases = [case for case in cases if case[0] in sequences]
     for sequence, published in cases:
         generator = torch.Generator(device="cuda").manual_seed(sequence)
         shape = (1, sequence, hidden)
@@ -757,6 +765,18 @@ def main() -> int:
     result = result_line(torch, C1, timing, args.steps, args.warmup, args.sets, traffic)
     result["copy_ceiling"] = copy_ceiling(torch, stream)
     result["public_api"] = public_api_steps(torch, C1, stream)
+    # The reference's own published metric (speedup over its PyTorch
+    # decomposition on the same GPU, H = 384) at a length where the GPU work
+    # dominates; the full table is --reference-table.
+    (line,) = reference_table(torch, warmup=20, reps=200, sequences=(262144,))
+    result["reference_method"] = {
+        "shape": "B=1, T=262144, H=384, fp16 branch, p=0.15",
+        "forward_speedup_vs_torch": line["forward"]["speedup"],
+        "train_speedup_vs_torch": line["train"]["speedup"],
+        "reference_best_published_gfx1010": {"forward": max(v[0] for v in REFERENCE_SPEEDUPS.values()),
+                                              "train": max(v[1] for v in REFERENCE_SPEEDUPS.values())},
+        "kind": "median of 200 event-timed public calls, implementation='gfx950' vs 'torch'",
+    }
     if not args.no_cpu_baseline:
         print(f"[bench] CPU baseline (~{args.cpu_seconds:.0f} s)", flush=True)
         result["cpu_baseline"] = cpu_baseline(torch, C1, args.cpu_seconds)
