@@ -51,9 +51,10 @@ HIP_FLAGS = [
 # One translation unit per row shape (every dtype and alignment variant of
 # its kernels), plus the C ABI; compiled in parallel, linked into one library.
 # Specialized hidden sizes, and the (slots per lane, waves per row) pairs of
-# the run-time-length kernels that serve every other multiple of 64 up to 8192.
+# the run-time-length kernels that serve every other multiple of 64 up to 8192
+# (the (2, 4) unit also holds the (4, 2) forward it runs).
 HIDDEN_SIZES = (128, 256, 384, 512, 768, 1024)
-WIDE_SHAPES = ((1, 1), (2, 1), (3, 1), (4, 1), (3, 2), (4, 2), (3, 4), (4, 4), (3, 8), (4, 8))
+WIDE_SHAPES = ((1, 1), (2, 1), (3, 1), (4, 1), (3, 2), (2, 4), (3, 4), (4, 4), (3, 8), (4, 8))
 BUILD_DIR = ROOT / "_build"
 
 

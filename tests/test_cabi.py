@@ -74,10 +74,11 @@ def test_size_queries():
     assert _cabi.backward_workspace_bytes(37, 128, True) == 3 * 2 * 128 * 4
     assert _cabi.backward_workspace_bytes(41, 768, True) == 6 * 2 * 768 * 4
     assert _cabi.backward_workspace_bytes(1 << 20, 1024, True) == 256 * 2 * 1024 * 4
-    # Run-time row lengths: one wave per row up to 1024, else 2, 4 or 8 waves
-    # per row (4, 2 or 1 rows per 8-wave block).
+    # Run-time row lengths: one wave per row up to 1024, else 2 (up to 1536),
+    # 4 (up to 4096) or 8 waves per row (4, 2 or 1 rows per 8-wave block).
     assert _cabi.backward_workspace_bytes(41, 640, True) == 6 * 2 * 640 * 4
-    assert _cabi.backward_workspace_bytes(41, 2048, True) == 11 * 2 * 2048 * 4
+    assert _cabi.backward_workspace_bytes(41, 1280, True) == 11 * 2 * 1280 * 4
+    assert _cabi.backward_workspace_bytes(41, 2048, True) == 21 * 2 * 2048 * 4
     assert _cabi.backward_workspace_bytes(41, 4096, True) == 21 * 2 * 4096 * 4
     assert _cabi.backward_workspace_bytes(41, 8192, True) == 41 * 2 * 8192 * 4
     assert _cabi.backward_workspace_bytes(8192, 8192, True) == 256 * 2 * 8192 * 4
