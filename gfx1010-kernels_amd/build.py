@@ -51,10 +51,15 @@ HIP_FLAGS = [
 # One translation unit per row shape (every dtype and alignment variant of
 # its kernels), plus the C ABI; compiled in parallel, linked into one library.
 # Specialized hidden sizes, and the (slots per lane, waves per row) pairs of
-# the run-time-length kernels that serve every other multiple of 64 up to 8192
-# (the (2, 4) unit also holds the (4, 2) forward it runs).
+# the run-time-length kernels that serve every other multiple of 64 up to
+# 8192, per pass (the lists RLN_FOR_EACH_WIDE_FORWARD / _BACKWARD in
+# rln_device.h; the link fails on a pair missing here). The backward of 1024
+# columns runs the (1, 4) run-time-length kernel (backward_runs_wide).
 HIDDEN_SIZES = (128, 256, 384, 512, 768, 1024)
-WIDE_SHAPES = ((1, 1), (2, 1), (3, 1), (4, 1), (3, 2), (2, 4), (3, 4), (4, 4), (3, 8), (4, 8))
+FIXED_BACKWARD = (128, 256, 384, 512, 768)
+WIDE_FORWARD = ((1, 1), (2, 1), (3, 1), (4, 1), (3, 2), (4, 2), (3, 4), (4, 4), (3, 8), (4, 8))
+WIDE_BACKWARD = ((1, 1), (2, 1), (3, 1), (4, 1), (1, 4), (3, 2), (2, 4), (3, 4), (2, 8), (3, 8),
+                 (4, 8))
 BUILD_DIR = ROOT / "_build"
 
 
@@ -80,13 +85,15 @@ def build_library(jobs: int | None = None) -> Path:
     BUILD_DIR.mkdir(parents=True, exist_ok=True)
     units = [(CSRC / "rln_api.hip", BUILD_DIR / "rln_api.o", [])]
     units += [
-        (CSRC / "rln_hidden.hip", BUILD_DIR / f"rln_hidden_{hidden}.o", [f"-DRLN_HIDDEN={hidden}"])
+        (CSRC / "rln_hidden.hip", BUILD_DIR / f"rln_hidden_{hidden}.o",
+         [f"-DRLN_HIDDEN={hidden}", f"-DRLN_PASSES={1 | (hidden in FIXED_BACKWARD) << 1}"])
         for hidden in HIDDEN_SIZES
     ]
     units += [
         (CSRC / "rln_hidden.hip", BUILD_DIR / f"rln_wide_{v}x{p}.o",
-         [f"-DRLN_WIDE_V={v}", f"-DRLN_WIDE_P={p}"])
-        for v, p in WIDE_SHAPES
+         [f"-DRLN_WIDE_V={v}", f"-DRLN_WIDE_P={p}",
+          f"-DRLN_PASSES={((v, p) in WIDE_FORWARD) | ((v, p) in WIDE_BACKWARD) << 1}"])
+        for v, p in sorted(set(WIDE_FORWARD) | set(WIDE_BACKWARD))
     ]
     workers = jobs or min(len(units), max(1, (os.cpu_count() or 1)))
     with ThreadPoolExecutor(max_workers=workers) as pool:
@@ -94,7 +101,7 @@ def build_library(jobs: int | None = None) -> Path:
     hipcc = str(ROCM / "bin" / "hipcc")
     temporary = LIBRARY.with_name(LIBRARY.name + ".tmp")
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects),
-          f"-Wl,-soname,{LIBRARY.name}", "-o", str(temporary)])
+          f"-Wl,-soname,{LIBRARY.name}", "-Wl,-z,defs", "-o", str(temporary)])
     os.replace(temporary, LIBRARY)
     return LIBRARY
 

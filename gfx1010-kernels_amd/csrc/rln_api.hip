@@ -12,7 +12,8 @@
 namespace rln {
 
 RLN_FOR_EACH_FIXED(RLN_DECLARE_FIXED)
-RLN_FOR_EACH_WIDE(RLN_DECLARE_WIDE)
+RLN_FOR_EACH_WIDE_FORWARD(RLN_DECLARE_WIDE_FORWARD)
+RLN_FOR_EACH_WIDE_BACKWARD(RLN_DECLARE_WIDE_BACKWARD)
 
 namespace {
 
@@ -280,7 +281,7 @@ int rln_forward(
         && aligned_to(updated, 16)
         && aligned_to(normalized, vector_alignment(normalized_dtype))
         && aligned_to(branch, vector_alignment(branch_dtype));
-    return with_shape(hidden, [&](auto shape) {
+    return with_shape<Pass::kForward>(hidden, [&](auto shape) {
         return launch_forward_shape(a, shape, branch_dtype, normalized_dtype, aligned);
     });
 }
@@ -389,7 +390,7 @@ int rln_backward(
         && aligned_to(grad_normalized, vector_alignment(grad_normalized_dtype))
         && aligned_to(updated, 16) && aligned_to(weight, 16) && aligned_to(grad_x, 16)
         && aligned_to(grad_branch, vector_alignment(branch_dtype));
-    status = with_shape(hidden, [&](auto shape) {
+    status = with_shape<Pass::kBackward>(hidden, [&](auto shape) {
         return launch_backward_shape(a, shape, branch_dtype, grad_normalized_dtype, aligned);
     });
     if (status != RLN_OK) {

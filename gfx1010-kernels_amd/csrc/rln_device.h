@@ -128,9 +128,8 @@ int check_launch(const char* what);
 //  * WideShape<V, P>: every other multiple of 64 from kMinHidden to
 //    kMaxHidden, passed at run time. P waves own a row (P > 1 add their row
 //    sums through LDS), V slots per lane; slots past the end of the row
-//    stay idle. P = 1 up to 1024 columns, 2 up to 1536, 4 up to 4096, 8
-//    beyond; the forward of 1537 to 2048 columns runs on 2 waves instead
-//    (ForwardShape).
+//    stay idle. The forward and the backward choose P separately
+//    (wide_parts), and V is then the fewest slots that hold the row.
 
 constexpr int64_t kSpecializedHidden[] = {128, 256, 384, 512, 768, 1024};
 constexpr int64_t kMinHidden = 128;
@@ -218,7 +217,8 @@ struct ShapeInfo {
     int forward_threads;
 };
 
-// The forward's shape for dispatch shape S and normalized type N.
+// The forward's shape for dispatch shape S and normalized type N (the
+// specialized sizes' forward may use fewer lanes per row, forward_lanes).
 template <typename S, typename N>
 struct ForwardShape {
     using type = S;
@@ -227,27 +227,50 @@ template <int H, int Lanes, typename N>
 struct ForwardShape<FixedShape<H, Lanes>, N> {
     using type = FixedShape<H, forward_lanes<N>(H)>;
 };
-// Rows of 1537 to 2048 columns: the backward (the dispatch shape) runs four
-// waves of two slots per row, the forward two waves of four. Measured on
-// MI355X at H = 1600, 1792 and 2048: four waves make the backward 3-7 %
-// faster and the forward 3-8 % slower than two.
-template <typename N>
-struct ForwardShape<WideShape<2, 4>, N> {
-    using type = WideShape<4, 2>;
-};
 
 template <typename S>
 constexpr ShapeInfo info_of() {
     return {S::kRowsPerWave, S::kParts, S::kV, S::kForwardThreads};
 }
 
-// The dispatch (and backward) shape of a supported hidden size.
-inline ShapeInfo shape_info(int64_t hidden) {
-    if (specialized_hidden(hidden)) {
+enum class Pass { kForward, kBackward };
+
+// The specialized size whose backward runs the run-time-length kernel: 1024
+// columns on 4 waves of one slot per lane, all slots full, measured 3-4 %
+// faster than one wave of four slots from 64 M elements and 2 % at 8 M
+// (at 768 columns the same split, a quarter of its slots idle, is 2-13 %
+// slower than one wave of three).
+inline bool backward_runs_wide(int64_t hidden) {
+    return hidden == 1024;
+}
+
+// Waves per row of a run-time row length. Measured on MI355X, the backward
+// is faster on more waves with fewer slots as long as about 60 % of the
+// slots hold columns (4 waves x 2 slots against 2 x 3-4: 1.5 % at 1280
+// columns, 4 % at 1536, 5-7 % at 1600 and 2048; 8 x 2 against 4 x 3-4: 2 %
+// at 2560, 6-8 % from 3072 to 4096; at 1088 and 2112, where half the slots
+// would idle, it is 3-5 % slower), while the forward is faster on fewer
+// waves with more slots (2 x 4 against 4 x 2: 3-8 % at 1600 to 2048).
+inline int wide_parts(int64_t hidden, Pass pass) {
+    if (pass == Pass::kBackward && backward_runs_wide(hidden)) {
+        return 4;
+    }
+    if (hidden <= 1024) {
+        return 1;
+    }
+    if (pass == Pass::kForward) {
+        return hidden <= 2048 ? 2 : hidden <= 4096 ? 4 : 8;
+    }
+    return hidden <= 1216 ? 2 : hidden <= 2432 ? 4 : 8;
+}
+
+// The shape of a supported hidden size in one pass.
+inline ShapeInfo shape_info(int64_t hidden, Pass pass) {
+    if (specialized_hidden(hidden) && !(pass == Pass::kBackward && backward_runs_wide(hidden))) {
         const int lanes = fixed_lanes(hidden);
         return {kWaveSize / lanes, 1, static_cast<int>(hidden / 4 / lanes), 256};
     }
-    const int parts = hidden <= 1024 ? 1 : hidden <= 1536 ? 2 : hidden <= 4096 ? 4 : 8;
+    const int parts = wide_parts(hidden, pass);
     const int64_t per_slot = 4 * kWaveSize * parts;
     const int vectors = static_cast<int>((hidden + per_slot - 1) / per_slot);
     return {1, parts, vectors, parts > 4 ? parts * kWaveSize : 256};
@@ -276,7 +299,8 @@ int64_t forward_blocks(int64_t rows) {
 // The backward's grid is also the number of weight/bias partials: at most
 // 256 blocks of 8 waves, one block per CU.
 inline int64_t backward_blocks(int64_t rows, int64_t hidden) {
-    return launch_blocks(rows, shape_info(hidden), kBackwardThreads, kBackwardMaxBlocks, 1);
+    return launch_blocks(rows, shape_info(hidden, Pass::kBackward), kBackwardThreads,
+                         kBackwardMaxBlocks, 1);
 }
 
 // 1 if a launch over rows x hidden walks its rows paced, 0 for look-ahead.
@@ -287,7 +311,7 @@ inline int64_t backward_blocks(int64_t rows, int64_t hidden) {
 // block per CU, where look-ahead is up to 19 % faster); their backward is
 // faster with look-ahead at every size measured (up to 24 %).
 inline int forward_paced(int64_t rows, int64_t hidden) {
-    const ShapeInfo info = shape_info(hidden);
+    const ShapeInfo info = shape_info(hidden, Pass::kForward);
     const int64_t elements = rows * hidden;
     if (hidden < kPacedMinHidden || elements < kPacedElements) {
         return 0;
@@ -300,7 +324,7 @@ inline int forward_paced(int64_t rows, int64_t hidden) {
 
 inline int backward_paced(int64_t rows, int64_t hidden) {
     return hidden >= kPacedMinHidden && rows * hidden >= kPacedElements
-        && shape_info(hidden).parts == 1 ? 1 : 0;
+        && shape_info(hidden, Pass::kBackward).parts == 1 ? 1 : 0;
 }
 
 // ----------------------------------------------------------------------------
@@ -1236,11 +1260,11 @@ struct BackwardArgs {
 };
 
 // The dispatch shape must be the one shape_info() describes for the hidden
-// size, since the backward's grid (and so the deterministic order and the
-// workspace size) is computed from the latter.
+// size and pass, since the backward's grid (and so the deterministic order
+// and the workspace size) is computed from the latter.
 template <typename S>
-int check_shape(const S& shape) {
-    const ShapeInfo info = shape_info(shape.hidden());
+int check_shape(const S& shape, Pass pass) {
+    const ShapeInfo info = shape_info(shape.hidden(), pass);
     if (info.parts != S::kParts || info.rows_per_wave != S::kRowsPerWave
         || info.vectors != S::kV || info.forward_threads != S::kForwardThreads) {
         return fail(RLN_ERR_UNSUPPORTED, "shape mismatch for hidden size %lld",
@@ -1316,7 +1340,7 @@ int with_dtype(int dtype, Launch&& launch) {
 template <typename S>
 int launch_forward_shape(const ForwardArgs& a, S shape, int branch_dtype, int normalized_dtype,
                          bool aligned) {
-    const int status = check_shape(shape);
+    const int status = check_shape(shape, Pass::kForward);
     if (status != RLN_OK) {
         return status;
     }
@@ -1326,9 +1350,6 @@ int launch_forward_shape(const ForwardArgs& a, S shape, int branch_dtype, int no
             F forward_shape{};
             if constexpr (std::is_same_v<F, S>) {
                 forward_shape = shape;
-            } else if constexpr (F::kHidden == 0) {
-                forward_shape.hidden_ = shape.hidden();
-                forward_shape.inv_hidden_ = shape.inv_hidden();
             }
             return aligned ? launch_forward<F, B, N, true>(a, forward_shape)
                            : launch_forward<F, B, N, false>(a, forward_shape);
@@ -1339,7 +1360,7 @@ int launch_forward_shape(const ForwardArgs& a, S shape, int branch_dtype, int no
 template <typename S>
 int launch_backward_shape(const BackwardArgs& a, S shape, int branch_dtype,
                           int grad_normalized_dtype, bool aligned) {
-    const int status = check_shape(shape);
+    const int status = check_shape(shape, Pass::kBackward);
     if (status != RLN_OK) {
         return status;
     }
@@ -1351,8 +1372,21 @@ int launch_backward_shape(const BackwardArgs& a, S shape, int branch_dtype,
     });
 }
 
-// Calls `launch(shape)` with the dispatch shape of a supported hidden size.
-template <typename Launch>
+// The row shapes, one translation unit each (rln_hidden.hip): the
+// specialized sizes (the backward of those backward_runs_wide names excepted),
+// and the (slots per lane, waves per row) pairs of the run-time lengths each
+// pass runs (wide_parts).
+#define RLN_FOR_EACH_FIXED(X) X(128) X(256) X(384) X(512) X(768) X(1024)
+#define RLN_FOR_EACH_WIDE_FORWARD(X) \
+    X(1, 1) X(2, 1) X(3, 1) X(4, 1) X(3, 2) X(4, 2) X(3, 4) X(4, 4) X(3, 8) X(4, 8)
+#define RLN_FOR_EACH_WIDE_BACKWARD(X) \
+    X(1, 1) X(2, 1) X(3, 1) X(4, 1) X(1, 4) X(3, 2) X(2, 4) X(3, 4) X(2, 8) X(3, 8) X(4, 8)
+
+#define RLN_WIDE_CASE(V, P) \
+    case P * 16 + V: return launch(WideShape<V, P>{hidden, inv_hidden});
+
+// Calls `launch(shape)` with the shape a supported hidden size runs in `kPass`.
+template <Pass kPass, typename Launch>
 int with_shape(int64_t hidden, Launch&& launch) {
     switch (hidden) {
         case 128: return launch(FixedShape<128>{});
@@ -1360,45 +1394,43 @@ int with_shape(int64_t hidden, Launch&& launch) {
         case 384: return launch(FixedShape<384>{});
         case 512: return launch(FixedShape<512>{});
         case 768: return launch(FixedShape<768>{});
-        case 1024: return launch(FixedShape<1024>{});
+        case 1024:
+            if constexpr (kPass == Pass::kForward) {
+                return launch(FixedShape<1024>{});
+            }
+            break;
         default: break;
     }
     if (!hidden_supported(hidden)) {
         return fail(RLN_ERR_UNSUPPORTED, "unsupported native hidden size: %lld",
                     static_cast<long long>(hidden));
     }
-    const ShapeInfo info = shape_info(hidden);
+    const ShapeInfo info = shape_info(hidden, kPass);
     const float inv_hidden = 1.0f / static_cast<float>(hidden);
-    switch (info.parts * 16 + info.vectors) {
-        case 1 * 16 + 1: return launch(WideShape<1, 1>{hidden, inv_hidden});
-        case 1 * 16 + 2: return launch(WideShape<2, 1>{hidden, inv_hidden});
-        case 1 * 16 + 3: return launch(WideShape<3, 1>{hidden, inv_hidden});
-        case 1 * 16 + 4: return launch(WideShape<4, 1>{hidden, inv_hidden});
-        case 2 * 16 + 3: return launch(WideShape<3, 2>{hidden, inv_hidden});
-        case 4 * 16 + 2: return launch(WideShape<2, 4>{hidden, inv_hidden});
-        case 4 * 16 + 3: return launch(WideShape<3, 4>{hidden, inv_hidden});
-        case 4 * 16 + 4: return launch(WideShape<4, 4>{hidden, inv_hidden});
-        case 8 * 16 + 3: return launch(WideShape<3, 8>{hidden, inv_hidden});
-        case 8 * 16 + 4: return launch(WideShape<4, 8>{hidden, inv_hidden});
-        default: break;
+    if constexpr (kPass == Pass::kForward) {
+        switch (info.parts * 16 + info.vectors) {
+            RLN_FOR_EACH_WIDE_FORWARD(RLN_WIDE_CASE)
+            default: break;
+        }
+    } else {
+        switch (info.parts * 16 + info.vectors) {
+            RLN_FOR_EACH_WIDE_BACKWARD(RLN_WIDE_CASE)
+            default: break;
+        }
     }
     return fail(RLN_ERR_UNSUPPORTED, "no row shape for hidden size %lld",
                 static_cast<long long>(hidden));
 }
-
-// The row shapes, one translation unit each (rln_hidden.hip).
-#define RLN_FOR_EACH_FIXED(X) X(128) X(256) X(384) X(512) X(768) X(1024)
-#define RLN_FOR_EACH_WIDE(X) \
-    X(1, 1) X(2, 1) X(3, 1) X(4, 1) X(3, 2) X(2, 4) X(3, 4) X(4, 4) X(3, 8) X(4, 8)
 
 #define RLN_DECLARE_FIXED(H)                                                              \
     extern template int launch_forward_shape<FixedShape<H>>(                             \
         const ForwardArgs&, FixedShape<H>, int, int, bool);                               \
     extern template int launch_backward_shape<FixedShape<H>>(                            \
         const BackwardArgs&, FixedShape<H>, int, int, bool);
-#define RLN_DECLARE_WIDE(V, P)                                                            \
+#define RLN_DECLARE_WIDE_FORWARD(V, P)                                                    \
     extern template int launch_forward_shape<WideShape<V, P>>(                           \
-        const ForwardArgs&, WideShape<V, P>, int, int, bool);                             \
+        const ForwardArgs&, WideShape<V, P>, int, int, bool);
+#define RLN_DECLARE_WIDE_BACKWARD(V, P)                                                   \
     extern template int launch_backward_shape<WideShape<V, P>>(                          \
         const BackwardArgs&, WideShape<V, P>, int, int, bool);
 

@@ -20,13 +20,16 @@ import torch
 
 from oracle import rln_oracle as oracle
 
-# The reference's hidden sizes (specialized kernels), and one size for every
-# run-time-length kernel shape (slots per lane x waves per row): 1x1, 2x1,
-# 3x1, 4x1, 3x2 (1280, and 1536 at its upper end), the 1537-2048 rows whose
-# backward runs 2x4 and forward 4x2 (1600 and 1984 leave a slot partly idle),
-# 3x4, 4x4, 3x8, 4x8.
+# The reference's hidden sizes (specialized kernels), and sizes that cover
+# every run-time-length kernel shape (slots per lane x waves per row) of each
+# pass and both sides of each boundary where a pass changes its waves per row:
+# forward 1x1, 2x1, 3x1, 4x1, 3x2 (up to 1536), 4x2 (to 2048), 3x4, 4x4 (to
+# 4096), 3x8, 4x8; backward the same up to 1216 columns, then 2x4 (to 2432,
+# with 3x4 from 2049), 2x8 (to 4096), 3x8, 4x8. Several leave slots partly
+# idle (1600, 1984, 2496).
 SPECIALIZED_HIDDEN_SIZES = (128, 256, 384, 512, 768, 1024)
-WIDE_HIDDEN_SIZES = (192, 320, 640, 896, 1280, 1536, 1600, 1984, 2048, 2560, 4096, 5120, 8192)
+WIDE_HIDDEN_SIZES = (192, 320, 640, 896, 1216, 1280, 1536, 1600, 1984, 2048, 2432, 2496, 3072,
+                     4096, 5120, 8192)
 TOL_FORWARD = 1e-5
 TOL_INPUT_GRAD = 1e-5
 TOL_PARAMETER_GRAD = 1e-4
