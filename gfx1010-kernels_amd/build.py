@@ -58,8 +58,7 @@ HIP_FLAGS = [
 HIDDEN_SIZES = (128, 256, 384, 512, 768, 1024)
 FIXED_BACKWARD = (128, 256, 384, 512, 768)
 WIDE_FORWARD = ((1, 1), (2, 1), (3, 1), (4, 1), (3, 2), (4, 2), (3, 4), (4, 4), (3, 8), (4, 8))
-WIDE_BACKWARD = ((1, 1), (2, 1), (3, 1), (4, 1), (1, 4), (3, 2), (2, 4), (3, 4), (2, 8), (3, 8),
-                 (4, 8))
+WIDE_BACKWARD = ((1, 1), (2, 1), (3, 1), (1, 4), (3, 2), (2, 4), (3, 4), (2, 8), (3, 8), (4, 8))
 BUILD_DIR = ROOT / "_build"
 
 

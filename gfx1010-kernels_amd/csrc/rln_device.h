@@ -235,33 +235,28 @@ constexpr ShapeInfo info_of() {
 
 enum class Pass { kForward, kBackward };
 
-// The specialized size whose backward runs the run-time-length kernel: 1024
-// columns on 4 waves of one slot per lane, all slots full, measured 3-4 %
-// faster than one wave of four slots from 64 M elements and 2 % at 8 M
-// (at 768 columns the same split, a quarter of its slots idle, is 2-13 %
-// slower than one wave of three).
-inline bool backward_runs_wide(int64_t hidden) {
-    return hidden == 1024;
+// Waves per row of a run-time row length. Measured on MI355X, the backward
+// is faster on more waves with fewer slots as long as about as many slots
+// hold columns, or at least ~60 % of them: 4 waves x 1 slot against 1 x 4
+// for 769-1024 columns (6-7 % at 832 and 896, 2.5 % at 960, 3-4 % at 1024;
+// no gain at 8 M elements; at 768 the split, a quarter of its slots idle
+// against none for one wave of three, is 2-13 % slower); 4 x 2 against
+// 2 x 3-4 (1.5 % at 1280 columns, 4 % at 1536, 5-7 % at 1600 and 2048);
+// 8 x 2 against 4 x 3-4 (2 % at 2560, 6-8 % from 3072 to 4096); at 1088 and
+// 2112, where half the slots would idle, 4 x 2 is 3-5 % slower. The forward
+// is faster on fewer waves with more slots (2 x 4 against 4 x 2: 3-8 % at
+// 1600 to 2048).
+inline int wide_parts(int64_t hidden, Pass pass) {
+    if (pass == Pass::kForward) {
+        return hidden <= 1024 ? 1 : hidden <= 2048 ? 2 : hidden <= 4096 ? 4 : 8;
+    }
+    return hidden <= 768 ? 1 : hidden <= 1024 ? 4 : hidden <= 1216 ? 2 : hidden <= 2432 ? 4 : 8;
 }
 
-// Waves per row of a run-time row length. Measured on MI355X, the backward
-// is faster on more waves with fewer slots as long as about 60 % of the
-// slots hold columns (4 waves x 2 slots against 2 x 3-4: 1.5 % at 1280
-// columns, 4 % at 1536, 5-7 % at 1600 and 2048; 8 x 2 against 4 x 3-4: 2 %
-// at 2560, 6-8 % from 3072 to 4096; at 1088 and 2112, where half the slots
-// would idle, it is 3-5 % slower), while the forward is faster on fewer
-// waves with more slots (2 x 4 against 4 x 2: 3-8 % at 1600 to 2048).
-inline int wide_parts(int64_t hidden, Pass pass) {
-    if (pass == Pass::kBackward && backward_runs_wide(hidden)) {
-        return 4;
-    }
-    if (hidden <= 1024) {
-        return 1;
-    }
-    if (pass == Pass::kForward) {
-        return hidden <= 2048 ? 2 : hidden <= 4096 ? 4 : 8;
-    }
-    return hidden <= 1216 ? 2 : hidden <= 2432 ? 4 : 8;
+// The specialized size whose backward runs the run-time-length kernel (its
+// 4-wave split of 769-1024 columns).
+inline bool backward_runs_wide(int64_t hidden) {
+    return hidden == 1024;
 }
 
 // The shape of a supported hidden size in one pass.
@@ -1380,7 +1375,7 @@ int launch_backward_shape(const BackwardArgs& a, S shape, int branch_dtype,
 #define RLN_FOR_EACH_WIDE_FORWARD(X) \
     X(1, 1) X(2, 1) X(3, 1) X(4, 1) X(3, 2) X(4, 2) X(3, 4) X(4, 4) X(3, 8) X(4, 8)
 #define RLN_FOR_EACH_WIDE_BACKWARD(X) \
-    X(1, 1) X(2, 1) X(3, 1) X(4, 1) X(1, 4) X(3, 2) X(2, 4) X(3, 4) X(2, 8) X(3, 8) X(4, 8)
+    X(1, 1) X(2, 1) X(3, 1) X(1, 4) X(3, 2) X(2, 4) X(3, 4) X(2, 8) X(3, 8) X(4, 8)
 
 #define RLN_WIDE_CASE(V, P) \
     case P * 16 + V: return launch(WideShape<V, P>{hidden, inv_hidden});

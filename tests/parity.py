@@ -24,12 +24,12 @@ from oracle import rln_oracle as oracle
 # every run-time-length kernel shape (slots per lane x waves per row) of each
 # pass and both sides of each boundary where a pass changes its waves per row:
 # forward 1x1, 2x1, 3x1, 4x1, 3x2 (up to 1536), 4x2 (to 2048), 3x4, 4x4 (to
-# 4096), 3x8, 4x8; backward the same up to 1216 columns, then 2x4 (to 2432,
-# with 3x4 from 2049), 2x8 (to 4096), 3x8, 4x8. Several leave slots partly
-# idle (1600, 1984, 2496).
+# 4096), 3x8, 4x8; backward 1x1, 2x1, 3x1 (to 768), 1x4 (to 1024), 3x2 (to
+# 1216), 2x4 (to 2048), 3x4 (to 2432), 2x8 (to 4096), 3x8, 4x8. Several
+# leave slots partly idle (832, 1600, 1984, 2496).
 SPECIALIZED_HIDDEN_SIZES = (128, 256, 384, 512, 768, 1024)
-WIDE_HIDDEN_SIZES = (192, 320, 640, 896, 1216, 1280, 1536, 1600, 1984, 2048, 2432, 2496, 3072,
-                     4096, 5120, 8192)
+WIDE_HIDDEN_SIZES = (192, 320, 640, 832, 896, 1216, 1280, 1536, 1600, 1984, 2048, 2432, 2496,
+                     3072, 4096, 5120, 8192)
 TOL_FORWARD = 1e-5
 TOL_INPUT_GRAD = 1e-5
 TOL_PARAMETER_GRAD = 1e-4
