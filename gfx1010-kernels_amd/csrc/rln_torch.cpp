@@ -33,6 +33,7 @@
 #include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 
+#include <cstring>
 #include <mutex>
 #include <optional>
 #include <tuple>
@@ -212,6 +213,43 @@ int dtype_of(at::ScalarType type) {
     return RLN_DTYPE_F32;
 }
 
+// Row statistics and dropout mask of one forward call kept in a single
+// allocation (the autograd path, which never returns them): mean at element 0,
+// rstd at `rstd_offset`, the mask words at `mask_offset`, each 256-byte
+// aligned. Saves two caching-allocator calls per forward.
+struct RowStatsLayout {
+    int64_t rows;
+    int64_t mask_words;
+    int64_t rstd_offset;
+    int64_t mask_offset;
+    int64_t elements;
+};
+
+RowStatsLayout row_stats_layout(int64_t rows, int64_t hidden, bool dropout) {
+    const auto aligned = [](int64_t count) { return (count + 63) / 64 * 64; };
+    RowStatsLayout layout{};
+    layout.rows = rows;
+    layout.mask_words = dropout ? rln_mask_words(rows, hidden) : 0;
+    layout.rstd_offset = aligned(rows);
+    layout.mask_offset = layout.rstd_offset + aligned(rows);
+    layout.elements = layout.mask_offset + layout.mask_words;
+    return layout;
+}
+
+// A contiguous 1-D tensor of `count` elements of `type` at element `offset`
+// of `base`'s storage, built without a dispatcher call.
+at::Tensor storage_slice(const at::Tensor& base, int64_t offset, int64_t count,
+                         caffe2::TypeMeta type) {
+    auto slice = at::detail::make_tensor<c10::TensorImpl>(
+        c10::Storage(base.storage()), base.key_set(), type);
+    slice.unsafeGetTensorImpl()->set_sizes_contiguous({count});
+    slice.unsafeGetTensorImpl()->set_storage_offset(offset);
+    return slice;
+}
+
+// `row_stats`: when given, mean, rstd and mask live in one float32 tensor
+// stored there (row_stats_layout) and the returned mean/rstd/mask are
+// undefined; otherwise they are three separate tensors.
 std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> forward_impl(
     const at::Tensor& x,
     const at::Tensor& branch,
@@ -223,7 +261,8 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> forward_i
     int64_t threads,
     std::optional<at::ScalarType> normalized_dtype,
     at::Tensor* zeroed_grad_weight = nullptr,
-    at::Tensor* zeroed_grad_bias = nullptr) {
+    at::Tensor* zeroed_grad_bias = nullptr,
+    at::Tensor* row_stats = nullptr) {
     check_forward_inputs(x, branch, weight, bias, dropout_p, eps, threads);
     const at::ScalarType output_type = normalized_dtype.value_or(at::kFloat);
     TORCH_CHECK(supported_dtype(output_type),
@@ -234,9 +273,28 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> forward_i
     const bool dropout = training && dropout_p > 0.0;
     auto updated = at::empty_like(x);
     auto normalized = at::empty_like(x, x.options().dtype(output_type));
-    auto mean = at::empty({rows}, x.options());
-    auto rstd = at::empty({rows}, x.options());
-    auto mask = at::empty({dropout ? rln_mask_words(rows, hidden) : 0}, x.options().dtype(at::kInt));
+    at::Tensor mean;
+    at::Tensor rstd;
+    at::Tensor mask;
+    float* mean_ptr = nullptr;
+    float* rstd_ptr = nullptr;
+    uint32_t* mask_ptr = nullptr;
+    if (row_stats != nullptr) {
+        const RowStatsLayout layout = row_stats_layout(rows, hidden, dropout);
+        *row_stats = at::empty({layout.elements}, x.options());
+        float* base = row_stats->data_ptr<float>();
+        mean_ptr = base;
+        rstd_ptr = base + layout.rstd_offset;
+        mask_ptr = dropout ? reinterpret_cast<uint32_t*>(base + layout.mask_offset) : nullptr;
+    } else {
+        mean = at::empty({rows}, x.options());
+        rstd = at::empty({rows}, x.options());
+        mask = at::empty({dropout ? rln_mask_words(rows, hidden) : 0},
+                         x.options().dtype(at::kInt));
+        mean_ptr = mean.data_ptr<float>();
+        rstd_ptr = rstd.data_ptr<float>();
+        mask_ptr = dropout ? reinterpret_cast<uint32_t*>(mask.data_ptr<int32_t>()) : nullptr;
+    }
     rln_philox_t philox{};
     if (dropout) {
         philox = reserve_philox(x, hidden, layout_threads(hidden, threads));
@@ -258,9 +316,9 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor, at::Tensor> forward_i
         updated.data_ptr<float>(),
         normalized.data_ptr(),
         dtype_of(output_type),
-        mean.data_ptr<float>(),
-        rstd.data_ptr<float>(),
-        dropout ? reinterpret_cast<uint32_t*>(mask.data_ptr<int32_t>()) : nullptr,
+        mean_ptr,
+        rstd_ptr,
+        mask_ptr,
         zero_sums ? zeroed_grad_weight->data_ptr<float>() : nullptr,
         zero_sums ? zeroed_grad_bias->data_ptr<float>() : nullptr,
         rows,
@@ -384,10 +442,13 @@ std::vector<at::Tensor> backward_impl(
 }
 
 // Autograd contract of csrc/residual_layer_norm_bindings.cpp:10-98: saves
-// (updated, weight, mean, rstd, mask), does not materialize missing output
-// gradients, and returns weight/bias gradients only when `normalized` received
-// a gradient. Missing gradients are passed to the kernel as null pointers
-// instead of materialized zeros.
+// updated, weight, mean, rstd and mask (the last three in one row-statistics
+// tensor), does not materialize missing output gradients, and returns
+// weight/bias gradients only when `normalized` received a gradient. Missing
+// gradients are passed to the kernel as null pointers instead of materialized
+// zeros. The forward's host cost is kept low on purpose (three allocations
+// and two more for the gradient sums, one saved_data entry): small calls are
+// bound by it.
 class ResidualLayerNormFunction : public torch::autograd::Function<ResidualLayerNormFunction> {
  public:
     static torch::autograd::variable_list forward(
@@ -409,23 +470,23 @@ class ResidualLayerNormFunction : public torch::autograd::Function<ResidualLayer
         // training step); a repeated backward (retain_graph) allocates anew.
         at::Tensor grad_weight_sum;
         at::Tensor grad_bias_sum;
+        at::Tensor row_stats;
         const bool parameters = weight.requires_grad() || bias.requires_grad();
         auto result = forward_impl(
             x, branch, weight, bias, dropout_p, eps, training, threads, normalized_dtype,
-            parameters ? &grad_weight_sum : nullptr, parameters ? &grad_bias_sum : nullptr);
-        ctx->saved_data["grad_weight_sum"] = grad_weight_sum;
-        ctx->saved_data["grad_bias_sum"] = grad_bias_sum;
+            parameters ? &grad_weight_sum : nullptr, parameters ? &grad_bias_sum : nullptr,
+            &row_stats);
         auto updated = std::get<0>(result);
         auto normalized = std::get<1>(result);
-        ctx->save_for_backward(
-            {updated, weight, std::get<2>(result), std::get<3>(result), std::get<4>(result)});
+        ctx->save_for_backward({updated, weight, row_stats, grad_weight_sum, grad_bias_sum});
         ctx->set_materialize_grads(false);
-        // The scalars the backward needs, in one entry (each saved_data entry
-        // costs a hash-map insertion on every forward call).
-        ctx->saved_data["dropout_p"] = dropout_p;
+        // The scalars the backward needs, dropout_p as its bit pattern, in one
+        // entry (each saved_data entry costs a hash-map insertion per call).
+        int64_t dropout_bits = 0;
+        std::memcpy(&dropout_bits, &dropout_p, sizeof(dropout_bits));
         ctx->saved_data["state"] = std::vector<int64_t>{
             training ? 1 : 0, static_cast<int64_t>(branch.scalar_type()), threads, block_rows,
-            parameter_threads, parameter_groups};
+            parameter_threads, parameter_groups, dropout_bits};
         return {updated, normalized};
     }
 
@@ -448,22 +509,34 @@ class ResidualLayerNormFunction : public torch::autograd::Function<ResidualLayer
                 at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor()};
         }
         // Sums zeroed by the forward serve the first backward only.
-        at::Tensor grad_weight_sum = ctx->saved_data["grad_weight_sum"].toTensor();
-        at::Tensor grad_bias_sum = ctx->saved_data["grad_bias_sum"].toTensor();
-        ctx->saved_data["grad_weight_sum"] = at::Tensor();
-        ctx->saved_data["grad_bias_sum"] = at::Tensor();
+        at::Tensor grad_weight_sum;
+        at::Tensor grad_bias_sum;
+        if (ctx->saved_data.find("sums_used") == ctx->saved_data.end()) {
+            grad_weight_sum = saved[3];
+            grad_bias_sum = saved[4];
+            ctx->saved_data["sums_used"] = true;
+        }
         const std::vector<int64_t> state = ctx->saved_data["state"].toIntVector();
         const auto branch_dtype = static_cast<at::ScalarType>(state[1]);
+        const bool training = state[0] != 0;
+        double dropout_p = 0.0;
+        std::memcpy(&dropout_p, &state[6], sizeof(dropout_p));
+        const at::Tensor& updated = saved[0];
+        const int64_t hidden = updated.size(-1);
+        const RowStatsLayout layout =
+            row_stats_layout(updated.numel() / hidden, hidden, training && dropout_p > 0.0);
+        const auto f32 = caffe2::TypeMeta::Make<float>();
         auto gradients = backward_impl(
             grad_updated,
             grad_normalized,
-            saved[0],
+            updated,
             saved[1],
-            saved[2],
-            saved[3],
-            saved[4],
-            ctx->saved_data["dropout_p"].toDouble(),
-            state[0] != 0,
+            storage_slice(saved[2], 0, layout.rows, f32),
+            storage_slice(saved[2], layout.rstd_offset, layout.rows, f32),
+            storage_slice(saved[2], layout.mask_offset, layout.mask_words,
+                          caffe2::TypeMeta::Make<int32_t>()),
+            dropout_p,
+            training,
             branch_dtype == at::kHalf,
             state[2],
             state[3],

@@ -170,6 +170,11 @@ def can_use_residual_layer_norm(x, branch, weight, bias, dropout_p=0.0, eps=1e-5
     return residual_layer_norm_status(x.device).available
 
 
+# Device indices whose backend status is known to be available: the per-call
+# check of the strict path is one dict lookup (small calls are host-bound).
+_READY_DEVICES: set = set()
+
+
 def _strict_native(x, branch, weight, bias, dropout_p, eps, training, normalized_dtype):
     if not x.is_cuda:
         raise RuntimeError(f"{_UNAVAILABLE}: x must be a HIP tensor")
@@ -179,13 +184,14 @@ def _strict_native(x, branch, weight, bias, dropout_p, eps, training, normalized
         raise RuntimeError(
             f"{_UNAVAILABLE}: native hidden size must be one of {NATIVE_HIDDEN_SIZES_TEXT}"
         )
-    status = residual_layer_norm_status(x.device)
-    if not status.available:
-        raise RuntimeError(f"{_UNAVAILABLE}: {status.reason}")
+    device_index = x.get_device()
+    if device_index not in _READY_DEVICES:
+        status = residual_layer_norm_status(x.device)
+        if not status.available:
+            raise RuntimeError(f"{_UNAVAILABLE}: {status.reason}")
+        _READY_DEVICES.add(device_index)
     return native_residual_layer_norm(
-        x, branch, weight, bias, float(dropout_p), float(eps), bool(training),
-        normalized_dtype=normalized_dtype,
-    )
+        x, branch, weight, bias, dropout_p, eps, training, normalized_dtype)
 
 
 def _fall_back(reason, x, branch, weight, bias, dropout_p, eps, training, normalized_dtype):

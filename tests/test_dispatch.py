@@ -72,6 +72,9 @@ class FakeCudaTensor:
     ndim = 2
     shape = (4, 160)
 
+    def get_device(self):
+        return 0
+
 
 @pytest.mark.parametrize("implementation", STRICT)
 def test_forced_kernel_reports_hidden_size_before_backend_lookup(monkeypatch, implementation):
@@ -95,6 +98,7 @@ def test_forced_kernel_reports_unavailable_backend(monkeypatch, implementation):
         "residual_layer_norm_status",
         lambda device=None: BackendStatus(False, "x", "gfx942", "the native extension targets gfx950"),
     )
+    monkeypatch.setattr(normalization, "_READY_DEVICES", set())
     tensor = Tensor768()
     with pytest.raises(RuntimeError, match="unavailable: the native extension targets gfx950"):
         residual_layer_norm(tensor, tensor, tensor, tensor, implementation=implementation)
