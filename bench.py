@@ -40,7 +40,9 @@ C2 hidden-size sweep, C3 deterministic, the C4 cases), each with the same
 fields for its own shape. ``--reference-table`` adds the reference's own
 published measurement, run on this GPU: public-API forward and training-step
 speedups over the PyTorch decomposition at B = 1, H = 384, T = 128 .. 4096,
-beside the speedups the reference publishes for gfx1010.
+beside the speedups the reference publishes for gfx1010. ``--config NAME``
+(repeatable) runs only the named sweep configurations and skips the C1 line,
+so that a profiler run sees one configuration's launches.
 
 Algorithmic bytes per row (H = hidden, bb = branch bytes, mask H/8 bytes when
 dropping):
@@ -200,6 +202,9 @@ def parse_args():
                         help="also time a pre-norm transformer stack, fused vs unfused")
     parser.add_argument("--reference-table", action="store_true",
                         help="also print the reference's published speedup table, measured here")
+    parser.add_argument("--config", action="append", default=[], metavar="NAME",
+                        help="run only this sweep configuration (repeatable; e.g. 'C2 H=1024'), "
+                             "without the C1 line: one kernel's launches per run, for counters")
     return parser.parse_args()
 
 
@@ -639,20 +644,30 @@ def gbps(nbytes: int, ms: float) -> float:
 SPECIALIZED_HIDDEN = (128, 256, 384, 512, 768, 1024)
 
 
+def wide_parts(hidden: int, kernel: str) -> int:
+    """Waves per row of a run-time row length (rln_device.h wide_parts)."""
+    if kernel == "rln_forward_kernel":
+        return 1 if hidden <= 1024 else 2 if hidden <= 2048 else 4 if hidden <= 4096 else 8
+    return (1 if hidden <= 768 else 4 if hidden <= 1024 else 2 if hidden <= 1216 else
+            4 if hidden <= 2432 else 8)
+
+
 def kernel_name(kernel: str, workload: Workload) -> str:
     """The template instance of `kernel` this workload launches (as rocprofv3
     names it): its row shape, branch type, normalized / gradient type, and the
-    aligned access path."""
-    if workload.hidden in SPECIALIZED_HIDDEN:
-        lanes = 64 if (workload.hidden // 4) % 64 == 0 else 32
-        if kernel == "rln_forward_kernel":
-            lanes = {128: 16, 768: 32 if workload.normalized == "f32" else 64, 1024: 64}.get(
-                workload.hidden, 32)
-        shape = f"rln::FixedShape<{workload.hidden}, {lanes}>"
+    aligned access path. Mirrors the dispatch of rln_device.h: the specialized
+    sizes' lanes per row (the forward's forward_lanes), and the run-time-length
+    shapes each pass runs, 1024's backward among them (backward_runs_wide)."""
+    forward = kernel == "rln_forward_kernel"
+    hidden = workload.hidden
+    if hidden in SPECIALIZED_HIDDEN and (forward or hidden != 1024):
+        lanes = 64 if (hidden // 4) % 64 == 0 else 32
+        if forward:
+            lanes = {128: 16, 768: 64, 1024: 64}.get(hidden, 32)
+        shape = f"rln::FixedShape<{hidden}, {lanes}>"
     else:
-        parts = 1 if workload.hidden <= 1024 else 2 if workload.hidden <= 2048 else (
-            4 if workload.hidden <= 4096 else 8)
-        vectors = -(-workload.hidden // (256 * parts))
+        parts = wide_parts(hidden, kernel)
+        vectors = -(-hidden // (256 * parts))
         shape = f"rln::WideShape<{vectors}, {parts}>"
     types = {"f32": "float", "f16": "_Float16", "bf16": "__bf16"}
     return (f"rln::{kernel}<{shape}, {types[workload.branch]}, "
@@ -732,6 +747,12 @@ def main() -> int:
               "(one MI355X per box; the operator is row-parallel and would shard rows "
               "with no communication besides DDP's all-reduce of dW/db).", file=sys.stderr)
         return 2
+    names = [workload.name for workload in sweep_workloads()]
+    unknown = [name for name in args.config if name not in names]
+    if unknown:
+        print(f"bench.py: unknown --config {unknown}; the configurations are {names}",
+              file=sys.stderr)
+        return 2
     import torch
 
     from gfx1010_kernels import _cabi, residual_layer_norm_status
@@ -746,8 +767,8 @@ def main() -> int:
     if TRAFFIC_FILE.exists():
         traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
 
-    with torch.cuda.stream(stream):
-        if args.calibrate_copy_mib:
+    if args.calibrate_copy_mib:
+        with torch.cuda.stream(stream):
             elements = args.calibrate_copy_mib * (1 << 20) // 4
             source = torch.ones(elements, device="cuda")
             destination = torch.empty_like(source)
@@ -756,6 +777,12 @@ def main() -> int:
             print(f"[bench] calibration copy of {args.calibrate_copy_mib} MiB done", flush=True)
             del source, destination
 
+    if args.config:
+        chosen = [workload for workload in sweep_workloads() if workload.name in args.config]
+        run_sweep(torch, library, _cabi, stream, args, chosen)
+        return 0
+
+    with torch.cuda.stream(stream):
         runner = Runner(torch, library, _cabi, C1, args.sets, stream)
         timing = runner.measure(args.warmup, args.steps)
         del runner
@@ -792,22 +819,27 @@ def main() -> int:
             print(json.dumps(line), flush=True)
 
     if args.sweep:
-        for workload in sweep_workloads():
-            torch.cuda.empty_cache()
-            large = workload.rows * workload.hidden >= (1 << 26)
-            sets = 2 if large else args.sets
-            steps = max(args.steps // 10, 20) if large else args.steps
-            with torch.cuda.stream(stream):
-                runner = Runner(torch, library, _cabi, workload, sets, stream)
-                timing = runner.measure(min(args.warmup, 10) if large else args.warmup, steps)
-                del runner
-            line = result_line(torch, workload, timing, steps, args.warmup, sets, None)
-            line["sweep"] = True
-            if not workload.backward and not args.no_cpu_baseline:
-                # C0's forward-only CPU path is cheap to sample (~0.5 ms per step).
-                line["cpu_baseline"] = cpu_baseline(torch, workload, min(args.cpu_seconds, 5.0))
-            print(json.dumps(line), flush=True)
+        run_sweep(torch, library, _cabi, stream, args, sweep_workloads())
     return 0
+
+
+def run_sweep(torch, library, cabi, stream, args, workloads) -> None:
+    """One JSON line per workload (the configurations other than C1)."""
+    for workload in workloads:
+        torch.cuda.empty_cache()
+        large = workload.rows * workload.hidden >= (1 << 26)
+        sets = 2 if large else args.sets
+        steps = max(args.steps // 10, 20) if large else args.steps
+        with torch.cuda.stream(stream):
+            runner = Runner(torch, library, cabi, workload, sets, stream)
+            timing = runner.measure(min(args.warmup, 10) if large else args.warmup, steps)
+            del runner
+        line = result_line(torch, workload, timing, steps, args.warmup, sets, None)
+        line["sweep"] = True
+        if not workload.backward and not args.no_cpu_baseline:
+            # C0's forward-only CPU path is cheap to sample (~0.5 ms per step).
+            line["cpu_baseline"] = cpu_baseline(torch, workload, min(args.cpu_seconds, 5.0))
+        print(json.dumps(line), flush=True)
 
 
 if __name__ == "__main__":
