@@ -648,8 +648,8 @@ def wide_parts(hidden: int, kernel: str) -> int:
     """Waves per row of a run-time row length (rln_device.h wide_parts)."""
     if kernel == "rln_forward_kernel":
         return 1 if hidden <= 1024 else 2 if hidden <= 2048 else 4 if hidden <= 4096 else 8
-    return (1 if hidden <= 768 else 4 if hidden <= 1024 else 2 if hidden <= 1216 else
-            4 if hidden <= 2432 else 8)
+    return (1 if hidden <= 704 else 3 if hidden <= 768 else 4 if hidden <= 1024 else
+            2 if hidden <= 1216 else 4 if hidden <= 2432 else 8)
 
 
 def kernel_name(kernel: str, workload: Workload) -> str:
@@ -657,10 +657,12 @@ def kernel_name(kernel: str, workload: Workload) -> str:
     names it): its row shape, branch type, normalized / gradient type, and the
     aligned access path. Mirrors the dispatch of rln_device.h: the specialized
     sizes' lanes per row (the forward's forward_lanes), and the run-time-length
-    shapes each pass runs, 1024's backward among them (backward_runs_wide)."""
+    shapes each pass runs, 1024's backward and that of 768 columns from 65536
+    rows among them (backward_runs_wide)."""
     forward = kernel == "rln_forward_kernel"
     hidden = workload.hidden
-    if hidden in SPECIALIZED_HIDDEN and (forward or hidden != 1024):
+    runs_wide = hidden == 1024 or (hidden == 768 and workload.rows >= 65536)
+    if hidden in SPECIALIZED_HIDDEN and (forward or not runs_wide):
         lanes = 64 if (hidden // 4) % 64 == 0 else 32
         if forward:
             lanes = {128: 16, 768: 64, 1024: 64}.get(hidden, 32)

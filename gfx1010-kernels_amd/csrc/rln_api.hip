@@ -281,7 +281,7 @@ int rln_forward(
         && aligned_to(updated, 16)
         && aligned_to(normalized, vector_alignment(normalized_dtype))
         && aligned_to(branch, vector_alignment(branch_dtype));
-    return with_shape<Pass::kForward>(hidden, [&](auto shape) {
+    return with_shape<Pass::kForward>(hidden, rows, [&](auto shape) {
         return launch_forward_shape(a, shape, branch_dtype, normalized_dtype, aligned);
     });
 }
@@ -390,7 +390,7 @@ int rln_backward(
         && aligned_to(grad_normalized, vector_alignment(grad_normalized_dtype))
         && aligned_to(updated, 16) && aligned_to(weight, 16) && aligned_to(grad_x, 16)
         && aligned_to(grad_branch, vector_alignment(branch_dtype));
-    status = with_shape<Pass::kBackward>(hidden, [&](auto shape) {
+    status = with_shape<Pass::kBackward>(hidden, rows, [&](auto shape) {
         return launch_backward_shape(a, shape, branch_dtype, grad_normalized_dtype, aligned);
     });
     if (status != RLN_OK) {

@@ -170,6 +170,7 @@ struct FixedShape {
     static constexpr int kRowsPerWave = kWaveSize / kLanes;
     static constexpr bool kRagged = false;
     static constexpr int kForwardThreads = 256;
+    static constexpr int kBackwardBlockThreads = kBackwardThreads;
     static_assert(H % 64 == 0 && (H / 4) % kLanes == 0 && kLanes >= 16,
                   "row must split evenly over lanes");
     __host__ __device__ constexpr int64_t hidden() const { return H; }
@@ -186,8 +187,12 @@ struct WideShape {
     static constexpr int kParts = P;
     static constexpr int kRowsPerWave = 1;
     static constexpr bool kRagged = true;
-    static constexpr int kForwardThreads = P > 4 ? P * kWaveSize : 256;
-    static_assert(P == 1 || P == 2 || P == 4 || P == 8, "parts per row");
+    // Three-wave rows (the backward of large 768-column launches) run in
+    // 12-wave blocks, so that a block still holds whole rows and the grid
+    // keeps one weight/bias partial per CU.
+    static constexpr int kForwardThreads = P == 3 ? 6 * kWaveSize : P > 4 ? P * kWaveSize : 256;
+    static constexpr int kBackwardBlockThreads = P == 3 ? 12 * kWaveSize : kBackwardThreads;
+    static_assert(P == 1 || P == 2 || P == 3 || P == 4 || P == 8, "parts per row");
     int64_t hidden_;
     float inv_hidden_;  // 1.0f / hidden, rounded once on the host
     __host__ __device__ int64_t hidden() const { return hidden_; }
@@ -215,6 +220,7 @@ struct ShapeInfo {
     int parts;
     int vectors;  // slots per lane
     int forward_threads;
+    int backward_threads;
 };
 
 // The forward's shape for dispatch shape S and normalized type N (the
@@ -230,7 +236,7 @@ struct ForwardShape<FixedShape<H, Lanes>, N> {
 
 template <typename S>
 constexpr ShapeInfo info_of() {
-    return {S::kRowsPerWave, S::kParts, S::kV, S::kForwardThreads};
+    return {S::kRowsPerWave, S::kParts, S::kV, S::kForwardThreads, S::kBackwardBlockThreads};
 }
 
 enum class Pass { kForward, kBackward };
@@ -250,25 +256,35 @@ inline int wide_parts(int64_t hidden, Pass pass) {
     if (pass == Pass::kForward) {
         return hidden <= 1024 ? 1 : hidden <= 2048 ? 2 : hidden <= 4096 ? 4 : 8;
     }
-    return hidden <= 768 ? 1 : hidden <= 1024 ? 4 : hidden <= 1216 ? 2 : hidden <= 2432 ? 4 : 8;
+    return hidden <= 704 ? 1 : hidden <= 768 ? 3 : hidden <= 1024 ? 4 : hidden <= 1216 ? 2
+        : hidden <= 2432 ? 4 : 8;
 }
 
-// The specialized size whose backward runs the run-time-length kernel (its
-// 4-wave split of 769-1024 columns).
-inline bool backward_runs_wide(int64_t hidden) {
-    return hidden == 1024;
+// Launches of at least this many rows run the backward of 768 columns on
+// three waves of one slot (wide_parts): measured 2-4 % faster than one wave
+// of three slots from 65536 rows (50 M elements), and 5 % slower at 8192.
+constexpr int64_t kWide768BackwardRows = 65536;
+
+// A specialized size whose backward runs the run-time-length kernel for a
+// launch over `rows`: 1024 columns always (4 waves of one slot, as every row
+// of 769-1024 columns), 768 from kWide768BackwardRows.
+inline bool backward_runs_wide(int64_t hidden, int64_t rows) {
+    return hidden == 1024 || (hidden == 768 && rows >= kWide768BackwardRows);
 }
 
-// The shape of a supported hidden size in one pass.
-inline ShapeInfo shape_info(int64_t hidden, Pass pass) {
-    if (specialized_hidden(hidden) && !(pass == Pass::kBackward && backward_runs_wide(hidden))) {
+// The shape of a supported hidden size in one pass over `rows`.
+inline ShapeInfo shape_info(int64_t hidden, Pass pass, int64_t rows) {
+    if (specialized_hidden(hidden)
+        && !(pass == Pass::kBackward && backward_runs_wide(hidden, rows))) {
         const int lanes = fixed_lanes(hidden);
-        return {kWaveSize / lanes, 1, static_cast<int>(hidden / 4 / lanes), 256};
+        return {kWaveSize / lanes, 1, static_cast<int>(hidden / 4 / lanes), 256,
+                kBackwardThreads};
     }
     const int parts = wide_parts(hidden, pass);
     const int64_t per_slot = 4 * kWaveSize * parts;
     const int vectors = static_cast<int>((hidden + per_slot - 1) / per_slot);
-    return {1, parts, vectors, parts > 4 ? parts * kWaveSize : 256};
+    return {1, parts, vectors, parts == 3 ? 6 * kWaveSize : parts > 4 ? parts * kWaveSize : 256,
+            parts == 3 ? 12 * kWaveSize : kBackwardThreads};
 }
 
 // Blocks for a launch over `rows`: each block works on
@@ -292,10 +308,10 @@ int64_t forward_blocks(int64_t rows) {
 }
 
 // The backward's grid is also the number of weight/bias partials: at most
-// 256 blocks of 8 waves, one block per CU.
+// 256 blocks of 8 waves (12 for three-wave rows), one block per CU.
 inline int64_t backward_blocks(int64_t rows, int64_t hidden) {
-    return launch_blocks(rows, shape_info(hidden, Pass::kBackward), kBackwardThreads,
-                         kBackwardMaxBlocks, 1);
+    const ShapeInfo info = shape_info(hidden, Pass::kBackward, rows);
+    return launch_blocks(rows, info, info.backward_threads, kBackwardMaxBlocks, 1);
 }
 
 // 1 if a launch over rows x hidden walks its rows paced, 0 for look-ahead.
@@ -306,7 +322,7 @@ inline int64_t backward_blocks(int64_t rows, int64_t hidden) {
 // block per CU, where look-ahead is up to 19 % faster); their backward is
 // faster with look-ahead at every size measured (up to 24 %).
 inline int forward_paced(int64_t rows, int64_t hidden) {
-    const ShapeInfo info = shape_info(hidden, Pass::kForward);
+    const ShapeInfo info = shape_info(hidden, Pass::kForward, rows);
     const int64_t elements = rows * hidden;
     if (hidden < kPacedMinHidden || elements < kPacedElements) {
         return 0;
@@ -319,7 +335,7 @@ inline int forward_paced(int64_t rows, int64_t hidden) {
 
 inline int backward_paced(int64_t rows, int64_t hidden) {
     return hidden >= kPacedMinHidden && rows * hidden >= kPacedElements
-        && shape_info(hidden, Pass::kBackward).parts == 1 ? 1 : 0;
+        && shape_info(hidden, Pass::kBackward, rows).parts == 1 ? 1 : 0;
 }
 
 // ----------------------------------------------------------------------------
@@ -968,7 +984,7 @@ enum BackwardFlags : int {
 };
 
 template <typename S, typename B, typename GY, bool Aligned>
-__global__ __launch_bounds__(kBackwardThreads)
+__global__ __launch_bounds__(S::kBackwardBlockThreads)
 void rln_backward_kernel(
     const float* __restrict__ grad_updated,
     const GY* __restrict__ grad_normalized,
@@ -990,7 +1006,7 @@ void rln_backward_kernel(
     constexpr int L = S::kLanes;
     constexpr int V = S::kV;
     constexpr int P = S::kParts;
-    using T = Teams<S, kBackwardThreads>;
+    using T = Teams<S, S::kBackwardBlockThreads>;
     constexpr int kWaves = T::kWaves;
     constexpr bool kTwoAhead = P == 1 && V <= 3;
     const int64_t hidden = shape.hidden();
@@ -1182,7 +1198,7 @@ void rln_backward_kernel(
     __syncthreads();
     // V x P x L owners x 8 floats to produce; the block's threads share them.
     constexpr int kPerSlot = P * L * 8;
-    for (int entry = threadIdx.x; entry < V * kPerSlot; entry += kBackwardThreads) {
+    for (int entry = threadIdx.x; entry < V * kPerSlot; entry += S::kBackwardBlockThreads) {
         const int v = entry / kPerSlot;
         const int owner = (entry % kPerSlot) / 8;
         const int owner_part = owner / L;
@@ -1255,13 +1271,14 @@ struct BackwardArgs {
 };
 
 // The dispatch shape must be the one shape_info() describes for the hidden
-// size and pass, since the backward's grid (and so the deterministic order
-// and the workspace size) is computed from the latter.
+// size, pass and rows, since the backward's grid (and so the deterministic
+// order and the workspace size) is computed from the latter.
 template <typename S>
-int check_shape(const S& shape, Pass pass) {
-    const ShapeInfo info = shape_info(shape.hidden(), pass);
+int check_shape(const S& shape, Pass pass, int64_t rows) {
+    const ShapeInfo info = shape_info(shape.hidden(), pass, rows);
     if (info.parts != S::kParts || info.rows_per_wave != S::kRowsPerWave
-        || info.vectors != S::kV || info.forward_threads != S::kForwardThreads) {
+        || info.vectors != S::kV || info.forward_threads != S::kForwardThreads
+        || info.backward_threads != S::kBackwardBlockThreads) {
         return fail(RLN_ERR_UNSUPPORTED, "shape mismatch for hidden size %lld",
                     static_cast<long long>(shape.hidden()));
     }
@@ -1297,7 +1314,7 @@ int launch_forward(const ForwardArgs& a, S shape) {
 template <typename S, typename B, typename GY, bool Aligned>
 int launch_backward(const BackwardArgs& a, S shape) {
     const dim3 grid(static_cast<unsigned>(backward_blocks(a.rows, shape.hidden())));
-    rln_backward_kernel<S, B, GY, Aligned><<<grid, kBackwardThreads, 0, a.stream>>>(
+    rln_backward_kernel<S, B, GY, Aligned><<<grid, S::kBackwardBlockThreads, 0, a.stream>>>(
         a.grad_updated,
         static_cast<const GY*>(a.grad_normalized),
         a.updated,
@@ -1335,7 +1352,7 @@ int with_dtype(int dtype, Launch&& launch) {
 template <typename S>
 int launch_forward_shape(const ForwardArgs& a, S shape, int branch_dtype, int normalized_dtype,
                          bool aligned) {
-    const int status = check_shape(shape, Pass::kForward);
+    const int status = check_shape(shape, Pass::kForward, a.rows);
     if (status != RLN_OK) {
         return status;
     }
@@ -1355,7 +1372,7 @@ int launch_forward_shape(const ForwardArgs& a, S shape, int branch_dtype, int no
 template <typename S>
 int launch_backward_shape(const BackwardArgs& a, S shape, int branch_dtype,
                           int grad_normalized_dtype, bool aligned) {
-    const int status = check_shape(shape, Pass::kBackward);
+    const int status = check_shape(shape, Pass::kBackward, a.rows);
     if (status != RLN_OK) {
         return status;
     }
@@ -1368,27 +1385,32 @@ int launch_backward_shape(const BackwardArgs& a, S shape, int branch_dtype,
 }
 
 // The row shapes, one translation unit each (rln_hidden.hip): the
-// specialized sizes (the backward of those backward_runs_wide names excepted),
+// specialized sizes (1024's backward excepted, backward_runs_wide),
 // and the (slots per lane, waves per row) pairs of the run-time lengths each
 // pass runs (wide_parts).
 #define RLN_FOR_EACH_FIXED(X) X(128) X(256) X(384) X(512) X(768) X(1024)
 #define RLN_FOR_EACH_WIDE_FORWARD(X) \
     X(1, 1) X(2, 1) X(3, 1) X(4, 1) X(3, 2) X(4, 2) X(3, 4) X(4, 4) X(3, 8) X(4, 8)
 #define RLN_FOR_EACH_WIDE_BACKWARD(X) \
-    X(1, 1) X(2, 1) X(3, 1) X(1, 4) X(3, 2) X(2, 4) X(3, 4) X(2, 8) X(3, 8) X(4, 8)
+    X(1, 1) X(2, 1) X(3, 1) X(1, 3) X(1, 4) X(3, 2) X(2, 4) X(3, 4) X(2, 8) X(3, 8) X(4, 8)
 
 #define RLN_WIDE_CASE(V, P) \
     case P * 16 + V: return launch(WideShape<V, P>{hidden, inv_hidden});
 
-// Calls `launch(shape)` with the shape a supported hidden size runs in `kPass`.
+// Calls `launch(shape)` with the shape a supported hidden size runs in
+// `kPass` over `rows`.
 template <Pass kPass, typename Launch>
-int with_shape(int64_t hidden, Launch&& launch) {
+int with_shape(int64_t hidden, int64_t rows, Launch&& launch) {
     switch (hidden) {
         case 128: return launch(FixedShape<128>{});
         case 256: return launch(FixedShape<256>{});
         case 384: return launch(FixedShape<384>{});
         case 512: return launch(FixedShape<512>{});
-        case 768: return launch(FixedShape<768>{});
+        case 768:
+            if (kPass == Pass::kForward || !backward_runs_wide(hidden, rows)) {
+                return launch(FixedShape<768>{});
+            }
+            break;
         case 1024:
             if constexpr (kPass == Pass::kForward) {
                 return launch(FixedShape<1024>{});
@@ -1400,7 +1422,7 @@ int with_shape(int64_t hidden, Launch&& launch) {
         return fail(RLN_ERR_UNSUPPORTED, "unsupported native hidden size: %lld",
                     static_cast<long long>(hidden));
     }
-    const ShapeInfo info = shape_info(hidden, kPass);
+    const ShapeInfo info = shape_info(hidden, kPass, rows);
     const float inv_hidden = 1.0f / static_cast<float>(hidden);
     if constexpr (kPass == Pass::kForward) {
         switch (info.parts * 16 + info.vectors) {

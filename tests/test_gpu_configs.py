@@ -17,12 +17,13 @@ import torch
 from gfx1010_kernels import _C
 from oracle import rln_oracle as oracle
 from parity import (
+    KIND,
     TOL_FORWARD,
     TOL_INPUT_GRAD,
     TOL_PARAMETER_GRAD,
     assert_bitwise,
-    assert_fp16_close,
     assert_normwise,
+    assert_rounded_close,
     check_backward,
     check_forward,
     generator_state,
@@ -87,7 +88,7 @@ def check_sampled_rows(inputs, grads, outputs, gradients, dropout_p, seed, offse
         keep = oracle.decode_mask(words, len(picked), hidden)
     take = lambda t: host(t.index_select(0, index))  # noqa: E731
     expected = oracle.forward(take(x), take(branch), host(weight), host(bias), EPS, keep=keep,
-                              scale=scale)
+                              scale=scale, branch_type=KIND[branch.dtype])
     assert_bitwise(take(outputs[0]), expected["updated"], "sampled updated")
     assert_normwise(take(outputs[1]), expected["normalized"], TOL_FORWARD, "sampled normalized")
     assert_normwise(host(outputs[2][index]), expected["mean"], TOL_FORWARD, "sampled mean")
@@ -96,10 +97,11 @@ def check_sampled_rows(inputs, grads, outputs, gradients, dropout_p, seed, offse
                                     host(weight), EPS, keep=keep, scale=scale)
     assert_normwise(take(gradients[0]), grad_expected["grad_x"], TOL_INPUT_GRAD, "sampled grad_x")
     grad_branch = take(gradients[1])
-    if grad_branch.dtype == np.float16:
-        assert_fp16_close(grad_branch, grad_expected["grad_branch"], "sampled grad_branch")
-    else:
+    if gradients[1].dtype == torch.float32:
         assert_normwise(grad_branch, grad_expected["grad_branch"], TOL_INPUT_GRAD, "sampled grad_branch")
+    else:
+        assert_rounded_close(grad_branch, grad_expected["grad_branch"], KIND[gradients[1].dtype],
+                             "sampled grad_branch")
 
 
 def check_parameter_gradients(updated, grad_normalized, gradients, chunk=16384):
@@ -150,6 +152,40 @@ def test_c2_hidden_sweep_at_262144_rows(hidden):
     check_parameter_gradients(outputs[0], grads[1], gradients)
     n = rows * hidden
     assert abs(keep_count(outputs[4]) - 0.85 * n) < 6 * np.sqrt(n * 0.15 * 0.85)
+
+
+@pytest.mark.parametrize("rows", [65535, 65536])
+@pytest.mark.parametrize("branch_dtype,grad_normalized_dtype",
+                         [(torch.float16, torch.float32), (torch.bfloat16, torch.bfloat16)])
+def test_768_backward_on_both_sides_of_its_three_wave_switch(rows, branch_dtype,
+                                                             grad_normalized_dtype):
+    """From 65536 rows the backward of 768 columns runs three waves of one
+    slot per row (12-wave blocks), below it one wave of three slots: both
+    sides against the oracle on sampled rows and a float64 reduction of
+    dW/db, and each replays bitwise in deterministic mode."""
+    hidden = 768
+    inputs, grads = device_inputs(rows, hidden, branch_dtype, seed=4242)
+    grads = (grads[0], grads[1].to(grad_normalized_dtype))
+    torch.cuda.manual_seed(4242)
+    seed, offset = generator_state()
+    outputs = _C.residual_layer_norm_forward(*inputs, 0.1, EPS, True, 128)
+
+    def backward():
+        return _C.residual_layer_norm_backward(
+            grads[0], grads[1], outputs[0], inputs[2], outputs[2], outputs[3], outputs[4], 0.1,
+            True, branch_dtype == torch.float16, 128, 64, 64, 1, True, branch_dtype)
+
+    with deterministic_algorithms(True):
+        gradients = backward()
+        again = backward()
+    for first, second in zip(gradients, again):
+        assert torch.equal(first, second)
+    check_sampled_rows(inputs, grads, outputs, gradients, 0.1, seed, offset)
+    check_parameter_gradients(outputs[0], grads[1], gradients)
+    with deterministic_algorithms(False):
+        atomic = backward()
+    assert torch.equal(atomic[0], gradients[0]) and torch.equal(atomic[1], gradients[1])
+    check_parameter_gradients(outputs[0], grads[1], atomic)
 
 
 def test_c3_deterministic_bitwise_replay_over_three_runs():
