@@ -627,7 +627,10 @@ __device__ __forceinline__ float team_sum(float value, float (*exchange)[S::kPar
 // wave). Each lane then reads the 4 bits of each of its slots and returns
 // them packed, slot v in bits 4v .. 4v + 3. `stage` is the row's H / 16
 // pieces, used by this wave only: LDS accesses of one wave complete in
-// order, so no barrier is needed. Requires offset % 4 == 0 and at most 8
+// order, so no block barrier is needed; two wave barriers (compiler
+// ordering fences) keep the cross-lane handoff from being reordered: the
+// writes after the previous row's reads, the reads after the writes.
+// Requires offset % 4 == 0 and at most 8
 // items (the reference's two hiprand4 calls), checked on the host.
 template <typename S>
 __device__ __forceinline__ uint32_t reference_keep_bits(
@@ -643,6 +646,11 @@ __device__ __forceinline__ uint32_t reference_keep_bits(
     // Threads k * L + l with k >= H / L own no column (item 0 is already past
     // the row), so their draws are skipped.
     const int k_end = per_item < kChunks ? per_item : kChunks;
+    // The previous row's reads of `stage` (other lanes of this wave) come
+    // before this row's writes: a wave barrier keeps the compiler from
+    // moving LDS accesses across it, and one wave's LDS operations complete
+    // in issue order.
+    __builtin_amdgcn_wave_barrier();
     for (int k = 0; k < k_end; ++k) {
         const uint64_t subsequence = static_cast<uint64_t>(row) * threads + k * L + lane;
         for (int n = 0; n < calls; ++n) {
@@ -667,6 +675,8 @@ __device__ __forceinline__ uint32_t reference_keep_bits(
             }
         }
     }
+    // The staging writes of lanes < L / 16 come before every lane's reads.
+    __builtin_amdgcn_wave_barrier();
     uint32_t keep = 0;
 #pragma unroll
     for (int v = 0; v < S::kV; ++v) {

@@ -9,11 +9,16 @@ fused op instead of breaking around it (the reference does not support
 ``torch.compile``; docs/residual_layer_norm.md:301-302).
 
 * ``gfx1010_kernels::rln_forward(x, branch, weight, bias, dropout_p, eps, training,
-  normalized_dtype) -> (updated, normalized, mean, rstd, mask)`` runs
+  normalized_dtype, nonce) -> (updated, normalized, mean, rstd, mask)`` runs
   ``_C.residual_layer_norm_forward`` with the eager path's ``threads``; with
   dropout it reserves its Philox offsets from the device's default generator
   when it executes, exactly as the eager path does, so compiled and eager runs
-  draw the same masks from the same RNG state.
+  draw the same masks from the same RNG state. ``nonce`` is a fresh zero-size
+  tensor per call (``residual_layer_norm_op`` makes it): the op draws from the
+  generator, so two calls with equal arguments are different computations,
+  and the nonce keeps a compiler from merging them. AOTAutograd's common
+  subexpression pass merges identical calls of a functional custom op, but
+  never two ``aten.empty`` nodes, so each call's nonce differs.
 * ``gfx1010_kernels::rln_backward(grad_updated, grad_normalized, updated, weight,
   mean, rstd, mask, dropout_p, training, branch_dtype)
   -> (grad_x, grad_branch, grad_weight, grad_bias)`` runs
@@ -54,6 +59,7 @@ def rln_forward(
     eps: float,
     training: bool,
     normalized_dtype: Optional[torch.dtype] = None,
+    nonce: Optional[Tensor] = None,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor, Tensor]:
     return tuple(
         _native().residual_layer_norm_forward(
@@ -65,7 +71,8 @@ def rln_forward(
 
 
 @rln_forward.register_fake
-def _rln_forward_fake(x, branch, weight, bias, dropout_p, eps, training, normalized_dtype=None):
+def _rln_forward_fake(x, branch, weight, bias, dropout_p, eps, training, normalized_dtype=None,
+                      nonce=None):
     hidden = x.shape[-1]
     rows = x.numel() // hidden
     mask_words = rows * (hidden // 32) if (training and dropout_p > 0.0) else 0
@@ -113,7 +120,7 @@ def _rln_backward_fake(grad_updated, grad_normalized, updated, weight, mean, rst
 
 
 def _setup_context(ctx, inputs, output):
-    _, branch, weight, _, dropout_p, _, training, _ = inputs
+    _, branch, weight, _, dropout_p, _, training, _, _ = inputs
     updated, _, mean, rstd, mask = output
     ctx.save_for_backward(updated, weight, mean, rstd, mask)
     ctx.dropout_p = dropout_p
@@ -125,7 +132,7 @@ def _setup_context(ctx, inputs, output):
 
 def _backward(ctx, grad_updated, grad_normalized, _grad_mean, _grad_rstd, _grad_mask):
     if grad_updated is None and grad_normalized is None:
-        return None, None, None, None, None, None, None, None
+        return None, None, None, None, None, None, None, None, None
     updated, weight, mean, rstd, mask = ctx.saved_tensors
     if grad_updated is not None:
         grad_updated = grad_updated.contiguous()
@@ -137,7 +144,7 @@ def _backward(ctx, grad_updated, grad_normalized, _grad_mean, _grad_rstd, _grad_
     )
     if grad_normalized is None:
         grad_weight = grad_bias = None
-    return grad_x, grad_branch, grad_weight, grad_bias, None, None, None, None
+    return grad_x, grad_branch, grad_weight, grad_bias, None, None, None, None, None
 
 
 rln_forward.register_autograd(_backward, setup_context=_setup_context)
@@ -145,9 +152,13 @@ rln_forward.register_autograd(_backward, setup_context=_setup_context)
 
 def residual_layer_norm_op(x, branch, weight, bias, dropout_p, eps, training,
                            normalized_dtype=None):
-    """``(updated, normalized)`` through the registered custom op."""
+    """``(updated, normalized)`` through the registered custom op. Each call
+    passes a new zero-size nonce, so two dropout calls on equal arguments stay
+    two draws under ``torch.compile``."""
+    nonce = torch.empty(0, device=x.device)
     updated, normalized, _, _, _ = rln_forward(
-        x, branch, weight, bias, float(dropout_p), float(eps), bool(training), normalized_dtype
+        x, branch, weight, bias, float(dropout_p), float(eps), bool(training), normalized_dtype,
+        nonce,
     )
     return updated, normalized
 

@@ -9,6 +9,8 @@ and AOTAutograd without generating code for the surrounding ops.
 
 import contextlib
 
+import numpy as np
+
 import pytest
 import torch
 
@@ -81,3 +83,37 @@ def test_compiled_auto_falls_back_for_non_native_hidden_size():
     expected = torch.nn.functional.layer_norm(inputs[0] + inputs[1], (160,), inputs[2],
                                               inputs[3], 1e-5)
     torch.testing.assert_close(compiled(*inputs)[1], expected)
+
+
+@pytest.mark.parametrize("backend", ["inductor", "aot_eager"])
+def test_two_equal_dropout_calls_in_one_compiled_graph(backend):
+    """Two calls on equal arguments in one compiled training graph draw two
+    masks, equal bit for bit to two eager calls from the same RNG state, and
+    leave the generator where the eager calls leave it (AOTAutograd's
+    common-subexpression pass must not merge them into one draw)."""
+    shape = (3, 40, 768)
+    inputs = make_inputs(shape, torch.float16, seed=21)
+
+    def two_calls(x, branch, weight, bias):
+        first = residual_layer_norm(x, branch, weight, bias, dropout_p=0.5,
+                                    implementation="gfx950")
+        second = residual_layer_norm(x, branch, weight, bias, dropout_p=0.5,
+                                     implementation="gfx950")
+        return (*first, *second)
+
+    compiled = torch.compile(two_calls, backend=backend, fullgraph=True)
+    results, offsets = [], []
+    for function in (two_calls, compiled):
+        leaves = [t.detach().clone().requires_grad_(True) for t in inputs]
+        torch.cuda.manual_seed(77)
+        outputs = function(*leaves)
+        offsets.append(torch.cuda.default_generators[0].get_offset())
+        torch.cuda.synchronize()
+        results.append([host(t) for t in outputs])
+    eager, traced = results
+    # The two eager draws differ (a merged call would return the same
+    # `updated` twice).
+    assert not np.array_equal(eager[0], eager[2])
+    for index, (expected, actual) in enumerate(zip(eager, traced)):
+        assert_bitwise(actual, expected, f"compiled output {index} vs eager")
+    assert offsets[1] == offsets[0]

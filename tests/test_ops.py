@@ -44,3 +44,36 @@ def test_fake_shapes(shape, branch_dtype, dropout_p, training):
         assert grad_x.shape == grad_branch.shape == x.shape
         assert grad_x.dtype == torch.float32 and grad_branch.dtype == branch_dtype
         assert grad_weight.shape == grad_bias.shape == (hidden,)
+
+
+def _forward_nodes(graph):
+    return [node for node in graph.nodes
+            if node.op == "call_function" and "rln_forward" in str(node.target)]
+
+
+@pytest.mark.parametrize("dropout_p", [0.1, 0.0])
+def test_two_equal_calls_survive_common_subexpression_elimination(dropout_p):
+    """Two calls with equal arguments draw two masks eagerly (the op reserves
+    Philox offsets each time it runs), so a compiled graph must keep both.
+    The graph is traced from fake CUDA tensors and put through AOTAutograd's
+    common-subexpression pass (which it runs on the joint forward/backward
+    graph of a training step), the pass that merged them while the op had no
+    per-call input."""
+    from torch._functorch.compile_utils import fx_graph_cse
+    from torch.fx.experimental.proxy_tensor import make_fx
+
+    from gfx1010_kernels._ops import residual_layer_norm_op
+
+    def two_calls(x, branch, weight, bias):
+        first = residual_layer_norm_op(x, branch, weight, bias, dropout_p, 1e-5, True)
+        second = residual_layer_norm_op(x, branch, weight, bias, dropout_p, 1e-5, True)
+        return (*first, *second)
+
+    with FakeTensorMode():
+        x = torch.empty(6, 768, device="cuda")
+        branch = torch.empty(6, 768, device="cuda", dtype=torch.float16)
+        weight = torch.empty(768, device="cuda")
+        bias = torch.empty(768, device="cuda")
+        module = make_fx(two_calls, tracing_mode="fake")(x, branch, weight, bias)
+    assert len(_forward_nodes(module.graph)) == 2
+    assert len(_forward_nodes(fx_graph_cse(module.graph))) == 2
