@@ -25,8 +25,16 @@ Prints one JSON line:
   cpu_baseline the reference's CPU decomposition (F.dropout + add +
                F.layer_norm, forward + autograd) on this host's cores
   step_us_spread  p20 / median / p80 of the step time over batches of 25
-  copy_ceiling    a plain device copy's GB/s at ~100 MB per launch, the
-               practical streaming ceiling on this box
+  copy_ceiling    a plain device copy's GB/s at ~100 MB per launch
+  ceiling_us   the streaming ceiling of this workload: one-pass non-temporal
+               kernels with the forward's and the backward's exact streams
+               (csrc/rln_ceiling.hip), timed like the op's kernels, and the
+               op's times as a fraction of them
+  parity       the timed C-ABI step (set 0, its Philox offset, weight/bias
+               sums accumulated from zero) checked before timing against the
+               PyTorch decomposition in float64 on this GPU, with the kernel's
+               own dropout mask applied: updated bitwise, the rest normwise at
+               the test suite's bars; a miss ends the run with status 1
   public_api      whole autograd steps through the public Python API on this
                GPU: these kernels (implementation="gfx950") and the
                reference's decomposition run by PyTorch-ROCm ("torch")
@@ -35,6 +43,15 @@ Prints one JSON line:
                (B = 1, H = 384), at T = 262144 where the GPU work dominates,
                beside the best ratios the reference publishes for gfx1010
 
+The roofline kernel's average duration comes from a fixed 400 back-to-back
+launches, whatever ``--steps`` is. ``roofline.traffic`` is read from
+profiles/rln_backward_c1_traffic.json only when that file's kernel-source
+digest matches the sources in this tree (else null, with ``traffic_note``);
+``--traffic-summary FETCH_DIR WRITE_DIR`` writes that file from two
+``rocprofv3 --pmc FETCH_SIZE`` / ``WRITE_SIZE`` runs of ``bench.py --quick
+--calibrate-copy-mib 256``. ``--quick`` runs the C1 line alone (no public-API,
+reference-method, ceiling or CPU legs), for profiler passes.
+
 ``--sweep`` adds one JSON line per other BASELINE.json configuration (C0, the
 C2 hidden-size sweep, C3 deterministic, the C4 cases), each with the same
 fields for its own shape. ``--reference-table`` adds the reference's own
@@ -42,7 +59,9 @@ published measurement, run on this GPU: public-API forward and training-step
 speedups over the PyTorch decomposition at B = 1, H = 384, T = 128 .. 4096,
 beside the speedups the reference publishes for gfx1010. ``--config NAME``
 (repeatable) runs only the named sweep configurations and skips the C1 line,
-so that a profiler run sees one configuration's launches.
+so that a profiler run sees one configuration's launches. ``--ceiling`` adds
+one line per configuration (C1 and the sweep's, or the ``--config`` ones)
+with the op's and the streaming-ceiling kernels' times side by side.
 
 Algorithmic bytes per row (H = hidden, bb = branch bytes, mask H/8 bytes when
 dropping):
@@ -53,6 +72,8 @@ dropping):
 from __future__ import annotations
 
 import argparse
+import ctypes
+import hashlib
 import json
 import os
 import platform
@@ -71,6 +92,11 @@ HBM_PEAK_GBPS = 8000.0
 METRIC = "fwd & fwd+bwd achieved HBM GB/s (% of ~8 TB/s peak), rows/s at H=768"
 EPS = 1e-5
 TRAFFIC_FILE = REPO / "profiles" / "rln_backward_c1_traffic.json"
+CSRC = REPO / "gfx1010-kernels_amd" / "csrc"
+KERNEL_SOURCES = ("rln_device.h", "rln_api.hip", "rln_hidden.hip")
+CEILING_LIBRARY = REPO / "gfx1010-kernels_amd" / "gfx1010_kernels" / "librln_ceiling_gfx950.so"
+# Back-to-back launches timed for the roofline kernel and the ceiling kernels.
+ROOFLINE_LAUNCHES = 400
 
 
 # The reference's threads per row (reference _normalization_native.py:5-12),
@@ -202,6 +228,13 @@ def parse_args():
                         help="also time a pre-norm transformer stack, fused vs unfused")
     parser.add_argument("--reference-table", action="store_true",
                         help="also print the reference's published speedup table, measured here")
+    parser.add_argument("--ceiling", action="store_true",
+                        help="add op-vs-streaming-ceiling lines per configuration")
+    parser.add_argument("--quick", action="store_true",
+                        help="C1 line only (no public-API, reference, ceiling or CPU legs)")
+    parser.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                        help="write profiles/rln_backward_c1_traffic.json from two rocprofv3 "
+                             "--pmc output directories (no GPU needed)")
     parser.add_argument("--config", action="append", default=[], metavar="NAME",
                         help="run only this sweep configuration (repeatable; e.g. 'C2 H=1024'), "
                              "without the C1 line: one kernel's launches per run, for counters")
@@ -568,7 +601,10 @@ class Runner:
         end.synchronize()
         return start.elapsed_time(end) / count
 
-    def measure(self, warmup: int, steps: int) -> dict:
+    def measure(self, warmup: int, steps: int, launches: int = ROOFLINE_LAUNCHES) -> dict:
+        """Step time over exactly `steps` timed steps (the contract's K); the
+        per-kernel averages (the roofline) over `launches` back-to-back
+        launches of one kernel, whatever `steps` is."""
         w = self.w
         for index in range(warmup):
             self.step(index)
@@ -582,14 +618,15 @@ class Runner:
         for _ in range(max(steps // 25, 4)):
             batches.append(self.timed(lambda i: self.step(base + i), 25))
             base += 25
-        forward_ms = self.timed(lambda i: self.forward(base + i), steps)
-        base += steps
-        result = {"step_ms": step_ms, "forward_ms": forward_ms, "step_batches_ms": batches}
+        forward_ms = self.timed(lambda i: self.forward(base + i), launches)
+        base += launches
+        result = {"step_ms": step_ms, "forward_ms": forward_ms, "step_batches_ms": batches,
+                  "launches": launches}
         if w.backward:
             # Every set now holds the saved state of a forward; re-running the
             # backward on it is the same work as the step's backward.
-            result["backward_ms"] = self.timed(lambda i: self.backward(base + i), steps)
-            base += steps
+            result["backward_ms"] = self.timed(lambda i: self.backward(base + i), launches)
+            base += launches
             # Backward on the set forwarded `lag` steps earlier (two, or one
             # when only two sets rotate).
             lag = min(2, len(self.sets) - 1)
@@ -625,6 +662,245 @@ def copy_ceiling(torch, stream, mib: int = 50, copies: int = 200) -> dict:
     moved = 2 * elements * 4
     return {"gbps": round(moved / (us * 1e-6) / 1e9, 1), "us_per_copy": round(us, 3),
             "bytes_moved": moved, "kind": f"torch copy_ of {mib} MiB, 4 buffer pairs rotated"}
+
+
+def kernel_sources_digest() -> str:
+    """Digest of the kernel sources a traffic profile describes."""
+    digest = hashlib.sha256()
+    for name in KERNEL_SOURCES:
+        digest.update(name.encode())
+        digest.update((CSRC / name).read_bytes())
+    return digest.hexdigest()[:16]
+
+
+def load_traffic() -> tuple[int | None, str]:
+    """HBM bytes per C1 backward launch from the committed PMC summary, when it
+    profiles the kernel sources in this tree; else (None, why not)."""
+    if not TRAFFIC_FILE.exists():
+        return None, f"no {TRAFFIC_FILE.name}"
+    record = json.loads(TRAFFIC_FILE.read_text())
+    digest = kernel_sources_digest()
+    if record.get("sources_digest") != digest:
+        return None, (f"stale: {TRAFFIC_FILE.name} profiles kernel sources "
+                      f"{record.get('sources_digest')}, this tree has {digest}")
+    return record["hbm_bytes_per_launch"], (
+        f"rocprofv3 PMC FETCH_SIZE x {record['fetch_scale']} + WRITE_SIZE x "
+        f"{record['write_scale']} per dispatch, kernel sources {digest}, commit "
+        f"{record.get('commit')}")
+
+
+def _counter_means(directory: str) -> tuple[str, dict[str, float]]:
+    """(counter name, mean value per dispatch by kernel name) of one rocprofv3
+    --pmc csv output directory."""
+    import csv
+    from collections import defaultdict
+
+    files = sorted(Path(directory).rglob("*counter_collection.csv"))
+    if not files:
+        raise SystemExit(f"bench.py: no *counter_collection.csv under {directory}")
+    values, counter = defaultdict(list), None
+    for path in files:
+        with path.open() as handle:
+            for row in csv.DictReader(handle):
+                counter = row["Counter_Name"]
+                values[row["Kernel_Name"]].append(float(row["Counter_Value"]))
+    return counter, {name: sum(v) / len(v) for name, v in values.items()}
+
+
+def traffic_summary(fetch_dir: str, write_dir: str) -> int:
+    """Writes TRAFFIC_FILE from a FETCH_SIZE and a WRITE_SIZE pass of
+    `bench.py --quick --calibrate-copy-mib 256`: each counter (KiB per
+    dispatch) is scaled by what it reads for the 256 MiB calibration copy
+    (the runtime's copyBuffer kernel: 262144 KiB read and written)."""
+    fetch_counter, fetch = _counter_means(fetch_dir)
+    write_counter, write = _counter_means(write_dir)
+    if (fetch_counter, write_counter) != ("FETCH_SIZE", "WRITE_SIZE"):
+        raise SystemExit(f"bench.py: expected FETCH_SIZE and WRITE_SIZE, got "
+                         f"{fetch_counter} and {write_counter}")
+
+    def lookup(table, prefix):
+        matches = [value for name, value in table.items() if name.startswith(prefix)]
+        if len(matches) != 1:
+            raise SystemExit(f"bench.py: {len(matches)} kernels named {prefix}")
+        return matches[0]
+
+    copy = "__amd_rocclr_copyBuffer"
+    fetch_scale = 262144.0 / lookup(fetch, copy)
+    write_scale = 262144.0 / lookup(write, copy)
+    record = {"workload": C1.describe(), "sources_digest": kernel_sources_digest()}
+    try:
+        import subprocess
+
+        record["commit"] = subprocess.run(["git", "-C", str(REPO), "rev-parse", "--short=12",
+                                           "HEAD"], capture_output=True, text=True,
+                                          check=True).stdout.strip()
+    except (OSError, subprocess.CalledProcessError):
+        record["commit"] = None
+    record.update(fetch_scale=round(fetch_scale, 5), write_scale=round(write_scale, 5))
+    for kernel, key, algorithmic in (("rln_backward_kernel", "", C1.backward_bytes()),
+                                     ("rln_forward_kernel", "forward_", C1.forward_bytes())):
+        name = kernel_name(kernel, C1)
+        fetch_kib, write_kib = lookup(fetch, name), lookup(write, name)
+        hbm = round(1024 * (fetch_kib * fetch_scale + write_kib * write_scale))
+        record[f"{key}kernel"] = name
+        record[f"{key}fetch_kib_per_dispatch"] = round(fetch_kib, 2)
+        record[f"{key}write_kib_per_dispatch"] = round(write_kib, 2)
+        record[f"{key}hbm_bytes_per_launch"] = hbm
+        record[f"{key}algorithmic_bytes_per_launch"] = algorithmic
+    TRAFFIC_FILE.write_text(json.dumps(record, indent=1) + "\n")
+    print(json.dumps(record))
+    return 0
+
+
+def decode_mask(torch, words, rows: int, hidden: int):
+    """keep[r, c] = bit c % 32 of int32 word r * hidden / 32 + c / 32, on the device."""
+    shifts = torch.arange(32, device=words.device, dtype=torch.int32)
+    bits = (words.view(rows, hidden // 32, 1) >> shifts) & 1
+    return bits.view(rows, hidden).bool()
+
+
+def parity_self_check(torch, runner: "Runner") -> dict:
+    """One step of exactly the path the benchmark times (set 0, step 0's Philox
+    offset, the weight/bias gradients accumulated into zeroed sums), checked
+    against the reference's decomposition (dropout -> add -> LayerNorm, and its
+    gradients, reference gfx1010_kernels/normalization.py:15-33) in float64 on
+    this GPU, with the kernel's own dropout mask applied explicitly: `updated`
+    bitwise; normalized, mean, rstd, grad_x (normwise <= 1e-5), grad_branch
+    (one ulp of its type + 1e-5 of the largest value), dW/db (normwise <= 1e-4),
+    and the mask's keep ratio within 6 sigma of 1 - p."""
+    w, t = runner.w, runner.sets[0]
+    t["grad_weight"].zero_()
+    t["grad_bias"].zero_()
+    runner.forward(0)
+    if w.backward:
+        runner.backward(0)
+    torch.cuda.synchronize()
+    f64 = torch.float64
+    rows, hidden = w.rows, w.hidden
+    branch = t["branch"].float()
+    errors, ok = {}, True
+    if w.dropping:
+        # 1.0f / (1.0f - float(p)), in fp32 as the library computes it
+        # (reference csrc/residual_layer_norm_kernel.hip:898-899).
+        one = torch.tensor(1.0, dtype=torch.float32)
+        scale = (one / (one - torch.tensor(w.dropout_p, dtype=torch.float32))).item()
+        keep = decode_mask(torch, t["mask"], rows, hidden)
+        dropped = ((branch * keep.float()) * scale).to(t["branch"].dtype).float()
+        kept = keep.double().mean().item()
+        sigma = (w.dropout_p * (1 - w.dropout_p) / (rows * hidden)) ** 0.5
+        errors["keep_ratio"] = round(kept, 6)
+        ok &= abs(kept - (1 - w.dropout_p)) <= 6 * sigma
+    else:
+        keep, scale, dropped = None, 1.0, branch
+    updated = t["x"] + dropped
+    errors["updated_bitwise"] = bool(torch.equal(updated.view(torch.int32),
+                                                 t["updated"].view(torch.int32)))
+    ok &= errors["updated_bitwise"]
+
+    def normwise(actual, expected):
+        return (actual.to(f64) - expected).abs().max().item() / max(expected.abs().max().item(),
+                                                                   1e-30)
+
+    def ulp_excess(actual, expected, dtype):
+        if dtype == torch.float32:
+            return normwise(actual, expected) - 1e-5
+        bits = 10 if dtype == torch.float16 else 7
+        floor = -14 if dtype == torch.float16 else -126
+        exponent = torch.floor(torch.log2(expected.abs().clamp_min(2.0 ** floor)))
+        bound = torch.exp2(exponent - bits) + 1e-5 * expected.abs().max()
+        return ((actual.to(f64) - expected).abs() - bound).max().item()
+
+    u = updated.to(f64)
+    mean = u.mean(dim=1)
+    centred = u - mean[:, None]
+    rstd = 1.0 / torch.sqrt((centred * centred).mean(dim=1) + EPS)
+    xhat = centred * rstd[:, None]
+    weight, bias = runner.weight.to(f64), runner.bias.to(f64)
+    normalized = xhat * weight + bias
+    errors["mean"] = normwise(t["mean"], mean)
+    errors["rstd"] = normwise(t["rstd"], rstd)
+    errors["normalized"] = (normwise(t["normalized"], normalized)
+                            if t["normalized"].dtype == torch.float32
+                            else ulp_excess(t["normalized"], normalized, t["normalized"].dtype))
+    ok &= errors["mean"] <= 1e-5 and errors["rstd"] <= 1e-5
+    ok &= errors["normalized"] <= (1e-5 if t["normalized"].dtype == torch.float32 else 0.0)
+    if w.backward:
+        gu, gy = t["grad_updated"].to(f64), t["grad_normalized"].to(f64)
+        q = gy * weight
+        grad_x = gu + rstd[:, None] * (q - q.mean(dim=1, keepdim=True)
+                                       - xhat * (q * xhat).mean(dim=1, keepdim=True))
+        grad_branch = grad_x * (keep.to(f64) * scale if keep is not None else 1.0)
+        errors["grad_x"] = normwise(t["grad_x"], grad_x)
+        errors["grad_branch_ulp_excess"] = ulp_excess(t["grad_branch"], grad_branch,
+                                                      t["grad_branch"].dtype)
+        errors["grad_weight"] = normwise(t["grad_weight"], (gy * xhat).sum(dim=0))
+        errors["grad_bias"] = normwise(t["grad_bias"], gy.sum(dim=0))
+        ok &= errors["grad_x"] <= 1e-5 and errors["grad_branch_ulp_excess"] <= 0.0
+        ok &= errors["grad_weight"] <= 1e-4 and errors["grad_bias"] <= 1e-4
+    for name, value in errors.items():
+        if isinstance(value, float):
+            errors[name] = float(f"{value:.3e}")
+    errors["pass"] = bool(ok)
+    errors["checked"] = ("one step of the timed C-ABI path vs float64 dropout/add/LayerNorm "
+                         "on this GPU with the kernel's mask")
+    return errors
+
+
+def ceiling_library():
+    library = ctypes.CDLL(str(CEILING_LIBRARY))
+    pointer, size = ctypes.c_void_p, ctypes.c_int64
+    library.rln_ceiling_forward.argtypes = [pointer, pointer, ctypes.c_int, pointer, pointer,
+                                            ctypes.c_int, pointer, pointer, pointer, size, size,
+                                            pointer]
+    library.rln_ceiling_backward.argtypes = [pointer, pointer, ctypes.c_int, pointer, pointer,
+                                             pointer, pointer, pointer, pointer, ctypes.c_int,
+                                             size, size, pointer]
+    return library
+
+
+def ceiling_times(torch, runner: "Runner", library, launches: int = ROOFLINE_LAUNCHES) -> dict:
+    """The streaming ceiling of the runner's workload: csrc/rln_ceiling.hip's
+    forward- and backward-shaped passes over the runner's own buffers (same
+    rotated sets), timed like the op's kernels; microseconds per launch."""
+    w = runner.w
+
+    def forward(step):
+        t = runner.sets[step % len(runner.sets)]
+        status = library.rln_ceiling_forward(
+            t["x"].data_ptr(), t["branch"].data_ptr(), w.branch_bytes, t["updated"].data_ptr(),
+            t["normalized"].data_ptr(), w.normalized_bytes,
+            t["mask"].data_ptr() if w.dropping else None, t["mean"].data_ptr(),
+            t["rstd"].data_ptr(), w.rows, w.hidden, runner.handle)
+        if status:
+            raise RuntimeError(f"rln_ceiling_forward failed: {status}")
+
+    def backward(step):
+        t = runner.sets[step % len(runner.sets)]
+        status = library.rln_ceiling_backward(
+            t["grad_updated"].data_ptr(), t["grad_normalized"].data_ptr(), w.normalized_bytes,
+            t["updated"].data_ptr(), t["mask"].data_ptr() if w.dropping else None,
+            t["mean"].data_ptr(), t["rstd"].data_ptr(), t["grad_x"].data_ptr(),
+            t["grad_branch"].data_ptr(), w.branch_bytes, w.rows, w.hidden, runner.handle)
+        if status:
+            raise RuntimeError(f"rln_ceiling_backward failed: {status}")
+
+    for index in range(2 * len(runner.sets)):
+        forward(index)
+        if w.backward:
+            backward(index)
+    result = {"fwd": round(runner.timed(forward, launches) * 1e3, 3)}
+    if w.backward:
+        result["bwd"] = round(runner.timed(backward, launches) * 1e3, 3)
+
+        def step(index):
+            forward(index)
+            backward(index)
+
+        result["step"] = round(runner.timed(step, launches) * 1e3, 3)
+    result["kind"] = ("one-pass non-temporal streaming kernels with the op's exact streams "
+                      f"(csrc/rln_ceiling.hip), {launches} launches back to back, "
+                      f"{len(runner.sets)} rotated sets")
+    return result
 
 
 def percentiles_us(batches_ms) -> dict:
@@ -726,6 +1002,8 @@ def result_line(torch, workload: Workload, timing: dict, steps: int, warmup: int
             "frac": round(dominant_gbps / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
             "algorithmic_bytes_per_launch": dominant_bytes,
+            "avg_us_per_launch": round(dominant_ms * 1e3, 3),
+            "launches": timing["launches"],
         },
         "cpu_baseline": None,
         "device": torch.cuda.get_device_name(0),
@@ -755,6 +1033,8 @@ def main() -> int:
         print(f"bench.py: unknown --config {unknown}; the configurations are {names}",
               file=sys.stderr)
         return 2
+    if args.traffic_summary:
+        return traffic_summary(*args.traffic_summary)
     import torch
 
     from gfx1010_kernels import _cabi, residual_layer_norm_status
@@ -765,9 +1045,7 @@ def main() -> int:
     library = _cabi.library()
     stream = torch.cuda.Stream()
 
-    traffic = None
-    if TRAFFIC_FILE.exists():
-        traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+    traffic, traffic_note = load_traffic()
 
     if args.calibrate_copy_mib:
         with torch.cuda.stream(stream):
@@ -781,17 +1059,39 @@ def main() -> int:
 
     if args.config:
         chosen = [workload for workload in sweep_workloads() if workload.name in args.config]
-        run_sweep(torch, library, _cabi, stream, args, chosen)
+        if args.ceiling:
+            run_ceilings(torch, library, _cabi, stream, args, chosen)
+        else:
+            run_sweep(torch, library, _cabi, stream, args, chosen)
         return 0
 
     with torch.cuda.stream(stream):
         runner = Runner(torch, library, _cabi, C1, args.sets, stream)
+        parity = parity_self_check(torch, runner)
+        print(f"[bench] C1 parity self-check: {parity}", flush=True)
+        if not parity["pass"]:
+            print("bench.py: the timed path misses the parity bars; not timing it",
+                  file=sys.stderr)
+            return 1
         timing = runner.measure(args.warmup, args.steps)
+        ceiling = None if args.quick else ceiling_times(torch, runner, ceiling_library())
         del runner
         print(f"[bench] C1: step {timing['step_ms'] * 1e3:.2f} us, forward "
               f"{timing['forward_ms'] * 1e3:.2f} us, backward {timing['backward_ms'] * 1e3:.2f} us, "
               f"cold step {timing['cold_ms'] * 1e3:.2f} us", flush=True)
     result = result_line(torch, C1, timing, args.steps, args.warmup, args.sets, traffic)
+    result["roofline"]["traffic_note"] = traffic_note
+    result["parity"] = parity
+    if args.quick:
+        print(json.dumps(result), flush=True)
+        return 0
+    result["ceiling_us"] = {
+        **ceiling,
+        "op_fwd": round(timing["forward_ms"] * 1e3, 3),
+        "op_bwd": round(timing["backward_ms"] * 1e3, 3),
+        "op_step": round(timing["step_ms"] * 1e3, 3),
+        "op_over_ceiling_step": round(timing["step_ms"] * 1e3 / ceiling["step"], 4),
+    }
     result["copy_ceiling"] = copy_ceiling(torch, stream)
     result["public_api"] = public_api_steps(torch, C1, stream)
     # The reference's own published metric (speedup over its PyTorch
@@ -822,7 +1122,34 @@ def main() -> int:
 
     if args.sweep:
         run_sweep(torch, library, _cabi, stream, args, sweep_workloads())
+    if args.ceiling:
+        run_ceilings(torch, library, _cabi, stream, args, [C1, *sweep_workloads()])
     return 0
+
+
+def run_ceilings(torch, library, cabi, stream, args, workloads) -> None:
+    """One line per workload: the op's kernels and the streaming-ceiling
+    kernels over the same buffers, microseconds per launch."""
+    ceiling = ceiling_library()
+    for workload in workloads:
+        torch.cuda.empty_cache()
+        large = workload.rows * workload.hidden >= (1 << 26)
+        launches = 40 if large else ROOFLINE_LAUNCHES
+        with torch.cuda.stream(stream):
+            runner = Runner(torch, library, cabi, workload, 2 if large else args.sets, stream)
+            timing = runner.measure(min(args.warmup, 10), max(args.steps // 10, 20) if large
+                                    else args.steps, launches)
+            limit = ceiling_times(torch, runner, ceiling, launches)
+            del runner
+        line = {"kind": "ceiling", "workload": workload.describe(),
+                "op_us": {"fwd": round(timing["forward_ms"] * 1e3, 3)}, "ceiling_us": limit}
+        if workload.backward:
+            line["op_us"].update(bwd=round(timing["backward_ms"] * 1e3, 3),
+                                 step=round(timing["step_ms"] * 1e3, 3))
+        for key in ("fwd", "bwd", "step"):
+            if key in line["op_us"]:
+                line[f"op_over_ceiling_{key}"] = round(line["op_us"][key] / limit[key], 4)
+        print(json.dumps(line), flush=True)
 
 
 def run_sweep(torch, library, cabi, stream, args, workloads) -> None:
@@ -834,10 +1161,13 @@ def run_sweep(torch, library, cabi, stream, args, workloads) -> None:
         steps = max(args.steps // 10, 20) if large else args.steps
         with torch.cuda.stream(stream):
             runner = Runner(torch, library, cabi, workload, sets, stream)
+            parity = parity_self_check(torch, runner)
             timing = runner.measure(min(args.warmup, 10) if large else args.warmup, steps)
             del runner
+        torch.cuda.empty_cache()
         line = result_line(torch, workload, timing, steps, args.warmup, sets, None)
         line["sweep"] = True
+        line["parity"] = parity
         if not workload.backward and not args.no_cpu_baseline:
             # C0's forward-only CPU path is cheap to sample (~0.5 ms per step).
             line["cpu_baseline"] = cpu_baseline(torch, workload, min(args.cpu_seconds, 5.0))

@@ -5,7 +5,9 @@ Produces, inside ``gfx1010_kernels/``:
 * ``librln_gfx950.so`` - the HIP kernels for gfx950 and the C ABI declared in
   ``include/rln.h`` (hipcc, device code for gfx950 only);
 * ``_C<EXT_SUFFIX>`` - the PyTorch glue module (g++, host code only), linked
-  against ``librln_gfx950.so`` with an ``$ORIGIN`` run path.
+  against ``librln_gfx950.so`` with an ``$ORIGIN`` run path;
+* ``librln_ceiling_gfx950.so`` - the streaming-ceiling kernels bench.py times
+  beside the operator (``csrc/rln_ceiling.hip``; not part of the operator).
 
 Run ``python gfx1010-kernels_amd/build.py`` or call :func:`build`.
 """
@@ -29,6 +31,7 @@ ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = "gfx950"
 LIBRARY = PACKAGE / f"librln_{ARCH}.so"
 GLUE = PACKAGE / f"_C{sysconfig.get_config_var('EXT_SUFFIX')}"
+CEILING = PACKAGE / f"librln_ceiling_{ARCH}.so"
 
 # Device-code flags. Packed fp32 instructions are disabled (the compiler may
 # otherwise form v_pk_{add,mul,fma}_f32 from float code); FP contraction is
@@ -107,6 +110,17 @@ def build_library(jobs: int | None = None) -> Path:
     return LIBRARY
 
 
+def build_ceiling() -> Path:
+    """Compile the benchmark's streaming-ceiling kernels into their own library."""
+    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+    hipcc = str(ROCM / "bin" / "hipcc")
+    temporary = CEILING.with_name(CEILING.name + ".tmp")
+    _run([hipcc, *HIP_FLAGS, "-shared", str(CSRC / "rln_ceiling.hip"),
+          f"-Wl,-soname,{CEILING.name}", "-Wl,-z,defs", "-o", str(temporary)])
+    os.replace(temporary, CEILING)
+    return CEILING
+
+
 def _torch_paths() -> tuple[list[str], Path, bool]:
     import torch
     from torch.utils import cpp_extension
@@ -164,6 +178,7 @@ def build() -> tuple[Path, Path]:
     PACKAGE.mkdir(parents=True, exist_ok=True)
     library = build_library()
     glue = build_glue()
+    build_ceiling()
     return library, glue
 
 

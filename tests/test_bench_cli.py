@@ -23,7 +23,8 @@ def test_help_lists_the_measurement_modes():
     result = subprocess.run([sys.executable, str(BENCH), "--help"], capture_output=True,
                             text=True, timeout=120)
     assert result.returncode == 0
-    for flag in ("--steps", "--warmup", "--sweep", "--prenorm", "--reference-table", "--config"):
+    for flag in ("--steps", "--warmup", "--sweep", "--prenorm", "--reference-table", "--config",
+                 "--ceiling", "--quick", "--traffic-summary"):
         assert flag in result.stdout
 
 
@@ -56,3 +57,68 @@ def test_kernel_names_follow_the_library_backward_shapes():
         blocks = _cabi.backward_workspace_bytes(rows, hidden, True) // (2 * hidden * 4)
         parts = bench.wide_parts(hidden, "rln_backward_kernel")
         assert blocks == -(-rows // (8 // parts)), hidden
+
+
+def _bench_module():
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("bench_under_test", BENCH)
+    bench = importlib.util.module_from_spec(spec)
+    sys.modules["bench_under_test"] = bench
+    spec.loader.exec_module(bench)
+    return bench
+
+
+def test_mask_decoding_matches_the_oracle_layout():
+    """The parity self-check decodes the kernel's mask words on the device with
+    bit c % 32 of word r * H / 32 + c / 32; it must agree with the oracle's
+    decoder (pinned against the reference's layout in test_oracle.py)."""
+    import numpy as np
+    import torch
+
+    from oracle import rln_oracle as oracle
+
+    bench = _bench_module()
+    rows, hidden = 5, 96
+    words = np.random.default_rng(3).integers(0, 2 ** 32, rows * hidden // 32, dtype=np.uint64)
+    words = words.astype(np.uint32)
+    keep = bench.decode_mask(torch, torch.from_numpy(words.view(np.int32)), rows, hidden)
+    assert np.array_equal(keep.numpy(), oracle.decode_mask(words, rows, hidden).astype(bool))
+
+
+def test_traffic_summary_scales_counters_and_stamps_the_sources(tmp_path, monkeypatch):
+    """--traffic-summary turns two rocprofv3 --pmc csv directories into the
+    traffic record: each counter scaled by its value for the 256 MiB
+    calibration copy; the record carries the kernel-source digest, and a record
+    with another digest is reported stale instead of used."""
+    import json
+
+    bench = _bench_module()
+    backward = bench.kernel_name("rln_backward_kernel", bench.C1)
+    forward = bench.kernel_name("rln_forward_kernel", bench.C1)
+    rows = {"FETCH_SIZE": {"__amd_rocclr_copyBuffer": 131072.0, backward: 37000.0,
+                           forward: 18500.0},
+            "WRITE_SIZE": {"__amd_rocclr_copyBuffer": 262144.0, backward: 38000.0,
+                           forward: 50000.0}}
+    for counter, values in rows.items():
+        directory = tmp_path / counter / "host"
+        directory.mkdir(parents=True)
+        lines = ["Kernel_Name,Counter_Name,Counter_Value"]
+        for name, value in values.items():
+            for jitter in (-1.0, 1.0):
+                lines.append(f'"{name}(float const*)",{counter},{value + jitter}')
+        (directory / "1_counter_collection.csv").write_text("\n".join(lines) + "\n")
+    target = tmp_path / "traffic.json"
+    monkeypatch.setattr(bench, "TRAFFIC_FILE", target)
+    assert bench.traffic_summary(str(tmp_path / "FETCH_SIZE"), str(tmp_path / "WRITE_SIZE")) == 0
+    record = json.loads(target.read_text())
+    assert record["fetch_scale"] == 2.0 and record["write_scale"] == 1.0
+    assert record["hbm_bytes_per_launch"] == 1024 * (37000 * 2 + 38000)
+    assert record["forward_hbm_bytes_per_launch"] == 1024 * (18500 * 2 + 50000)
+    assert record["sources_digest"] == bench.kernel_sources_digest()
+    traffic, note = bench.load_traffic()
+    assert traffic == record["hbm_bytes_per_launch"] and "commit" in note
+    record["sources_digest"] = "0" * 16
+    target.write_text(json.dumps(record))
+    traffic, note = bench.load_traffic()
+    assert traffic is None and note.startswith("stale")
