@@ -11,9 +11,40 @@ Tolerances (written here once, used by every parity test):
   of that type at the fp64 oracle value, plus 1e-5 of the largest magnitude
   (the kernel rounds its fp32 result once);
 * ``grad_weight`` / ``grad_bias``: normwise relative error <= 1e-4.
+
+Golden fixtures (``conditioned_bounds``): per element, a bound from fp32
+error propagation through the two-pass LayerNorm, with u = 2^-24 (fp32 unit
+roundoff), n = ceil(log2 H) + 4 (additions along one row reduction), R the
+rows, and kappa_r = 1 + |mean_r| * rstd_r the row's conditioning (large for
+nearly-constant rows, whose fp32 mean carries an error of order u * |mean|):
+
+* mean_r: 2 n u max_i |u_ri|;  rstd_r: 4 n u kappa_r rstd_r;
+* normalized: 4 n u kappa_r max|w| (1 + |xhat_ri|);
+* grad_x: 8 n u kappa_r rstd_r max_i|q_ri| (1 + max_i|xhat_ri|) (1 + |xhat_ri|)
+  + 2 u |grad_updated_ri|, with q = grad_normalized * w (grad_branch: the same
+  times keep * scale, plus one ulp of its type);
+* grad_weight_c: sum_r |gy_rc| 2 n u kappa_r (1 + |xhat_rc|)
+  + 2 (ceil(log2 R) + 4) u sum_r |gy_rc xhat_rc|; grad_bias_c: 2 (ceil(log2 R)
+  + 4) u sum_r |gy_rc|.
+
+A float32 two-pass evaluation meets these with margin on every fixture; a
+one-pass variance, or a gradient without its xhat * mean(q * xhat) term,
+exceeds them (tests/test_parity_checker.py). For well-conditioned rows they
+are as tight as the 1e-5 normwise bar.
+
+Full-size tensors (``check_full_tensor``): the whole dropout mask against the
+C oracle (drawn in row chunks on a thread pool), ``updated`` on every row
+bitwise against its fp32 recomputation from that mask on the device, and
+``normalized``, ``mean``, ``rstd``, ``grad_x``, ``grad_branch`` on every row
+against a float64 LayerNorm and its gradient computed with torch on the
+device, at the bars above (normwise over the whole tensor).
 """
 
 from __future__ import annotations
+
+import math
+import os
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 import torch
@@ -212,3 +243,162 @@ def check_backward(gradients, grad_updated, grad_normalized, updated, weight, ep
         assert_normwise(host(grad_bias), expected["grad_bias"], TOL_PARAMETER_GRAD,
                         f"{what} grad_bias")
     return expected
+
+
+def oracle_mask_words_parallel(rows, hidden, seed, offset, threshold, threads=128, chunk=8192):
+    """The oracle's mask words of a whole [rows, hidden] tensor, drawn in row
+    chunks on a thread pool (the C oracle releases the GIL)."""
+    workers = min(16, os.cpu_count() or 1)
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        parts = pool.map(
+            lambda first: oracle_mask_rows(first, min(chunk, rows - first), hidden, seed,
+                                           offset, threshold, threads),
+            range(0, rows, chunk))
+        return np.concatenate(list(parts))
+
+
+def device_keep(words, first_row, rows, hidden):
+    """Keep flags of rows [first_row, first_row + rows) from int32 mask words on
+    the device (bit c % 32 of word r * hidden / 32 + c / 32)."""
+    per_row = hidden // 32
+    block = words[first_row * per_row:(first_row + rows) * per_row]
+    shifts = torch.arange(32, device=words.device, dtype=torch.int32)
+    return ((block.view(rows, per_row, 1) >> shifts) & 1).view(rows, hidden).bool()
+
+
+def _ulp_bound(expected, dtype):
+    """One ulp of `dtype` (fp16 / bf16) at |expected|, as a float64 tensor."""
+    bits, floor = (10, -14) if dtype == torch.float16 else (7, -126)
+    exponent = torch.floor(torch.log2(expected.abs().clamp_min(2.0 ** floor)))
+    return torch.exp2(exponent - bits)
+
+
+class _Normwise:
+    """Running max|actual - expected| and max|expected| over row chunks; for a
+    half-precision tensor also the running max of |actual - expected| - ulp."""
+
+    def __init__(self):
+        self.error = 0.0
+        self.scale = 0.0
+        self.excess = -float("inf")
+
+    def add(self, actual, expected):
+        difference = (actual.to(torch.float64) - expected).abs()
+        self.error = max(self.error, difference.max().item())
+        self.scale = max(self.scale, expected.abs().max().item())
+        if actual.dtype in (torch.float16, torch.bfloat16):
+            self.excess = max(self.excess,
+                              (difference - _ulp_bound(expected, actual.dtype)).max().item())
+
+    def check(self, tolerance, what, dtype=torch.float32):
+        if dtype in (torch.float16, torch.bfloat16):
+            bound = 1e-5 * self.scale
+            assert self.excess <= bound, (
+                f"{what}: {KIND[dtype]} error exceeds one ulp by {self.excess:.3e} "
+                f"(allowed {bound:.3e})")
+        else:
+            error = self.error / max(self.scale, 1e-30)
+            assert error <= tolerance, f"{what}: normwise error {error:.3e} > {tolerance:.1e}"
+
+
+def check_full_tensor(inputs, grads, outputs, gradients, dropout_p, eps, seed, offset,
+                      threads=128, chunk=16384, what=""):
+    """Every row of a full-size forward + backward against the oracle's mask and a
+    float64 recomputation on the device (bars in the module docstring).
+    `inputs` = (x, branch, weight, bias) [rows, hidden] on the device; `grads` =
+    (grad_updated, grad_normalized); `outputs` = (updated, normalized, mean, rstd,
+    mask); `gradients` = (grad_x, grad_branch, ...)."""
+    x, branch, weight, bias = inputs
+    rows, hidden = x.shape
+    active, scale, threshold = oracle.dropout_constants(dropout_p, True)
+    words = None
+    if active:
+        expected_words = oracle_mask_words_parallel(rows, hidden, seed, offset, threshold,
+                                                    threads)
+        assert_bitwise(host(outputs[4]).view(np.uint32), expected_words, f"{what} mask")
+        words = torch.from_numpy(expected_words.view(np.int32)).to(x.device)
+    f64 = torch.float64
+    weight64, bias64 = weight.to(f64), bias.to(f64)
+    checks = {name: _Normwise() for name in ("normalized", "mean", "rstd", "grad_x",
+                                             "grad_branch")}
+    for start in range(0, rows, chunk):
+        stop = min(rows, start + chunk)
+        count = stop - start
+        branch_rows = branch[start:stop].float()
+        keep = None
+        if words is not None:
+            keep = device_keep(words, start, count, hidden)
+            branch_rows = ((branch_rows * keep.float()) * float(scale)).to(branch.dtype).float()
+        updated = x[start:stop] + branch_rows
+        same = torch.equal(updated.view(torch.int32), outputs[0][start:stop].view(torch.int32))
+        assert same, f"{what} updated differs bitwise in rows {start}..{stop - 1}"
+        u = updated.to(f64)
+        mean = u.mean(dim=1, keepdim=True)
+        centred = u - mean
+        rstd = 1.0 / torch.sqrt((centred * centred).mean(dim=1, keepdim=True) + eps)
+        xhat = centred * rstd
+        checks["normalized"].add(outputs[1][start:stop], xhat * weight64 + bias64)
+        checks["mean"].add(outputs[2][start:stop], mean[:, 0])
+        checks["rstd"].add(outputs[3][start:stop], rstd[:, 0])
+        if gradients is None:
+            continue
+        grad_updated, grad_normalized = grads
+        q = grad_normalized[start:stop].to(f64) * weight64
+        grad_x = rstd * (q - q.mean(dim=1, keepdim=True)
+                         - xhat * (q * xhat).mean(dim=1, keepdim=True))
+        if grad_updated is not None:
+            grad_x = grad_x + grad_updated[start:stop].to(f64)
+        grad_branch = grad_x if keep is None else grad_x * (keep.to(f64) * float(scale))
+        checks["grad_x"].add(gradients[0][start:stop], grad_x)
+        checks["grad_branch"].add(gradients[1][start:stop], grad_branch)
+    checks["normalized"].check(TOL_FORWARD, f"{what} normalized", outputs[1].dtype)
+    checks["mean"].check(TOL_FORWARD, f"{what} mean")
+    checks["rstd"].check(TOL_FORWARD, f"{what} rstd")
+    if gradients is not None:
+        checks["grad_x"].check(TOL_INPUT_GRAD, f"{what} grad_x")
+        checks["grad_branch"].check(TOL_INPUT_GRAD, f"{what} grad_branch", gradients[1].dtype)
+
+
+FP32_UNIT_ROUNDOFF = 2.0 ** -24
+
+
+def conditioned_bounds(updated, weight, eps, grad_updated=None, grad_normalized=None):
+    """Per-element fp32 error bounds (module docstring) for a fixture whose
+    fp32 `updated` is [R, H]; float64 numpy arrays keyed by output name."""
+    u = np.asarray(updated, dtype=np.float64)
+    rows, hidden = u.shape
+    w = np.asarray(weight, dtype=np.float64)
+    unit = FP32_UNIT_ROUNDOFF
+    n = math.ceil(math.log2(hidden)) + 4
+    n_rows = math.ceil(math.log2(max(rows, 2))) + 4
+    mean = u.mean(axis=1)
+    centred = u - mean[:, None]
+    rstd = 1.0 / np.sqrt((centred * centred).mean(axis=1) + float(eps))
+    xhat = centred * rstd[:, None]
+    kappa = 1.0 + np.abs(mean) * rstd
+    bounds = {
+        "mean": 2 * n * unit * np.abs(u).max(axis=1),
+        "rstd": 4 * n * unit * kappa * rstd,
+        "normalized": 4 * n * unit * kappa[:, None] * np.abs(w).max() * (1 + np.abs(xhat)),
+        "kappa": kappa,
+    }
+    if grad_updated is None and grad_normalized is None:
+        return bounds
+    gu = np.zeros_like(u) if grad_updated is None else np.asarray(grad_updated, np.float64)
+    gy = np.zeros_like(u) if grad_normalized is None else np.asarray(grad_normalized, np.float64)
+    q = gy * w
+    bounds["grad_x"] = (8 * n * unit * (kappa * rstd * np.abs(q).max(axis=1)
+                                        * (1 + np.abs(xhat).max(axis=1)))[:, None]
+                        * (1 + np.abs(xhat)) + 2 * unit * np.abs(gu))
+    bounds["grad_weight"] = ((np.abs(gy) * 2 * n * unit * kappa[:, None] * (1 + np.abs(xhat)))
+                             .sum(axis=0) + 2 * n_rows * unit * np.abs(gy * xhat).sum(axis=0))
+    bounds["grad_bias"] = 2 * n_rows * unit * np.abs(gy).sum(axis=0)
+    return bounds
+
+
+def assert_within(actual, expected, bound, what=""):
+    """|actual - expected| <= bound elementwise (arrays broadcast)."""
+    excess = np.abs(np.asarray(actual, np.float64) - np.asarray(expected, np.float64)) / bound
+    worst = float(np.max(excess)) if excess.size else 0.0
+    assert worst <= 1.0, f"{what}: error reaches {worst:.3f} of the fp32 conditioned bound"
+    return worst

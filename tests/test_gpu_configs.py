@@ -1,11 +1,13 @@
 """The BASELINE.json configurations at their full sizes.
 
-C0, C1, the C4 tail and the C4 single row run the complete oracle. For the
-262 144-row configs (C2, C4 large) and C3, full fp64 host oracles would take
-minutes, so parity uses size-independent properties: every output of a sample
-of rows against the oracle (the op is row-local), the full dropout mask's keep
-ratio, the weight/bias gradients against an independent float64 reduction,
-and bitwise replay.
+C0, C1, the C4 tail and the C4 single row run the complete oracle. The
+262 144-row configs (C2 at every hidden size, C4 large), C3 and both sides of
+the 768-column backward switch are checked on every row
+(parity.check_full_tensor): the whole dropout mask bitwise against the C
+oracle, `updated` bitwise against its fp32 recomputation from that mask, and
+normalized, mean, rstd, grad_x and grad_branch against a float64 LayerNorm and
+its gradient on the device; the weight/bias gradients against a float64
+reduction over all rows; C3 also replays bitwise.
 """
 
 import contextlib
@@ -15,22 +17,17 @@ import pytest
 import torch
 
 from gfx1010_kernels import _C
-from oracle import rln_oracle as oracle
 from parity import (
-    KIND,
-    TOL_FORWARD,
-    TOL_INPUT_GRAD,
     TOL_PARAMETER_GRAD,
     assert_bitwise,
     assert_normwise,
-    assert_rounded_close,
     check_backward,
     check_forward,
+    check_full_tensor,
     generator_state,
     host,
     make_grads,
     make_inputs,
-    oracle_mask_rows,
 )
 
 pytestmark = pytest.mark.gpu
@@ -48,7 +45,7 @@ def deterministic_algorithms(enabled):
 
 
 def device_inputs(rows, hidden, branch_dtype, seed, branch_std=1.0, x_mean=0.0):
-    """Large seeded inputs generated on the device (copied back only for sampled rows)."""
+    """Large seeded inputs generated on the device (checked there, in float64)."""
     generator = torch.Generator(device="cuda").manual_seed(seed)
     x = torch.randn(rows, hidden, device="cuda", generator=generator) + x_mean
     branch = (torch.randn(rows, hidden, device="cuda", generator=generator) * branch_std).to(branch_dtype)
@@ -68,40 +65,6 @@ def raw_backward(grads, outputs, weight, dropout_p, branch_is_half):
 def keep_count(mask):
     table = torch.tensor([bin(i).count("1") for i in range(256)], device=mask.device)
     return int(table[mask.view(torch.uint8).long()].sum())
-
-
-def check_sampled_rows(inputs, grads, outputs, gradients, dropout_p, seed, offset, sample=24,
-                       threads=128):
-    x, branch, weight, bias = inputs
-    rows, hidden = x.shape
-    rng = np.random.default_rng(rows + hidden)
-    picked = np.unique(np.concatenate([[0, rows - 1], rng.choice(rows, sample, replace=False)]))
-    index = torch.from_numpy(picked).to("cuda")
-    active, scale, threshold = oracle.dropout_constants(dropout_p, True)
-    keep = None
-    if active:
-        words = np.concatenate([
-            oracle_mask_rows(int(r), 1, hidden, seed, offset, threshold, threads)
-            for r in picked])
-        gpu_words = host(outputs[4].view(rows, hidden // 32).index_select(0, index)).view(np.uint32)
-        assert_bitwise(gpu_words.ravel(), words, "sampled mask")
-        keep = oracle.decode_mask(words, len(picked), hidden)
-    take = lambda t: host(t.index_select(0, index))  # noqa: E731
-    expected = oracle.forward(take(x), take(branch), host(weight), host(bias), EPS, keep=keep,
-                              scale=scale, branch_type=KIND[branch.dtype])
-    assert_bitwise(take(outputs[0]), expected["updated"], "sampled updated")
-    assert_normwise(take(outputs[1]), expected["normalized"], TOL_FORWARD, "sampled normalized")
-    assert_normwise(host(outputs[2][index]), expected["mean"], TOL_FORWARD, "sampled mean")
-    assert_normwise(host(outputs[3][index]), expected["rstd"], TOL_FORWARD, "sampled rstd")
-    grad_expected = oracle.backward(take(grads[0]), take(grads[1]), expected["updated"],
-                                    host(weight), EPS, keep=keep, scale=scale)
-    assert_normwise(take(gradients[0]), grad_expected["grad_x"], TOL_INPUT_GRAD, "sampled grad_x")
-    grad_branch = take(gradients[1])
-    if gradients[1].dtype == torch.float32:
-        assert_normwise(grad_branch, grad_expected["grad_branch"], TOL_INPUT_GRAD, "sampled grad_branch")
-    else:
-        assert_rounded_close(grad_branch, grad_expected["grad_branch"], KIND[gradients[1].dtype],
-                             "sampled grad_branch")
 
 
 def check_parameter_gradients(updated, grad_normalized, gradients, chunk=16384):
@@ -148,7 +111,8 @@ def test_c2_hidden_sweep_at_262144_rows(hidden):
     seed, offset = generator_state()
     outputs = _C.residual_layer_norm_forward(*inputs, 0.15, EPS, True, 128)
     gradients = raw_backward(grads, outputs, inputs[2], 0.15, True)
-    check_sampled_rows(inputs, grads, outputs, gradients, 0.15, seed, offset)
+    check_full_tensor(inputs, grads, outputs, gradients, 0.15, EPS, seed, offset,
+                      what=f"C2 H={hidden}")
     check_parameter_gradients(outputs[0], grads[1], gradients)
     n = rows * hidden
     assert abs(keep_count(outputs[4]) - 0.85 * n) < 6 * np.sqrt(n * 0.15 * 0.85)
@@ -180,7 +144,8 @@ def test_768_backward_on_both_sides_of_its_three_wave_switch(rows, branch_dtype,
         again = backward()
     for first, second in zip(gradients, again):
         assert torch.equal(first, second)
-    check_sampled_rows(inputs, grads, outputs, gradients, 0.1, seed, offset)
+    check_full_tensor(inputs, grads, outputs, gradients, 0.1, EPS, seed, offset,
+                      what=f"768 x {rows}")
     check_parameter_gradients(outputs[0], grads[1], gradients)
     with deterministic_algorithms(False):
         atomic = backward()
@@ -202,7 +167,7 @@ def test_c3_deterministic_bitwise_replay_over_three_runs():
     for run in runs[1:]:
         for a, b in zip(runs[0], run):
             assert_bitwise(b, a, "C3 replay")
-    check_sampled_rows(inputs, grads, outputs, gradients, 0.15, seed, offset)
+    check_full_tensor(inputs, grads, outputs, gradients, 0.15, EPS, seed, offset, what="C3")
     check_parameter_gradients(outputs[0], grads[1], gradients)
 
 
@@ -242,7 +207,8 @@ def test_c4_large_steady_state_shape():
     seed, offset = generator_state()
     outputs = _C.residual_layer_norm_forward(*inputs, 0.1, EPS, True, 128)
     gradients = raw_backward(grads, outputs, inputs[2], 0.1, True)
-    check_sampled_rows(inputs, grads, outputs, gradients, 0.1, seed, offset)
+    check_full_tensor(inputs, grads, outputs, gradients, 0.1, EPS, seed, offset,
+                      what="C4 large")
     check_parameter_gradients(outputs[0], grads[1], gradients)
     n = rows * hidden
     assert abs(keep_count(outputs[4]) - 0.9 * n) < 6 * np.sqrt(n * 0.1 * 0.9)

@@ -2,21 +2,17 @@
 
 One call over more than 2^31 elements per tensor (8.6 GB fp32 each, ~60 GB in
 all, well inside MI355X's 288 GB), for a specialized and a multi-wave row
-shape: sampled rows, the last one included, match the oracle (mask bit for
-bit), and the weight/bias gradients match a float64 reduction over all rows.
+shape: every row matches the oracle (parity.check_full_tensor: the whole
+mask bit for bit, `updated` bitwise, the rest against float64 on the device),
+and the weight/bias gradients match a float64 reduction over all rows.
 """
 
 import pytest
 import torch
 
 from gfx1010_kernels import _C
-from parity import generator_state
-from test_gpu_configs import (
-    check_parameter_gradients,
-    check_sampled_rows,
-    device_inputs,
-    raw_backward,
-)
+from parity import check_full_tensor, generator_state
+from test_gpu_configs import check_parameter_gradients, device_inputs, raw_backward
 
 pytestmark = pytest.mark.gpu
 EPS = 1e-5
@@ -31,5 +27,6 @@ def test_more_than_2_31_elements(hidden):
     outputs = _C.residual_layer_norm_forward(*inputs, 0.1, EPS, True, 128)
     gradients = raw_backward(grads, outputs, inputs[2], 0.1, True)
     torch.cuda.synchronize()
-    check_sampled_rows(inputs, grads, outputs, gradients, 0.1, seed, offset)
+    check_full_tensor(inputs, grads, outputs, gradients, 0.1, EPS, seed, offset,
+                      chunk=(1 << 24) // hidden, what=f"2^31+ H={hidden}")
     check_parameter_gradients(outputs[0], grads[1], gradients)

@@ -7,16 +7,19 @@ one-wave rows (forward and backward), from 2^26 elements for the forward of
 multi-wave rows (hidden > 1024) except 8 waves of 4 slots. Every output of a row
 except the weight/bias sums depends on that row alone, so the first rows of
 a paced launch must equal, bit for bit, a look-ahead launch over just those
-rows; the sums of the paced launch are checked against a float64 reduction
-and the element-access (misaligned) path against the aligned one. Calls go
-through the C ABI with explicit Philox seeds and offsets.
+rows; every row of the paced launch is also checked against the oracle
+(parity.check_full_tensor: the whole mask, `updated` bitwise, the rest
+against float64), its sums against a float64 reduction, and the
+element-access (misaligned) path against the aligned one. Calls go through
+the C ABI with explicit Philox seeds and offsets (the library's own dropout
+layout).
 """
 
 import pytest
 import torch
 
 from gfx1010_kernels import _cabi
-from parity import TOL_PARAMETER_GRAD, assert_bitwise, assert_normwise, host
+from parity import TOL_PARAMETER_GRAD, assert_bitwise, assert_normwise, check_full_tensor, host
 
 pytestmark = pytest.mark.gpu
 EPS = 1e-5
@@ -128,6 +131,10 @@ def test_paced_rows_equal_look_ahead_rows(hidden, branch_dtype, normalized_dtype
     assert_same_bits(paced["mask"][:words], look_ahead["mask"], "mask")
     check_parameter_sums(paced, case[5], paced_rows)
     check_parameter_sums(look_ahead, case[5], prefix)
+    check_full_tensor(case[:4], case[4:], [paced[name] for name in ("updated", "normalized",
+                                                                    "mean", "rstd", "mask")],
+                      [paced["grad_x"], paced["grad_branch"]], 0.1, EPS, SEED, OFFSET,
+                      threads=0, what=f"paced H={hidden}")
 
 
 @pytest.mark.parametrize("deterministic", [False, True], ids=["atomic", "deterministic"])
