@@ -5,6 +5,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "rln_device.h"
@@ -294,7 +295,53 @@ size_t rln_backward_workspace_bytes(int64_t rows, int64_t hidden, int determinis
         * sizeof(float);
 }
 
-int rln_backward(
+}  // extern "C"
+
+// Scratch of rln_backward_noalloc: the deterministic weight/bias partials,
+// RLN_NOALLOC_SCRATCH_BYTES on every device the library runs on, held until
+// the process ends. Host code never passes `scratch` itself to a kernel (on
+// the host the name stands for a host-side stand-in, not the device array):
+// it uses the address hipGetSymbolAddress returns for the current device.
+static __device__ __align__(256) float scratch[RLN_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+namespace rln {
+namespace {
+
+// Argument checks shared by rln_backward and rln_backward_noalloc (the C ABI
+// names them in include/rln.h); RLN_OK or the failing code.
+int check_backward(const float* updated, const float* weight, const float* mean,
+                   const float* rstd, float* grad_x, void* grad_branch, int branch_dtype,
+                   int grad_normalized_dtype, const float* grad_weight, const float* grad_bias,
+                   const uint32_t* dropout_mask, int64_t rows, int64_t hidden, double dropout_p,
+                   int training) {
+    int status = check_common(rows, hidden, branch_dtype);
+    if (status != RLN_OK) {
+        return status;
+    }
+    if (!updated || !weight || !mean || !rstd || !grad_x || !grad_branch) {
+        return fail(RLN_ERR_INVALID, "backward tensors must not be null");
+    }
+    if (!valid_dtype(grad_normalized_dtype)) {
+        return fail(RLN_ERR_INVALID, "grad_normalized must use float16, bfloat16 or float32");
+    }
+    if ((grad_weight == nullptr) != (grad_bias == nullptr)) {
+        return fail(RLN_ERR_INVALID, "grad_weight and grad_bias must both be given or both be null");
+    }
+    DropoutConstants drop{};
+    status = dropout_constants(dropout_p, training, &drop);
+    if (status != RLN_OK) {
+        return status;
+    }
+    if (drop.active && !dropout_mask) {
+        return fail(RLN_ERR_INVALID, "dropout_mask must not be null when dropout is active");
+    }
+    return RLN_OK;
+}
+
+// The backward launch sequence behind both backward entry points, after
+// check_backward passed: workspace = the per-block weight/bias partials of
+// the deterministic reduction (or NULL when none are needed).
+int backward_launches(
     const float* grad_updated,
     const void* grad_normalized,
     int grad_normalized_dtype,
@@ -317,28 +364,9 @@ int rln_backward(
     void* workspace,
     size_t workspace_bytes,
     void* stream) {
-    rln::t_last_error.clear();
-    int status = check_common(rows, hidden, branch_dtype);
-    if (status != RLN_OK) {
-        return status;
-    }
-    if (!updated || !weight || !mean || !rstd || !grad_x || !grad_branch) {
-        return fail(RLN_ERR_INVALID, "backward tensors must not be null");
-    }
-    if (!valid_dtype(grad_normalized_dtype)) {
-        return fail(RLN_ERR_INVALID, "grad_normalized must use float16, bfloat16 or float32");
-    }
-    if ((grad_weight == nullptr) != (grad_bias == nullptr)) {
-        return fail(RLN_ERR_INVALID, "grad_weight and grad_bias must both be given or both be null");
-    }
+    int status = RLN_OK;
     DropoutConstants drop{};
-    status = dropout_constants(dropout_p, training, &drop);
-    if (status != RLN_OK) {
-        return status;
-    }
-    if (drop.active && !dropout_mask) {
-        return fail(RLN_ERR_INVALID, "dropout_mask must not be null when dropout is active");
-    }
+    dropout_constants(dropout_p, training, &drop);
     const bool parameters = grad_weight != nullptr && grad_normalized != nullptr;
     const bool partials = parameters && uses_partials(deterministic);
     const size_t needed = partials ? rln_backward_workspace_bytes(rows, hidden, deterministic) : 0;
@@ -405,6 +433,128 @@ int rln_backward(
         status = check_launch("rln_parameter_reduce_kernel");
     }
     return status;
+}
+
+// rln_backward_noalloc's per-device addresses of `scratch` (defined at file
+// scope below), looked up once per device with that device current.
+constexpr int kNoAllocMaxDevices = 64;
+std::once_flag g_scratch_once[kNoAllocMaxDevices];
+void* g_scratch_address[kNoAllocMaxDevices];
+hipError_t g_scratch_status[kNoAllocMaxDevices];
+
+// This device's address of `scratch` (the device is current), or NULL with
+// the failure recorded.
+void* device_scratch() {
+    int device = -1;
+    const hipError_t current = hipGetDevice(&device);
+    if (current != hipSuccess || device < 0 || device >= kNoAllocMaxDevices) {
+        fail(RLN_ERR_HIP, "rln_backward_noalloc: no usable current device (%s, device %d)",
+             hipGetErrorString(current), device);
+        return nullptr;
+    }
+    std::call_once(g_scratch_once[device], [device] {
+        void* address = nullptr;
+        g_scratch_status[device] = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+        g_scratch_address[device] = g_scratch_status[device] == hipSuccess ? address : nullptr;
+    });
+    if (g_scratch_address[device] == nullptr) {
+        fail(RLN_ERR_HIP, "rln_backward_noalloc: hipGetSymbolAddress(scratch) failed on device "
+             "%d: %s", device, hipGetErrorString(g_scratch_status[device]));
+    }
+    return g_scratch_address[device];
+}
+
+}  // namespace
+}  // namespace rln
+
+extern "C" {
+
+int rln_backward(
+    const float* grad_updated,
+    const void* grad_normalized,
+    int grad_normalized_dtype,
+    const float* updated,
+    const float* weight,
+    const float* mean,
+    const float* rstd,
+    const uint32_t* dropout_mask,
+    float* grad_x,
+    void* grad_branch,
+    int branch_dtype,
+    float* grad_weight,
+    float* grad_bias,
+    int64_t rows,
+    int64_t hidden,
+    double dropout_p,
+    int training,
+    int deterministic,
+    int accumulate_parameters,
+    void* workspace,
+    size_t workspace_bytes,
+    void* stream) {
+    rln::t_last_error.clear();
+    const int status = check_backward(updated, weight, mean, rstd, grad_x, grad_branch,
+                                      branch_dtype, grad_normalized_dtype, grad_weight,
+                                      grad_bias, dropout_mask, rows, hidden, dropout_p, training);
+    if (status != RLN_OK) {
+        return status;
+    }
+    return backward_launches(grad_updated, grad_normalized, grad_normalized_dtype, updated, weight,
+                             mean, rstd, dropout_mask, grad_x, grad_branch, branch_dtype,
+                             grad_weight, grad_bias, rows, hidden, dropout_p, training,
+                             deterministic, accumulate_parameters, workspace, workspace_bytes,
+                             stream);
+}
+
+int rln_backward_noalloc(
+    const float* grad_updated,
+    const void* grad_normalized,
+    int grad_normalized_dtype,
+    const float* updated,
+    const float* weight,
+    const float* mean,
+    const float* rstd,
+    const uint32_t* dropout_mask,
+    float* grad_x,
+    void* grad_branch,
+    int branch_dtype,
+    float* grad_weight,
+    float* grad_bias,
+    int64_t rows,
+    int64_t hidden,
+    double dropout_p,
+    int training,
+    int deterministic,
+    int accumulate_parameters,
+    void* stream) {
+    rln::t_last_error.clear();
+    const int status = check_backward(updated, weight, mean, rstd, grad_x, grad_branch,
+                                      branch_dtype, grad_normalized_dtype, grad_weight,
+                                      grad_bias, dropout_mask, rows, hidden, dropout_p, training);
+    if (status != RLN_OK) {
+        return status;
+    }
+    const bool parameters = grad_weight != nullptr && grad_normalized != nullptr;
+    const size_t needed = parameters ? rln_backward_workspace_bytes(rows, hidden, deterministic) : 0;
+    if (needed > RLN_NOALLOC_SCRATCH_BYTES) {
+        return fail(RLN_ERR_INVALID,
+                    "rln_backward_noalloc: the weight/bias partials of %lld rows x %lld need "
+                    "%zu bytes, above its %zu-byte scratch (use rln_backward with a workspace)",
+                    static_cast<long long>(rows), static_cast<long long>(hidden), needed,
+                    static_cast<size_t>(RLN_NOALLOC_SCRATCH_BYTES));
+    }
+    void* workspace = nullptr;
+    if (needed > 0) {
+        workspace = device_scratch();
+        if (workspace == nullptr) {
+            return RLN_ERR_HIP;
+        }
+    }
+    return backward_launches(grad_updated, grad_normalized, grad_normalized_dtype, updated, weight,
+                             mean, rstd, dropout_mask, grad_x, grad_branch, branch_dtype,
+                             grad_weight, grad_bias, rows, hidden, dropout_p, training,
+                             deterministic, accumulate_parameters, workspace,
+                             RLN_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 uint64_t rln_philox_increment(int64_t hidden, int64_t threads) {

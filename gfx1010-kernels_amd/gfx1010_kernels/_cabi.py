@@ -62,6 +62,11 @@ SIGNATURES = {
         [_P, _P, ctypes.c_int, _P, _P, _P, _P, _P, _P, _P, ctypes.c_int, _P, _P, _I64, _I64,
          ctypes.c_double, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P, ctypes.c_size_t, _P],
     ),
+    "rln_backward_noalloc": (
+        ctypes.c_int,
+        [_P, _P, ctypes.c_int, _P, _P, _P, _P, _P, _P, _P, ctypes.c_int, _P, _P, _I64, _I64,
+         ctypes.c_double, ctypes.c_int, ctypes.c_int, ctypes.c_int, _P],
+    ),
     "rln_backward_workspace_bytes": (ctypes.c_size_t, [_I64, _I64, ctypes.c_int]),
     "rln_philox_increment": (ctypes.c_uint64, [_I64, _I64]),
     "rln_mask_words": (_I64, [_I64, _I64]),
@@ -134,6 +139,27 @@ def backward(
             rstd, mask, grad_x, grad_branch, branch_dtype, grad_weight, grad_bias, rows,
             hidden, dropout_p, int(bool(training)), int(bool(deterministic)),
             int(bool(accumulate_parameters)), workspace, workspace_bytes, stream,
+        )
+    )
+
+
+# include/rln.h RLN_NOALLOC_SCRATCH_BYTES: rln_backward_noalloc's per-device scratch.
+NOALLOC_SCRATCH_BYTES = 4 << 20
+
+
+def backward_noalloc(
+    grad_updated, grad_normalized, updated, weight, mean, rstd, mask, grad_x,
+    grad_branch, branch_dtype, grad_weight, grad_bias, rows, hidden, dropout_p,
+    training, deterministic, stream=None, accumulate_parameters=False,
+    grad_normalized_dtype=RLN_DTYPE_F32,
+):
+    """Call ``rln_backward_noalloc`` (no workspace, nothing allocated); raises RlnError."""
+    _check(
+        library().rln_backward_noalloc(
+            grad_updated, grad_normalized, grad_normalized_dtype, updated, weight, mean,
+            rstd, mask, grad_x, grad_branch, branch_dtype, grad_weight, grad_bias, rows,
+            hidden, dropout_p, int(bool(training)), int(bool(deterministic)),
+            int(bool(accumulate_parameters)), stream,
         )
     )
 

@@ -25,7 +25,8 @@
  *    (csrc/residual_layer_norm_kernel.hip:500-511, :162-164).
  *  - `stream` is a hipStream_t (NULL = the legacy default stream). Work is
  *    enqueued asynchronously; nothing synchronizes the host.
- *  - No entry point allocates device memory.
+ *  - No entry point allocates device memory; rln_backward_noalloc also takes
+ *    no workspace (it keeps a static per-device scratch instead).
  *  - Return value: RLN_OK, or an RLN_ERR_* code with a message available
  *    from rln_last_error() (thread-local, valid until the next call on the
  *    same thread).
@@ -168,6 +169,48 @@ int rln_backward(
     int accumulate_parameters,
     void* workspace,
     size_t workspace_bytes,
+    void* stream);
+
+/* Scratch bytes rln_backward_noalloc keeps per device (see below). */
+#define RLN_NOALLOC_SCRATCH_BYTES (4u << 20)
+
+/*
+ * Backward that allocates nothing and takes no workspace. It has
+ * no counterpart in the reference: it is for callers that cannot allocate
+ * device memory or pass a workspace (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). Same arguments, checks and
+ * results as rln_backward without workspace / workspace_bytes: the
+ * deterministic weight/bias partials live in a library-owned static device
+ * array of RLN_NOALLOC_SCRATCH_BYTES on each device (held until the process
+ * ends; its address is looked up once per device on the first call). A call
+ * whose partials need more (rln_backward_workspace_bytes(rows, hidden, 1)
+ * above that, e.g. hidden above 2048 once the backward runs its full 256
+ * blocks) fails with RLN_ERR_INVALID before any GPU work. Every call on a
+ * device shares that device's scratch, and nothing in it needs clearing (each
+ * call overwrites what it reads): calls that overlap on one device (different
+ * streams, different host threads) race and must be ordered by the caller.
+ * Atomic mode uses no scratch.
+ */
+int rln_backward_noalloc(
+    const float* grad_updated,
+    const void* grad_normalized,
+    int grad_normalized_dtype,
+    const float* updated,
+    const float* weight,
+    const float* mean,
+    const float* rstd,
+    const uint32_t* dropout_mask,
+    float* grad_x,
+    void* grad_branch,
+    int branch_dtype,
+    float* grad_weight,
+    float* grad_bias,
+    int64_t rows,
+    int64_t hidden,
+    double dropout_p,
+    int training,
+    int deterministic,
+    int accumulate_parameters,
     void* stream);
 
 /* Workspace bytes rln_backward needs (0 in atomic mode): the per-block

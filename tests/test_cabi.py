@@ -178,3 +178,24 @@ def test_glue_module_imports_and_checks_device_first():
     with pytest.raises(RuntimeError, match="x must be a HIP tensor"):
         _C.residual_layer_norm(x, x, torch.ones(128), torch.zeros(128), 0.0, 1e-5, True, 128, 64, 64, 1)
     assert _C.target_arch() == "gfx950"
+
+
+def test_noalloc_backward_refuses_partials_above_its_scratch_before_any_gpu_work():
+    """rln_backward_noalloc checks its arguments and the size of the weight /
+    bias partials on the host, before any HIP call: a shape whose
+    deterministic partials exceed RLN_NOALLOC_SCRATCH_BYTES fails with
+    RLN_ERR_INVALID and says why; atomic mode needs no scratch at all."""
+    rows, hidden = 65536, 4096
+    needed = _cabi.backward_workspace_bytes(rows, hidden, True)
+    assert needed > _cabi.NOALLOC_SCRATCH_BYTES
+    assert _cabi.backward_workspace_bytes(rows, 2048, True) <= _cabi.NOALLOC_SCRATCH_BYTES
+    fake = 0x1000  # never dereferenced: the call fails before any GPU work
+    with pytest.raises(_cabi.RlnError) as caught:
+        _cabi.backward_noalloc(fake, fake, fake, fake, fake, fake, fake, fake, fake,
+                               _cabi.RLN_DTYPE_F16, fake, fake, rows, hidden, 0.1, True, True)
+    assert caught.value.status == _cabi.RLN_ERR_INVALID
+    assert f"need {needed} bytes" in str(caught.value) and "scratch" in str(caught.value)
+    with pytest.raises(_cabi.RlnError) as caught:
+        _cabi.backward_noalloc(fake, fake, None, fake, fake, fake, fake, fake, fake,
+                               _cabi.RLN_DTYPE_F16, fake, fake, rows, hidden, 0.1, True, True)
+    assert "backward tensors must not be null" in str(caught.value)
