@@ -44,7 +44,8 @@ Prints one JSON line:
                beside the best ratios the reference publishes for gfx1010
 
 The roofline kernel's average duration comes from a fixed 400 back-to-back
-launches, whatever ``--steps`` is. ``roofline.traffic`` is read from
+launches, whatever ``--steps`` is; those kernel timings run first, then the
+``--warmup`` untimed steps, then exactly ``--steps`` timed steps. ``roofline.traffic`` is read from
 profiles/rln_backward_c1_traffic.json only when that file's kernel-source
 digest matches the sources in this tree (else null, with ``traffic_note``);
 ``--traffic-summary FETCH_DIR WRITE_DIR`` writes that file from two
@@ -554,32 +555,50 @@ class Runner:
         return {"f32": self.cabi.RLN_DTYPE_F32, "f16": self.cabi.RLN_DTYPE_F16,
                 "bf16": self.cabi.RLN_DTYPE_BF16}[name]
 
+    def _launch_arguments(self):
+        """Per set, the C-ABI argument tuples of its forward and backward,
+        built once (ctypes-converted), so that a launch from the timing loops
+        costs the host as little as the C call itself: the forward's ~9 us at
+        C0 is shorter than building the arguments anew each time."""
+        w, cabi = self.w, self.cabi
+        p, i64, f64 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_double
+        self._philox = cabi.RlnPhilox(self.seed, 0, None, None, w.stream_threads)
+        philox = ctypes.byref(self._philox)
+        handle = p(self.handle)
+        workspace = self.workspace
+        self._forward_args, self._backward_args = [], []
+        for t in self.sets:
+            self._forward_args.append((
+                p(t["x"].data_ptr()), p(t["branch"].data_ptr()), self.code(w.branch),
+                p(self.weight.data_ptr()), p(self.bias.data_ptr()), p(t["updated"].data_ptr()),
+                p(t["normalized"].data_ptr()), self.code(w.normalized), p(t["mean"].data_ptr()),
+                p(t["rstd"].data_ptr()), p(t["mask"].data_ptr()), None, None, i64(w.rows),
+                i64(w.hidden), f64(w.dropout_p), f64(EPS), int(w.training), philox, handle))
+            if w.backward:
+                self._backward_args.append((
+                    p(t["grad_updated"].data_ptr()), p(t["grad_normalized"].data_ptr()),
+                    self.code(w.normalized), p(t["updated"].data_ptr()), p(self.weight.data_ptr()),
+                    p(t["mean"].data_ptr()), p(t["rstd"].data_ptr()), p(t["mask"].data_ptr()),
+                    p(t["grad_x"].data_ptr()), p(t["grad_branch"].data_ptr()), self.code(w.branch),
+                    p(t["grad_weight"].data_ptr()), p(t["grad_bias"].data_ptr()), i64(w.rows),
+                    i64(w.hidden), f64(w.dropout_p), int(w.training), int(w.deterministic), 1,
+                    p(workspace.data_ptr()) if workspace is not None else None,
+                    workspace.numel() if workspace is not None else 0, handle))
+
     def forward(self, step: int):
-        t, w = self.sets[step % len(self.sets)], self.w
-        philox = self.cabi.RlnPhilox(self.seed, self.increment * step, None, None,
-                                     w.stream_threads)
-        status = self.library.rln_forward(
-            t["x"].data_ptr(), t["branch"].data_ptr(), self.code(w.branch), self.weight.data_ptr(),
-            self.bias.data_ptr(), t["updated"].data_ptr(), t["normalized"].data_ptr(),
-            self.code(w.normalized), t["mean"].data_ptr(), t["rstd"].data_ptr(),
-            t["mask"].data_ptr(), None, None, w.rows, w.hidden,
-            w.dropout_p, EPS, int(w.training), philox, self.handle)
-        if status:
+        """The forward of `step` (its set, its Philox offset) through rln_forward."""
+        if not hasattr(self, "_forward_args"):
+            self._launch_arguments()
+        self._philox.offset = self.increment * step
+        if self.library.rln_forward(*self._forward_args[step % len(self.sets)]):
             raise RuntimeError(self.cabi.last_error())
 
     def backward(self, step: int):
-        t, w = self.sets[step % len(self.sets)], self.w
-        workspace = self.workspace
-        status = self.library.rln_backward(
-            t["grad_updated"].data_ptr(), t["grad_normalized"].data_ptr(),
-            self.code(w.normalized), t["updated"].data_ptr(), self.weight.data_ptr(), t["mean"].data_ptr(),
-            t["rstd"].data_ptr(), t["mask"].data_ptr(), t["grad_x"].data_ptr(),
-            t["grad_branch"].data_ptr(), self.code(w.branch), t["grad_weight"].data_ptr(),
-            t["grad_bias"].data_ptr(), w.rows, w.hidden, w.dropout_p, int(w.training),
-            int(w.deterministic), 1,
-            workspace.data_ptr() if workspace is not None else None,
-            workspace.numel() if workspace is not None else 0, self.handle)
-        if status:
+        """The backward of `step`'s set through rln_backward (weight/bias
+        gradients accumulated into the set's sums)."""
+        if not hasattr(self, "_forward_args"):
+            self._launch_arguments()
+        if self.library.rln_backward(*self._backward_args[step % len(self.sets)]):
             raise RuntimeError(self.cabi.last_error())
 
     def step(self, index: int):
@@ -602,15 +621,28 @@ class Runner:
         return start.elapsed_time(end) / count
 
     def measure(self, warmup: int, steps: int, launches: int = ROOFLINE_LAUNCHES) -> dict:
-        """Step time over exactly `steps` timed steps (the contract's K); the
-        per-kernel averages (the roofline) over `launches` back-to-back
-        launches of one kernel, whatever `steps` is."""
+        """Per-kernel averages (the roofline) over `launches` back-to-back
+        launches of one kernel, whatever `steps` is; then `warmup` untimed
+        steps and the step time over exactly `steps` timed steps (the
+        contract's W and K), with the GPU already busy for the kernel timings
+        before them; then the spread and the cold step."""
         w = self.w
-        for index in range(warmup):
+        for index in range(2 * len(self.sets)):
             self.step(index)
         self.stream.synchronize()
-        base = warmup
-        step_ms = self.timed(lambda i: self.step(base + i), steps)
+        base = 2 * len(self.sets)
+        forward_ms = self.timed(lambda i: self.forward(base + i), launches)
+        base += launches
+        result = {"forward_ms": forward_ms, "launches": launches}
+        if w.backward:
+            # Every set holds the saved state of a forward; re-running the
+            # backward on it is the same work as the step's backward.
+            result["backward_ms"] = self.timed(lambda i: self.backward(base + i), launches)
+            base += launches
+        for index in range(warmup):
+            self.step(base + index)
+        base += warmup
+        result["step_ms"] = self.timed(lambda i: self.step(base + i), steps)
         base += steps
         # Spread: the same steps timed in batches of 25 (p20 / median / p80
         # of the per-batch step time).
@@ -618,15 +650,8 @@ class Runner:
         for _ in range(max(steps // 25, 4)):
             batches.append(self.timed(lambda i: self.step(base + i), 25))
             base += 25
-        forward_ms = self.timed(lambda i: self.forward(base + i), launches)
-        base += launches
-        result = {"step_ms": step_ms, "forward_ms": forward_ms, "step_batches_ms": batches,
-                  "launches": launches}
+        result["step_batches_ms"] = batches
         if w.backward:
-            # Every set now holds the saved state of a forward; re-running the
-            # backward on it is the same work as the step's backward.
-            result["backward_ms"] = self.timed(lambda i: self.backward(base + i), launches)
-            base += launches
             # Backward on the set forwarded `lag` steps earlier (two, or one
             # when only two sets rotate).
             lag = min(2, len(self.sets) - 1)
@@ -769,8 +794,9 @@ def parity_self_check(torch, runner: "Runner") -> dict:
     (one ulp of its type + 1e-5 of the largest value), dW/db (normwise <= 1e-4),
     and the mask's keep ratio within 6 sigma of 1 - p."""
     w, t = runner.w, runner.sets[0]
-    t["grad_weight"].zero_()
-    t["grad_bias"].zero_()
+    if w.backward:
+        t["grad_weight"].zero_()
+        t["grad_bias"].zero_()
     runner.forward(0)
     if w.backward:
         runner.backward(0)
@@ -1084,6 +1110,8 @@ def main() -> int:
     result["parity"] = parity
     if args.quick:
         print(json.dumps(result), flush=True)
+        if args.sweep:
+            run_sweep(torch, library, _cabi, stream, args, sweep_workloads())
         return 0
     result["ceiling_us"] = {
         **ceiling,

@@ -101,6 +101,29 @@ void rln_zero_parameters_kernel(float* __restrict__ grad_weight, float* __restri
     }
 }
 
+// Compute units of the current device, looked up once per device (0 when
+// the runtime cannot say; the forward then keeps its device-independent grid).
+int compute_units() {
+    constexpr int kMaxDevices = 64;
+    static std::once_flag once[kMaxDevices];
+    static int units[kMaxDevices];
+    int device = -1;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) {
+        hipGetLastError();
+        return 0;
+    }
+    std::call_once(once[device], [device] {
+        int count = 0;
+        if (hipDeviceGetAttribute(&count, hipDeviceAttributeMultiprocessorCount, device)
+            != hipSuccess) {
+            hipGetLastError();
+            count = 0;
+        }
+        units[device] = count;
+    });
+    return units[device];
+}
+
 bool aligned_to(const void* pointer, uintptr_t alignment) {
     return pointer == nullptr || (reinterpret_cast<uintptr_t>(pointer) & (alignment - 1)) == 0;
 }
@@ -278,6 +301,7 @@ int rln_forward(
         a.philox.offset_ptr = philox->offset_ptr;
         a.philox.threads = static_cast<int>(philox->threads);
     }
+    a.compute_units = compute_units();
     const bool aligned = aligned_to(x, 16) && aligned_to(weight, 16) && aligned_to(bias, 16)
         && aligned_to(updated, 16)
         && aligned_to(normalized, vector_alignment(normalized_dtype))

@@ -18,9 +18,11 @@
 //    other work may reuse. A scalar-access variant of every kernel serves
 //    misaligned pointers with the identical arithmetic, so both variants are
 //    bitwise equal.
-//  * Waves walk rows with a grid-stride loop over a grid that depends only on
-//    (rows, H), never on the device, so the dropout stream and the
-//    deterministic parameter-gradient order are reproducible anywhere.
+//  * Waves walk rows with a grid-stride loop. The backward's grid depends
+//    only on (rows, H), never on the device, so its deterministic
+//    parameter-gradient order is reproducible anywhere; the forward's may
+//    follow the device's CU count (its outputs, the dropout mask included,
+//    depend on the row alone).
 //  * Dropout draws from Philox4x32-10 (Salmon et al., SC'11) in one of two
 //    layouts. The reference's (hidden sizes 128-1024): its hipRAND stream,
 //    one Philox state per (row, thread) of a launch with 128, 192 or 256
@@ -300,11 +302,29 @@ inline int64_t launch_blocks(int64_t rows, const ShapeInfo& info, int threads, i
 }
 
 // The forward gives each team at least two row steps so that its
-// look-ahead load overlaps a row's computation, with at most 2048 blocks.
+// look-ahead load overlaps a row's computation, with at most 2048 blocks,
+// and then a whole number of blocks per CU (`cus`, the device's compute
+// units; 0 = unknown): a launch whose block count is not a multiple of the
+// CU count leaves some CUs one block more, which then run alone at the end
+// (measured on MI355X: the C4 tail, [12291, 384], forward 14.8 us at 769
+// blocks, 14.1 us at 768). Rows owned by one whole wave of a specialized size
+// (768 and 1024 columns) run at most three blocks per CU: C1 [8192, 768]
+// 17.1 us against 17.4 us at four, C3 [65536, 1024] 164 us against 169 us at
+// eight, [262144, 1024] 718 us against 731 us; the narrower shapes, two or
+// four rows per wave, measured best at their own count. Every output of the
+// forward is a function of its row alone (the dropout mask of (seed, offset,
+// row, column)), so its grid may depend on the device.
 template <typename S>
-int64_t forward_blocks(int64_t rows) {
-    return launch_blocks(rows, info_of<S>(), S::kForwardThreads, kForwardMaxBlocks,
-                         RLN_FWD_GROUPS_PER_WAVE);
+int64_t forward_blocks(int64_t rows, int cus) {
+    int64_t blocks = launch_blocks(rows, info_of<S>(), S::kForwardThreads, kForwardMaxBlocks,
+                                   RLN_FWD_GROUPS_PER_WAVE);
+    if (cus > 0 && blocks > cus) {
+        if (S::kHidden > 0 && S::kLanes == kWaveSize && blocks > 3 * cus) {
+            blocks = 3 * cus;
+        }
+        blocks -= blocks % cus;
+    }
+    return blocks;
 }
 
 // The backward's grid is also the number of weight/bias partials: at most
@@ -1258,6 +1278,7 @@ struct ForwardArgs {
     float scale;
     uint32_t threshold;
     PhiloxArgs philox;
+    int compute_units;  // of the launch device; 0 = unknown (forward_blocks)
     hipStream_t stream;
 };
 
@@ -1297,7 +1318,7 @@ int check_shape(const S& shape, Pass pass, int64_t rows) {
 
 template <typename S, typename B, typename N, bool Aligned>
 int launch_forward(const ForwardArgs& a, S shape) {
-    const dim3 grid(static_cast<unsigned>(forward_blocks<S>(a.rows)));
+    const dim3 grid(static_cast<unsigned>(forward_blocks<S>(a.rows, a.compute_units)));
     rln_forward_kernel<S, B, N, Aligned><<<grid, S::kForwardThreads, 0, a.stream>>>(
         a.x,
         static_cast<const B*>(a.branch),
