@@ -232,7 +232,9 @@ def parse_args():
     parser.add_argument("--ceiling", action="store_true",
                         help="add op-vs-streaming-ceiling lines per configuration")
     parser.add_argument("--quick", action="store_true",
-                        help="C1 line only (no public-API, reference, ceiling or CPU legs)")
+                        help="C1 line only, its kernels launched only as the step launches them "
+                             "(no input-grads-only backward, public-API, reference, ceiling "
+                             "or CPU legs): the profiling runs")
     parser.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                         help="write profiles/rln_backward_c1_traffic.json from two rocprofv3 "
                              "--pmc output directories (no GPU needed)")
@@ -385,14 +387,20 @@ def prenorm_stack(torch, stream, depth: int = 12, hidden: int = 768, tokens: int
     return result
 
 
-def public_api_steps(torch, workload: Workload, stream, steps: int = 100) -> dict:
+GRAPH_STEPS = (1, 8, 32)
+
+
+def public_api_steps(torch, workload: Workload, stream, steps: int = 96) -> dict:
     """Whole autograd steps through the public API on this GPU, as a user runs
     them: `implementation="gfx950"` (these kernels) and
     `implementation="torch"` (the reference's decomposition, F.dropout + add +
     F.layer_norm, run by PyTorch-ROCm on the same GPU). `eager` includes
-    Python dispatch, autograd and allocation per step; `graph` replays the
-    same step captured in a HIP graph (the op draws a fresh dropout mask on
-    every replay)."""
+    Python dispatch, autograd and allocation per step; `host_us` is the CPU
+    time to issue one eager forward and one eager step (perf_counter over
+    `steps` calls, no synchronization inside: when it exceeds the GPU's time
+    the eager step is host-bound); `graph_steps` replays HIP graphs holding 1,
+    8 and 32 consecutive steps (the op draws a fresh dropout mask on every
+    replay of every step), per step; `graph` is the one-step graph."""
     from gfx1010_kernels import residual_layer_norm
 
     generator = torch.Generator(device="cuda").manual_seed(workload.seed)
@@ -409,36 +417,54 @@ def public_api_steps(torch, workload: Workload, stream, steps: int = 100) -> dic
     leaves = (x, branch, weight, bias)
     total = workload.forward_bytes() + workload.backward_bytes()
 
-    def timed(body):
+    def timed(body, calls, steps_per_call=1):
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         start.record(stream)
-        for _ in range(steps):
+        for _ in range(calls):
             body()
         end.record(stream)
         end.synchronize()
-        ms = start.elapsed_time(end) / steps
+        ms = start.elapsed_time(end) / (calls * steps_per_call)
         return {"us_per_step": round(ms * 1e3, 3), "gbps": round(total / (ms * 1e-3) / 1e9, 1)}
+
+    def host_us(body, calls):
+        torch.cuda.synchronize()
+        began = time.perf_counter()
+        for _ in range(calls):
+            body()
+        issued = time.perf_counter() - began
+        torch.cuda.synchronize()
+        return round(issued * 1e6 / calls, 2)
 
     result = {}
     with torch.cuda.stream(stream):
         for implementation in ("gfx950", "torch"):
-            def step():
-                updated, normalized = residual_layer_norm(
+            def forward():
+                return residual_layer_norm(
                     x, branch, weight, bias, dropout_p=workload.dropout_p, eps=EPS,
                     training=workload.training, implementation=implementation)
-                return torch.autograd.grad((updated, normalized), leaves, grads)
+
+            def step():
+                return torch.autograd.grad(forward(), leaves, grads)
 
             for _ in range(10):
                 step()
-            eager = timed(step)
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph, stream=stream):
-                step()
-            graph.replay()
-            result[implementation] = {"eager": eager, "graph": timed(graph.replay)}
-            del graph
+            entry = {"eager": timed(step, steps),
+                     "host_us": {"forward": host_us(forward, steps), "step": host_us(step, steps)}}
+            graph_steps = {}
+            for count in GRAPH_STEPS:
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, stream=stream):
+                    for _ in range(count):
+                        step()
+                graph.replay()
+                graph_steps[str(count)] = timed(graph.replay, max(steps // count, 4), count)
+                del graph
+            entry["graph"] = graph_steps["1"]
+            entry["graph_steps"] = graph_steps
+            result[implementation] = entry
     result["kind"] = ("fwd+bwd through residual_layer_norm(..., implementation=...) and "
                       f"torch.autograd.grad, {steps} steps back to back, one input set")
     return result
@@ -584,6 +610,9 @@ class Runner:
                     i64(w.hidden), f64(w.dropout_p), int(w.training), int(w.deterministic), 1,
                     p(workspace.data_ptr()) if workspace is not None else None,
                     workspace.numel() if workspace is not None else 0, handle))
+        # The same backwards with grad_weight and grad_bias NULL.
+        self._input_grad_args = [args[:11] + (None, None) + args[13:]
+                                 for args in self._backward_args]
 
     def forward(self, step: int):
         """The forward of `step` (its set, its Philox offset) through rln_forward."""
@@ -599,6 +628,13 @@ class Runner:
         if not hasattr(self, "_forward_args"):
             self._launch_arguments()
         if self.library.rln_backward(*self._backward_args[step % len(self.sets)]):
+            raise RuntimeError(self.cabi.last_error())
+
+    def backward_input_grads(self, step: int):
+        """The backward of `step`'s set with the weight/bias gradients not
+        requested (both NULL): the input gradients alone, which shows what
+        the parameter sums add to the backward."""
+        if self.library.rln_backward(*self._input_grad_args[step % len(self.sets)]):
             raise RuntimeError(self.cabi.last_error())
 
     def step(self, index: int):
@@ -620,12 +656,14 @@ class Runner:
         end.synchronize()
         return start.elapsed_time(end) / count
 
-    def measure(self, warmup: int, steps: int, launches: int = ROOFLINE_LAUNCHES) -> dict:
+    def measure(self, warmup: int, steps: int, launches: int = ROOFLINE_LAUNCHES,
+                input_grads: bool = True) -> dict:
         """Per-kernel averages (the roofline) over `launches` back-to-back
         launches of one kernel, whatever `steps` is; then `warmup` untimed
         steps and the step time over exactly `steps` timed steps (the
         contract's W and K), with the GPU already busy for the kernel timings
-        before them; then the spread and the cold step."""
+        before them; then the spread and the cold step. With `input_grads`,
+        also the backward with dW/db not requested, over `launches`."""
         w = self.w
         for index in range(2 * len(self.sets)):
             self.step(index)
@@ -639,6 +677,10 @@ class Runner:
             # backward on it is the same work as the step's backward.
             result["backward_ms"] = self.timed(lambda i: self.backward(base + i), launches)
             base += launches
+            if input_grads:
+                result["backward_input_grads_ms"] = self.timed(
+                    lambda i: self.backward_input_grads(base + i), launches)
+                base += launches
         for index in range(warmup):
             self.step(base + index)
         base += warmup
@@ -714,9 +756,27 @@ def load_traffic() -> tuple[int | None, str]:
         f"{record.get('commit')}")
 
 
-def _counter_means(directory: str) -> tuple[str, dict[str, float]]:
-    """(counter name, mean value per dispatch by kernel name) of one rocprofv3
-    --pmc csv output directory."""
+def mangled_kernel_name(name: str) -> str:
+    """The Itanium-ABI mangled prefix (through the template arguments) of a
+    kernel_name() instance, e.g. rln::rln_backward_kernel<rln::FixedShape<768,
+    64>, _Float16, float, true> -> _ZN3rln19rln_backward_kernelINS_10Fixed
+    ShapeILi768ELi64EEEDF16_fLb1EEE. rocprofv3 leaves names with _Float16 or
+    __bf16 arguments mangled, so counter csv rows are matched on this too."""
+    import re
+
+    match = re.fullmatch(r"rln::(\w+)<rln::(\w+)<(\d+), (\d+)>, ([\w ]+), ([\w ]+), (true|false)>",
+                         name)
+    if match is None:
+        raise ValueError(f"not a kernel_name() instance: {name}")
+    kernel, shape, first, second, branch, normalized, aligned = match.groups()
+    types = {"float": "f", "_Float16": "DF16_", "__bf16": "DF16b"}
+    return (f"_ZN3rln{len(kernel)}{kernel}INS_{len(shape)}{shape}ILi{first}ELi{second}EEE"
+            f"{types[branch]}{types[normalized]}Lb{int(aligned == 'true')}EEE")
+
+
+def _counter_values(directory: str) -> tuple[str, dict[str, list[float]]]:
+    """(counter name, the value of every dispatch by kernel name) of one
+    rocprofv3 --pmc csv output directory."""
     import csv
     from collections import defaultdict
 
@@ -729,29 +789,39 @@ def _counter_means(directory: str) -> tuple[str, dict[str, float]]:
             for row in csv.DictReader(handle):
                 counter = row["Counter_Name"]
                 values[row["Kernel_Name"]].append(float(row["Counter_Value"]))
-    return counter, {name: sum(v) / len(v) for name, v in values.items()}
+    return counter, dict(values)
 
 
 def traffic_summary(fetch_dir: str, write_dir: str) -> int:
     """Writes TRAFFIC_FILE from a FETCH_SIZE and a WRITE_SIZE pass of
     `bench.py --quick --calibrate-copy-mib 256`: each counter (KiB per
-    dispatch) is scaled by what it reads for the 256 MiB calibration copy
-    (the runtime's copyBuffer kernel: 262144 KiB read and written)."""
-    fetch_counter, fetch = _counter_means(fetch_dir)
-    write_counter, write = _counter_means(write_dir)
+    dispatch, averaged over the kernel's dispatches) is scaled by what it reads
+    for the 256 MiB calibration copy (the runtime's largest copyBuffer
+    dispatch: 262144 KiB read and written)."""
+    fetch_counter, fetch = _counter_values(fetch_dir)
+    write_counter, write = _counter_values(write_dir)
     if (fetch_counter, write_counter) != ("FETCH_SIZE", "WRITE_SIZE"):
         raise SystemExit(f"bench.py: expected FETCH_SIZE and WRITE_SIZE, got "
                          f"{fetch_counter} and {write_counter}")
 
     def lookup(table, prefix):
-        matches = [value for name, value in table.items() if name.startswith(prefix)]
+        mangled = mangled_kernel_name(prefix)
+        matches = [v for name, v in table.items()
+                   if name.startswith(prefix) or name.startswith(mangled)]
         if len(matches) != 1:
             raise SystemExit(f"bench.py: {len(matches)} kernels named {prefix}")
-        return matches[0]
+        return sum(matches[0]) / len(matches[0])
 
-    copy = "__amd_rocclr_copyBuffer"
-    fetch_scale = 262144.0 / lookup(fetch, copy)
-    write_scale = 262144.0 / lookup(write, copy)
+    def calibration(table):
+        copies = [v for name, v in table.items() if name.startswith("__amd_rocclr_copyBuffer")]
+        largest = max((value for v in copies for value in v), default=0.0)
+        if largest < 0.25 * 262144:
+            raise SystemExit("bench.py: no 256 MiB calibration copy in the counters "
+                             "(run the passes with --calibrate-copy-mib 256)")
+        return largest
+
+    fetch_scale = 262144.0 / calibration(fetch)
+    write_scale = 262144.0 / calibration(write)
     record = {"workload": C1.describe(), "sources_digest": kernel_sources_digest()}
     try:
         import subprocess
@@ -1038,6 +1108,10 @@ def result_line(torch, workload: Workload, timing: dict, steps: int, warmup: int
     if workload.backward:
         cold = gbps(total, timing["cold_ms"])
         line["bwd_us"] = round(timing["backward_ms"] * 1e3, 3)
+        # The same backward with dW/db not requested: the difference is the
+        # cost of the weight/bias sums (block combine + fp32 atomics).
+        if "backward_input_grads_ms" in timing:
+            line["bwd_input_grads_only_us"] = round(timing["backward_input_grads_ms"] * 1e3, 3)
         line["cold_step"] = {
             "us_per_step": round(timing["cold_ms"] * 1e3, 3),
             "gbps": round(cold, 2),
@@ -1099,7 +1173,9 @@ def main() -> int:
             print("bench.py: the timed path misses the parity bars; not timing it",
                   file=sys.stderr)
             return 1
-        timing = runner.measure(args.warmup, args.steps)
+        # --quick (the profiling runs) launches the kernels only as the step
+        # does, so per-kernel counter averages describe the step's launches.
+        timing = runner.measure(args.warmup, args.steps, input_grads=not args.quick)
         ceiling = None if args.quick else ceiling_times(torch, runner, ceiling_library())
         del runner
         print(f"[bench] C1: step {timing['step_ms'] * 1e3:.2f} us, forward "

@@ -8,6 +8,7 @@ import subprocess
 import sys
 from pathlib import Path
 
+
 BENCH = Path(__file__).resolve().parents[1] / "bench.py"
 
 
@@ -86,27 +87,34 @@ def test_mask_decoding_matches_the_oracle_layout():
     assert np.array_equal(keep.numpy(), oracle.decode_mask(words, rows, hidden).astype(bool))
 
 
+# The two C1 kernels as rocprofv3's counter csv names them (mangled).
+MANGLED_BACKWARD = ("_ZN3rln19rln_backward_kernelINS_10FixedShapeILi768ELi64EEEDF16_fLb1EEEvPKfPKT1_"
+                    "S4_S4_S4_S4_PKjPfPT0_SA_SA_SA_lT_ifi")
+MANGLED_FORWARD = ("_ZN3rln18rln_forward_kernelINS_10FixedShapeILi768ELi64EEEDF16_fLb1EEEvPKfPKT0_"
+                   "S4_S4_PfPT1_S8_S8_PjS8_S8_lT_fifjNS_10PhiloxArgsEi")
+
+
 def test_traffic_summary_scales_counters_and_stamps_the_sources(tmp_path, monkeypatch):
     """--traffic-summary turns two rocprofv3 --pmc csv directories into the
-    traffic record: each counter scaled by its value for the 256 MiB
-    calibration copy; the record carries the kernel-source digest, and a record
-    with another digest is reported stale instead of used."""
+    traffic record: kernel rows matched by their mangled names, each counter scaled by its value for the 256 MiB calibration copy (the
+    largest copyBuffer dispatch, among the runtime's small ones); the record
+    carries the kernel-source digest, and a record with another digest is
+    reported stale instead of used."""
     import json
 
     bench = _bench_module()
-    backward = bench.kernel_name("rln_backward_kernel", bench.C1)
-    forward = bench.kernel_name("rln_forward_kernel", bench.C1)
-    rows = {"FETCH_SIZE": {"__amd_rocclr_copyBuffer": 131072.0, backward: 37000.0,
-                           forward: 18500.0},
-            "WRITE_SIZE": {"__amd_rocclr_copyBuffer": 262144.0, backward: 38000.0,
-                           forward: 50000.0}}
+    rows = {"FETCH_SIZE": [("__amd_rocclr_copyBuffer", 131072.0), ("__amd_rocclr_copyBuffer", 1.5),
+                           (MANGLED_BACKWARD, 37000.0), (MANGLED_FORWARD, 18500.0)],
+            "WRITE_SIZE": [("__amd_rocclr_copyBuffer", 262144.0), ("__amd_rocclr_copyBuffer", 3.0),
+                           (MANGLED_BACKWARD, 38000.0), (MANGLED_FORWARD, 50000.0)]}
     for counter, values in rows.items():
         directory = tmp_path / counter / "host"
         directory.mkdir(parents=True)
         lines = ["Kernel_Name,Counter_Name,Counter_Value"]
-        for name, value in values.items():
-            for jitter in (-1.0, 1.0):
-                lines.append(f'"{name}(float const*)",{counter},{value + jitter}')
+        for name, value in values:
+            jitters = (0.0,) if name.startswith("__") else (-1.0, 1.0)
+            for jitter in jitters:
+                lines.append(f'"{name}",{counter},{value + jitter}')
         (directory / "1_counter_collection.csv").write_text("\n".join(lines) + "\n")
     target = tmp_path / "traffic.json"
     monkeypatch.setattr(bench, "TRAFFIC_FILE", target)
@@ -122,3 +130,25 @@ def test_traffic_summary_scales_counters_and_stamps_the_sources(tmp_path, monkey
     target.write_text(json.dumps(record))
     traffic, note = bench.load_traffic()
     assert traffic is None and note.startswith("stale")
+
+
+def test_mangled_kernel_names_are_the_library_symbols():
+    """mangled_kernel_name() gives the prefix rocprofv3 prints for the C1
+    kernels, and, where the built library and llvm-readelf are at hand, every
+    kernel bench.py names for its workloads is a symbol of the library."""
+    bench = _bench_module()
+    for kernel, mangled in (("rln_backward_kernel", MANGLED_BACKWARD),
+                            ("rln_forward_kernel", MANGLED_FORWARD)):
+        prefix = bench.mangled_kernel_name(bench.kernel_name(kernel, bench.C1))
+        assert mangled.startswith(prefix) and mangled[len(prefix):].startswith("vPK")
+    readelf = Path("/opt/rocm/llvm/bin/llvm-readelf")
+    library = BENCH.parent / "gfx1010-kernels_amd" / "gfx1010_kernels" / "librln_gfx950.so"
+    if not (readelf.exists() and library.exists()):
+        return
+    symbols = subprocess.run([str(readelf), "-s", "--wide", str(library)], capture_output=True,
+                             text=True, check=True).stdout
+    for workload in [bench.C1, *bench.sweep_workloads()]:
+        kernels = ["rln_forward_kernel"] + (["rln_backward_kernel"] if workload.backward else [])
+        for kernel in kernels:
+            prefix = bench.mangled_kernel_name(bench.kernel_name(kernel, workload))
+            assert prefix in symbols, (workload.describe(), kernel, prefix)
