@@ -398,7 +398,9 @@ def public_api_steps(torch, workload: Workload, stream, steps: int = 96) -> dict
     Python dispatch, autograd and allocation per step; `host_us` is the CPU
     time to issue one eager forward and one eager step (perf_counter over
     `steps` calls, no synchronization inside: when it exceeds the GPU's time
-    the eager step is host-bound); `graph_steps` replays HIP graphs holding 1,
+    the eager step is host-bound), and `engine_floor` that of
+    torch.autograd.grad over one elementwise op (x * 2), PyTorch's own floor
+    for a step with a CUDA backward; `graph_steps` replays HIP graphs holding 1,
     8 and 32 consecutive steps (the op draws a fresh dropout mask on every
     replay of every step), per step; `graph` is the one-step graph."""
     from gfx1010_kernels import residual_layer_norm
@@ -449,10 +451,15 @@ def public_api_steps(torch, workload: Workload, stream, steps: int = 96) -> dict
             def step():
                 return torch.autograd.grad(forward(), leaves, grads)
 
+            def engine_floor():
+                # One elementwise CUDA node through the same autograd engine.
+                return torch.autograd.grad((x * 2.0,), (x,), (grads[0],))
+
             for _ in range(10):
                 step()
             entry = {"eager": timed(step, steps),
-                     "host_us": {"forward": host_us(forward, steps), "step": host_us(step, steps)}}
+                     "host_us": {"forward": host_us(forward, steps), "step": host_us(step, steps),
+                                 "engine_floor": host_us(engine_floor, steps)}}
             graph_steps = {}
             for count in GRAPH_STEPS:
                 graph = torch.cuda.CUDAGraph()
