@@ -227,6 +227,9 @@ def parse_args():
                         help="also launch one device copy of this many MiB (PMC calibration)")
     parser.add_argument("--prenorm", action="store_true",
                         help="also time a pre-norm transformer stack, fused vs unfused")
+    parser.add_argument("--char-gpt", action="store_true",
+                        help="also time the reference's char-GPT AMP microstep (B=1, T=1024, "
+                             "C=384, L=8), original vs fused normalization flow")
     parser.add_argument("--reference-table", action="store_true",
                         help="also print the reference's published speedup table, measured here")
     parser.add_argument("--ceiling", action="store_true",
@@ -384,6 +387,112 @@ def prenorm_stack(torch, stream, depth: int = 12, hidden: int = 768, tokens: int
     result["speedup"] = round(result["unfused"]["ms_per_step"] / result["fused"]["ms_per_step"], 3)
     result["config"] = {"depth": depth, "hidden": hidden, "tokens": tokens,
                         "dropout_p": dropout_p, "sublayers": "bf16", "steps": steps}
+    return result
+
+
+def char_gpt_microstep(torch, stream, batch: int = 1, sequence: int = 1024, hidden: int = 384,
+                       depth: int = 8, heads: int = 6, vocab: int = 65, dropout_p: float = 0.2,
+                       warmup: int = 10, samples: int = 40) -> dict:
+    """The reference's model-level measurement (docs/residual_layer_norm.md:
+    380-385): a character-level GPT with B = 1, T = 1024, C = 384, L = 8, one
+    complete AMP (fp16 autocast) forward + backward microstep, 10 warmups and
+    40 event-timed samples, "original" normalization flow against the fused
+    one. The model is nanoGPT-shaped (its shakespeare-char vocabulary of 65
+    and dropout 0.2; the reference states neither): token + position
+    embeddings with dropout, pre-norm blocks of causal self-attention (6
+    heads, fused attention kernels only: a missing one raises rather than
+    falling back to the math path) and a 4x GELU MLP, each with residual
+    dropout, a final LayerNorm, an untied vocabulary projection and the
+    cross-entropy loss. "original" runs `x = x + dropout(sublayer(ln(x)))`;
+    "fused" runs prenorm_forward (every residual add + dropout fused into the
+    LayerNorm after it, implementation="gfx950"). Weights are random, the
+    tokens synthetic. Returns medians in milliseconds."""
+    from torch import nn
+    from torch.nn import functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    from gfx1010_kernels import prenorm_forward
+
+    class Attention(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.qkv = nn.Linear(hidden, 3 * hidden)
+            self.proj = nn.Linear(hidden, hidden)
+
+        def forward(self, h):
+            b, t, c = h.shape
+            q, k, v = self.qkv(h).split(hidden, dim=2)
+            q, k, v = (z.view(b, t, heads, c // heads).transpose(1, 2) for z in (q, k, v))
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+                y = F.scaled_dot_product_attention(q, k, v, is_causal=True)
+            return self.proj(y.transpose(1, 2).reshape(b, t, c))
+
+    class Block(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.ln_1 = nn.LayerNorm(hidden)
+            self.attn = Attention()
+            self.ln_2 = nn.LayerNorm(hidden)
+            self.mlp = nn.Sequential(nn.Linear(hidden, 4 * hidden), nn.GELU(),
+                                     nn.Linear(4 * hidden, hidden))
+
+    class CharGPT(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.tokens = nn.Embedding(vocab, hidden)
+            self.positions = nn.Embedding(sequence, hidden)
+            self.h = nn.ModuleList(Block() for _ in range(depth))
+            self.ln_f = nn.LayerNorm(hidden)
+            self.head = nn.Linear(hidden, vocab, bias=False)
+
+        def forward(self, index, fused):
+            positions = torch.arange(sequence, device=index.device)
+            x = F.dropout(self.tokens(index) + self.positions(positions), dropout_p, True)
+            if fused:
+                _, out = prenorm_forward(x, self.h, self.ln_f, dropout_p=dropout_p, training=True,
+                                         implementation="gfx950")
+            else:
+                for block in self.h:
+                    x = x + F.dropout(block.attn(block.ln_1(x)), dropout_p, True)
+                    x = x + F.dropout(block.mlp(block.ln_2(x)), dropout_p, True)
+                out = self.ln_f(x)
+            return self.head(out)
+
+    torch.manual_seed(0)
+    model = CharGPT().cuda()
+    generator = torch.Generator(device="cuda").manual_seed(1)
+    index = torch.randint(0, vocab, (batch, sequence), device="cuda", generator=generator)
+    targets = torch.randint(0, vocab, (batch, sequence), device="cuda", generator=generator)
+
+    def microstep(fused):
+        with torch.autocast(device_type="cuda", dtype=torch.float16):
+            logits = model(index, fused)
+            loss = F.cross_entropy(logits.view(-1, vocab).float(), targets.view(-1))
+        loss.backward()
+
+    result = {}
+    with torch.cuda.stream(stream):
+        for name, fused in (("original", False), ("fused", True)):
+            times = []
+            for sample in range(warmup + samples):
+                model.zero_grad(set_to_none=True)
+                start = torch.cuda.Event(enable_timing=True)
+                end = torch.cuda.Event(enable_timing=True)
+                start.record(stream)
+                microstep(fused)
+                end.record(stream)
+                end.synchronize()
+                if sample >= warmup:
+                    times.append(start.elapsed_time(end))
+            result[name] = {"median_ms": round(statistics.median(times), 4),
+                            "p20_ms": round(sorted(times)[len(times) // 5], 4),
+                            "p80_ms": round(sorted(times)[(4 * len(times)) // 5], 4)}
+    result["speedup"] = round(result["original"]["median_ms"] / result["fused"]["median_ms"], 4)
+    result["config"] = {"batch": batch, "sequence": sequence, "hidden": hidden, "depth": depth,
+                        "heads": heads, "vocab": vocab, "dropout_p": dropout_p, "amp": "fp16",
+                        "warmup": warmup, "samples": samples}
+    result["reference_published"] = {"original_ms": 150.119, "fused_ms": 148.946,
+                                     "speedup": 1.008, "gpu": "gfx1010 (RX 5600 XT)"}
     return result
 
 
@@ -1225,6 +1334,11 @@ def main() -> int:
     if args.prenorm:
         line = {"metric": "pre-norm stack fwd+bwd step time (ms)", "higher_is_better": False,
                 **prenorm_stack(torch, stream)}
+        print(json.dumps(line), flush=True)
+
+    if args.char_gpt:
+        line = {"metric": "char-GPT AMP fwd+bwd microstep time (ms)", "higher_is_better": False,
+                **char_gpt_microstep(torch, stream)}
         print(json.dumps(line), flush=True)
 
     if args.reference_table:

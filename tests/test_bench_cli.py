@@ -25,7 +25,7 @@ def test_help_lists_the_measurement_modes():
                             text=True, timeout=120)
     assert result.returncode == 0
     for flag in ("--steps", "--warmup", "--sweep", "--prenorm", "--reference-table", "--config",
-                 "--ceiling", "--quick", "--traffic-summary"):
+                 "--ceiling", "--quick", "--traffic-summary", "--char-gpt"):
         assert flag in result.stdout
 
 
