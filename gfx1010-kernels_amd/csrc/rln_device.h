@@ -70,6 +70,14 @@
 #ifndef RLN_FWD_GROUPS_PER_WAVE
 #define RLN_FWD_GROUPS_PER_WAVE 2
 #endif
+// Forward launches over at least this many elements (rows of up to four
+// waves) run one row step per team, on up to RLN_FWD_LARGE_MAX_BLOCKS blocks.
+#ifndef RLN_FWD_LARGE_ELEMENTS
+#define RLN_FWD_LARGE_ELEMENTS (1ll << 23)
+#endif
+#ifndef RLN_FWD_LARGE_MAX_BLOCKS
+#define RLN_FWD_LARGE_MAX_BLOCKS 24576
+#endif
 #ifndef RLN_BWD_MAX_BLOCKS
 #define RLN_BWD_MAX_BLOCKS 256
 #endif
@@ -99,6 +107,8 @@ namespace rln {
 constexpr int kWaveSize = 64;
 constexpr int kBackwardThreads = RLN_BWD_THREADS;
 constexpr int64_t kForwardMaxBlocks = RLN_FWD_MAX_BLOCKS;
+constexpr int64_t kForwardLargeElements = RLN_FWD_LARGE_ELEMENTS;
+constexpr int64_t kForwardLargeMaxBlocks = RLN_FWD_LARGE_MAX_BLOCKS;
 constexpr int64_t kBackwardMaxBlocks = RLN_BWD_MAX_BLOCKS;
 constexpr int64_t kPacedElements = RLN_PACED_ELEMENTS;
 constexpr int64_t kPacedMinHidden = RLN_PACED_MIN_HIDDEN;
@@ -301,7 +311,7 @@ inline int64_t launch_blocks(int64_t rows, const ShapeInfo& info, int threads, i
     return blocks < cap ? blocks : cap;
 }
 
-// The forward gives each team at least two row steps so that its
+// Small forward launches give each team at least two row steps so that its
 // look-ahead load overlaps a row's computation, with at most 2048 blocks,
 // and then a whole number of blocks per CU (`cus`, the device's compute
 // units; 0 = unknown): a launch whose block count is not a multiple of the
@@ -309,19 +319,35 @@ inline int64_t launch_blocks(int64_t rows, const ShapeInfo& info, int threads, i
 // (measured on MI355X: the C4 tail, [12291, 384], forward 14.8 us at 769
 // blocks, 14.1 us at 768). Rows owned by one whole wave of a specialized size
 // (768 and 1024 columns) run at most three blocks per CU: C1 [8192, 768]
-// 17.1 us against 17.4 us at four, C3 [65536, 1024] 164 us against 169 us at
-// eight, [262144, 1024] 718 us against 731 us; the narrower shapes, two or
-// four rows per wave, measured best at their own count. Every output of the
-// forward is a function of its row alone (the dropout mask of (seed, offset,
-// row, column)), so its grid may depend on the device.
+// 17.1 us against 17.4 us at four and 17.8 us at 2048 (one step per team);
+// the narrower shapes, two or four rows per wave, measured best at their own
+// count. Large launches (2^23 elements and up) of rows of up to four waves
+// instead run one row step per team, up to 24576 blocks, again a whole number
+// per CU: the hardware keeps as many of them resident as registers allow and
+// starts the next as one ends, which streams faster than fewer teams walking
+// many rows. Measured at 262144 rows (forward, us, the small-launch grid
+// against one step per team, alternated in one run where marked *): H = 128
+// 99 -> 92, 256 179 -> 159, 384 258 -> 238, 512 352 -> 317, 768 541-550 ->
+// 491-495 *, 1024 681-758 -> 652-653 *; [65536, 1024] 166-169 -> 159 *,
+// [65536, 256] 44.7 -> 40.2, [16384, 768] 32.4 -> 31.9; run-time rows of
+// 640-4096 columns 3-6 % faster. Eight-wave rows (4097-8192 columns, one row
+// per 512-thread block and few blocks per CU) keep the small-launch grid:
+// 321 us against 387 us at [16384, 8192]. Every output of the forward is a
+// function of its row alone (the dropout mask of (seed, offset, row,
+// column)), so its grid may depend on the device.
 template <typename S>
-int64_t forward_blocks(int64_t rows, int cus) {
-    int64_t blocks = launch_blocks(rows, info_of<S>(), S::kForwardThreads, kForwardMaxBlocks,
-                                   RLN_FWD_GROUPS_PER_WAVE);
-    if (cus > 0 && blocks > cus) {
-        if (S::kHidden > 0 && S::kLanes == kWaveSize && blocks > 3 * cus) {
+int64_t forward_blocks(int64_t rows, int64_t hidden, int cus) {
+    int64_t blocks;
+    if (S::kParts < 8 && rows * hidden >= kForwardLargeElements) {
+        blocks = launch_blocks(rows, info_of<S>(), S::kForwardThreads, kForwardLargeMaxBlocks, 1);
+    } else {
+        blocks = launch_blocks(rows, info_of<S>(), S::kForwardThreads, kForwardMaxBlocks,
+                               RLN_FWD_GROUPS_PER_WAVE);
+        if (cus > 0 && S::kHidden > 0 && S::kLanes == kWaveSize && blocks > 3 * cus) {
             blocks = 3 * cus;
         }
+    }
+    if (cus > 0 && blocks > cus) {
         blocks -= blocks % cus;
     }
     return blocks;
@@ -1318,7 +1344,8 @@ int check_shape(const S& shape, Pass pass, int64_t rows) {
 
 template <typename S, typename B, typename N, bool Aligned>
 int launch_forward(const ForwardArgs& a, S shape) {
-    const dim3 grid(static_cast<unsigned>(forward_blocks<S>(a.rows, a.compute_units)));
+    const dim3 grid(
+        static_cast<unsigned>(forward_blocks<S>(a.rows, shape.hidden(), a.compute_units)));
     rln_forward_kernel<S, B, N, Aligned><<<grid, S::kForwardThreads, 0, a.stream>>>(
         a.x,
         static_cast<const B*>(a.branch),
