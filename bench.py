@@ -235,9 +235,10 @@ def parse_args():
     parser.add_argument("--ceiling", action="store_true",
                         help="add op-vs-streaming-ceiling lines per configuration")
     parser.add_argument("--quick", action="store_true",
-                        help="C1 line only, its kernels launched only as the step launches them "
-                             "(no input-grads-only backward, public-API, reference, ceiling "
-                             "or CPU legs): the profiling runs")
+                        help="C1 line only (with --sweep or --config: those lines), kernels "
+                             "launched only as the step launches them (no input-grads-only "
+                             "backward, public-API, reference, ceiling or CPU legs): the "
+                             "profiling runs")
     parser.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                         help="write profiles/rln_backward_c1_traffic.json from two rocprofv3 "
                              "--pmc output directories (no GPU needed)")
@@ -1387,7 +1388,8 @@ def run_sweep(torch, library, cabi, stream, args, workloads) -> None:
         with torch.cuda.stream(stream):
             runner = Runner(torch, library, cabi, workload, sets, stream)
             parity = parity_self_check(torch, runner)
-            timing = runner.measure(min(args.warmup, 10) if large else args.warmup, steps)
+            timing = runner.measure(min(args.warmup, 10) if large else args.warmup, steps,
+                                    input_grads=not args.quick)
             del runner
         torch.cuda.empty_cache()
         line = result_line(torch, workload, timing, steps, args.warmup, sets, None)
