@@ -1,0 +1,54 @@
+"""Both sides of the forward's launch-shape switch, every row class.
+
+Forward launches below 2^23 elements run 2-3 persistent blocks per CU whose
+teams walk several rows; from 2^23 elements (rows of up to four waves) one
+row step per team on up to 24576 blocks, rounded down to a whole number of
+blocks per CU, so that some teams still take a second step. Each case runs a
+forward + backward just below and just above the switch, with ragged row
+counts, and checks every element against the oracle
+(parity.check_full_tensor): the whole mask bitwise, `updated` bitwise, the
+rest against float64 on the device, dW/db against a float64 reduction.
+"""
+
+import pytest
+import torch
+
+from gfx1010_kernels import _C
+from parity import check_full_tensor, generator_state
+from test_gpu_configs import check_parameter_gradients, device_inputs
+
+pytestmark = pytest.mark.gpu
+EPS = 1e-5
+SWITCH = 1 << 23
+
+# (hidden, rows below the switch, rows above it, branch type): one-wave rows of a
+# specialized size, four and two rows per wave, and run-time rows of two, four
+# and eight waves (eight-wave rows keep the persistent grid on both sides).
+CASES = [
+    (1024, 8191, 8193, torch.float16),
+    (128, 65535, 65537, torch.float16),
+    (384, 21845, 21846, torch.bfloat16),
+    (1600, 5242, 5243, torch.float16),
+    (4096, 2047, 2049, torch.float16),
+    (8192, 1023, 1025, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("side", ["below", "above"])
+@pytest.mark.parametrize("hidden,below,above,branch_dtype", CASES,
+                         ids=[f"H{case[0]}" for case in CASES])
+def test_forward_grid_switch(hidden, below, above, branch_dtype, side):
+    rows = below if side == "below" else above
+    assert (rows * hidden >= SWITCH) == (side == "above")
+    print(f"[launch shapes] rows={rows} H={hidden} {branch_dtype}", flush=True)
+    inputs, grads = device_inputs(rows, hidden, branch_dtype, seed=hidden + rows)
+    torch.cuda.manual_seed(hidden + rows)
+    seed, offset = generator_state()
+    outputs = _C.residual_layer_norm_forward(*inputs, 0.1, EPS, True, 128)
+    gradients = _C.residual_layer_norm_backward(
+        grads[0], grads[1], outputs[0], inputs[2], outputs[2], outputs[3], outputs[4], 0.1, True,
+        branch_dtype == torch.float16, 128, 64, 64, 1, True, branch_dtype)
+    assert gradients[1].dtype == branch_dtype
+    check_full_tensor(inputs, grads, outputs, gradients, 0.1, EPS, seed, offset,
+                      what=f"{rows} x {hidden}")
+    check_parameter_gradients(outputs[0], grads[1], gradients)
