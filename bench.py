@@ -727,7 +727,8 @@ class Runner:
                     i64(w.hidden), f64(w.dropout_p), int(w.training), int(w.deterministic), 1,
                     p(workspace.data_ptr()) if workspace is not None else None,
                     workspace.numel() if workspace is not None else 0, handle))
-        # The same backwards with grad_weight and grad_bias NULL.
+        # The same backwards with grad_weight and grad_bias (arguments 11 and
+        # 12 of rln_backward) NULL.
         self._input_grad_args = [args[:11] + (None, None) + args[13:]
                                  for args in self._backward_args]
 
@@ -751,6 +752,8 @@ class Runner:
         """The backward of `step`'s set with the weight/bias gradients not
         requested (both NULL): the input gradients alone, which shows what
         the parameter sums add to the backward."""
+        if not hasattr(self, "_forward_args"):
+            self._launch_arguments()
         if self.library.rln_backward(*self._input_grad_args[step % len(self.sets)]):
             raise RuntimeError(self.cabi.last_error())
 
