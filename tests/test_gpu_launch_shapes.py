@@ -52,3 +52,29 @@ def test_forward_grid_switch(hidden, below, above, branch_dtype, side):
     check_full_tensor(inputs, grads, outputs, gradients, 0.1, EPS, seed, offset,
                       what=f"{rows} x {hidden}")
     check_parameter_gradients(outputs[0], grads[1], gradients)
+
+
+@pytest.mark.parametrize("hidden,rows,branch_dtype,normalized_dtype", [
+    (768, 10923, torch.bfloat16, torch.bfloat16),
+    (256, 32769, torch.float16, torch.float16),
+    (2048, 4097, torch.bfloat16, torch.float16),
+], ids=["H768-bf16", "H256-f16", "H2048-bf16-f16"])
+def test_half_normalized_above_the_switch(hidden, rows, branch_dtype, normalized_dtype):
+    """The large-launch grid with a half-precision normalized output and
+    upstream gradient (one ulp of its type), whole tensors."""
+    assert rows * hidden >= SWITCH
+    print(f"[launch shapes] rows={rows} H={hidden} {branch_dtype} -> {normalized_dtype}",
+          flush=True)
+    inputs, grads = device_inputs(rows, hidden, branch_dtype, seed=3 * hidden + rows)
+    grads = (grads[0], grads[1].to(normalized_dtype))
+    torch.cuda.manual_seed(3 * hidden + rows)
+    seed, offset = generator_state()
+    outputs = _C.residual_layer_norm_forward(*inputs, 0.1, EPS, True, 128,
+                                             normalized_dtype=normalized_dtype)
+    assert outputs[1].dtype == normalized_dtype
+    gradients = _C.residual_layer_norm_backward(
+        grads[0], grads[1], outputs[0], inputs[2], outputs[2], outputs[3], outputs[4], 0.1, True,
+        branch_dtype == torch.float16, 128, 64, 64, 1, True, branch_dtype)
+    check_full_tensor(inputs, grads, outputs, gradients, 0.1, EPS, seed, offset,
+                      what=f"{rows} x {hidden} {normalized_dtype}")
+    check_parameter_gradients(outputs[0], grads[1], gradients)
