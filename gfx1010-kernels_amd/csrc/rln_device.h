@@ -70,8 +70,8 @@
 #ifndef RLN_FWD_GROUPS_PER_WAVE
 #define RLN_FWD_GROUPS_PER_WAVE 2
 #endif
-// Forward launches over at least this many elements (rows of up to four
-// waves) run one row step per team, on up to RLN_FWD_LARGE_MAX_BLOCKS blocks.
+// Forward launches over at least this many elements run one row step per
+// team (two for eight-wave rows), on up to RLN_FWD_LARGE_MAX_BLOCKS blocks.
 #ifndef RLN_FWD_LARGE_ELEMENTS
 #define RLN_FWD_LARGE_ELEMENTS (1ll << 23)
 #endif
@@ -321,9 +321,9 @@ inline int64_t launch_blocks(int64_t rows, const ShapeInfo& info, int threads, i
 // (768 and 1024 columns) run at most three blocks per CU: C1 [8192, 768]
 // 17.1 us against 17.4 us at four and 17.8 us at 2048 (one step per team);
 // the narrower shapes, two or four rows per wave, measured best at their own
-// count. Large launches (2^23 elements and up) of rows of up to four waves
-// instead run one row step per team, up to 24576 blocks, again a whole number
-// per CU: the hardware keeps as many of them resident as registers allow and
+// count. Large launches (2^23 elements and up) instead run one row step per
+// team (two for eight-wave rows), up to 24576 blocks, again a whole number per
+// CU: the hardware keeps as many of them resident as registers allow and
 // starts the next as one ends, which streams faster than fewer teams walking
 // many rows. Measured at 262144 rows (forward, us, the small-launch grid
 // against one step per team, alternated in one run where marked *): H = 128
@@ -331,15 +331,18 @@ inline int64_t launch_blocks(int64_t rows, const ShapeInfo& info, int threads, i
 // 491-495 *, 1024 681-758 -> 652-653 *; [65536, 1024] 166-169 -> 159 *,
 // [65536, 256] 44.7 -> 40.2, [16384, 768] 32.4 -> 31.9; run-time rows of
 // 640-4096 columns 3-6 % faster. Eight-wave rows (4097-8192 columns, one row
-// per 512-thread block and few blocks per CU) keep the small-launch grid:
-// 321 us against 387 us at [16384, 8192]. Every output of the forward is a
+// per 512-thread block and few blocks per CU) need the look-ahead of a second
+// step: one step per team took 387 us at [16384, 8192] against 321-342 us for
+// the persistent grid, two steps 331-334 us against 338-341 us alternated in
+// one run ([26214, 5120]: 328 us against 335 us). Every output of the forward is a
 // function of its row alone (the dropout mask of (seed, offset, row,
 // column)), so its grid may depend on the device.
 template <typename S>
 int64_t forward_blocks(int64_t rows, int64_t hidden, int cus) {
     int64_t blocks;
-    if (S::kParts < 8 && rows * hidden >= kForwardLargeElements) {
-        blocks = launch_blocks(rows, info_of<S>(), S::kForwardThreads, kForwardLargeMaxBlocks, 1);
+    if (rows * hidden >= kForwardLargeElements) {
+        blocks = launch_blocks(rows, info_of<S>(), S::kForwardThreads, kForwardLargeMaxBlocks,
+                               S::kParts < 8 ? 1 : 2);
     } else {
         blocks = launch_blocks(rows, info_of<S>(), S::kForwardThreads, kForwardMaxBlocks,
                                RLN_FWD_GROUPS_PER_WAVE);

@@ -1,9 +1,9 @@
 """Both sides of the forward's launch-shape switch, every row class.
 
 Forward launches below 2^23 elements run 2-3 persistent blocks per CU whose
-teams walk several rows; from 2^23 elements (rows of up to four waves) one
-row step per team on up to 24576 blocks, rounded down to a whole number of
-blocks per CU, so that some teams still take a second step. Each case runs a
+teams walk several rows; from 2^23 elements one row step per team (two for
+eight-wave rows) on up to 24576 blocks, rounded down to a whole number of
+blocks per CU, so that some teams take one step more. Each case runs a
 forward + backward just below and just above the switch, with ragged row
 counts, and checks every element against the oracle
 (parity.check_full_tensor): the whole mask bitwise, `updated` bitwise, the
@@ -23,7 +23,7 @@ SWITCH = 1 << 23
 
 # (hidden, rows below the switch, rows above it, branch type): one-wave rows of a
 # specialized size, four and two rows per wave, and run-time rows of two, four
-# and eight waves (eight-wave rows keep the persistent grid on both sides).
+# and eight waves.
 CASES = [
     (1024, 8191, 8193, torch.float16),
     (128, 65535, 65537, torch.float16),
