@@ -785,10 +785,15 @@ class Runner:
         before them; then the spread and the cold step. With `input_grads`,
         also the backward with dW/db not requested, over `launches`."""
         w = self.w
-        for index in range(2 * len(self.sets)):
-            self.step(index)
-        self.stream.synchronize()
+        # Untimed steps until the GPU has run about 25 ms of this work: its
+        # clocks ramp up under load, and the first kernel timings after an
+        # idle GPU came out ~4 % slow (C1 forward 17.7 against 17.0 us).
+        first_ms = self.timed(lambda i: self.step(i), 2 * len(self.sets))
         base = 2 * len(self.sets)
+        ramp = min(int(25.0 / max(first_ms, 1e-3)), 5000)
+        for index in range(ramp):
+            self.step(base + index)
+        base += ramp
         forward_ms = self.timed(lambda i: self.forward(base + i), launches)
         base += launches
         result = {"forward_ms": forward_ms, "launches": launches}
