@@ -498,14 +498,16 @@ def char_gpt_microstep(torch, stream, batch: int = 1, sequence: int = 1024, hidd
 
 
 GRAPH_STEPS = (1, 8, 32)
+PUBLIC_API_SETS = 4
 
 
 def public_api_steps(torch, workload: Workload, stream, steps: int = 96) -> dict:
     """Whole autograd steps through the public API on this GPU, as a user runs
     them: `implementation="gfx950"` (these kernels) and
     `implementation="torch"` (the reference's decomposition, F.dropout + add +
-    F.layer_norm, run by PyTorch-ROCm on the same GPU). `eager` includes
-    Python dispatch, autograd and allocation per step; `host_us` is the CPU
+    F.layer_norm, run by PyTorch-ROCm on the same GPU), over 4 input sets
+    rotated from step to step. `eager` includes Python dispatch, autograd and
+    allocation per step; `host_us` is the CPU
     time to issue one eager forward and one eager step (perf_counter over
     `steps` calls, no synchronization inside: when it exceeds the GPU's time
     the eager step is host-bound), and `engine_floor` that of
@@ -518,16 +520,25 @@ def public_api_steps(torch, workload: Workload, stream, steps: int = 96) -> dict
     generator = torch.Generator(device="cuda").manual_seed(workload.seed)
     shape = (workload.rows, workload.hidden)
     branch_type = getattr(torch, DTYPE_NAMES[workload.branch])
-    x = torch.randn(shape, device="cuda", generator=generator).requires_grad_(True)
-    branch = (workload.branch_std * torch.randn(shape, device="cuda", generator=generator)).to(
-        branch_type).requires_grad_(True)
     weight = (1.0 + 0.02 * torch.randn(workload.hidden, device="cuda",
                                        generator=generator)).requires_grad_(True)
     bias = (0.02 * torch.randn(workload.hidden, device="cuda",
                                generator=generator)).requires_grad_(True)
-    grads = [torch.randn(shape, device="cuda", generator=generator) for _ in range(2)]
-    leaves = (x, branch, weight, bias)
+    # Input sets rotated from step to step, as in the C-ABI timing: each
+    # step's inputs and upstream gradients are other tensors than the last's.
+    sets = []
+    for _ in range(PUBLIC_API_SETS):
+        x = torch.randn(shape, device="cuda", generator=generator).requires_grad_(True)
+        branch = (workload.branch_std * torch.randn(shape, device="cuda", generator=generator)).to(
+            branch_type).requires_grad_(True)
+        grads = [torch.randn(shape, device="cuda", generator=generator) for _ in range(2)]
+        sets.append(((x, branch, weight, bias), grads))
     total = workload.forward_bytes() + workload.backward_bytes()
+    counter = [0]
+
+    def next_set():
+        counter[0] += 1
+        return sets[counter[0] % len(sets)]
 
     def timed(body, calls, steps_per_call=1):
         start = torch.cuda.Event(enable_timing=True)
@@ -553,16 +564,19 @@ def public_api_steps(torch, workload: Workload, stream, steps: int = 96) -> dict
     result = {}
     with torch.cuda.stream(stream):
         for implementation in ("gfx950", "torch"):
-            def forward():
+            def forward(leaves=None):
+                x, branch, weight_, bias_ = leaves or next_set()[0]
                 return residual_layer_norm(
-                    x, branch, weight, bias, dropout_p=workload.dropout_p, eps=EPS,
+                    x, branch, weight_, bias_, dropout_p=workload.dropout_p, eps=EPS,
                     training=workload.training, implementation=implementation)
 
             def step():
-                return torch.autograd.grad(forward(), leaves, grads)
+                leaves, grads = next_set()
+                return torch.autograd.grad(forward(leaves), leaves, grads)
 
             def engine_floor():
                 # One elementwise CUDA node through the same autograd engine.
+                (x, *_), grads = next_set()
                 return torch.autograd.grad((x * 2.0,), (x,), (grads[0],))
 
             for _ in range(10):
@@ -583,7 +597,8 @@ def public_api_steps(torch, workload: Workload, stream, steps: int = 96) -> dict
             entry["graph_steps"] = graph_steps
             result[implementation] = entry
     result["kind"] = ("fwd+bwd through residual_layer_norm(..., implementation=...) and "
-                      f"torch.autograd.grad, {steps} steps back to back, one input set")
+                      f"torch.autograd.grad, {steps} steps back to back, {PUBLIC_API_SETS} "
+                      "input sets rotated")
     return result
 
 
