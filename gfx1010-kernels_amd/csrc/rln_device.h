@@ -829,19 +829,24 @@ void rln_forward_kernel(
         }
     }
 
+    // The Philox key and position of this call (from the generator's device
+    // state under graph capture). Read after the team's first row loads are
+    // issued, so those loads do not wait behind them (C1 forward 0.1 us).
     uint32_t key0 = 0;
     uint32_t key1 = 0;
     uint64_t position = 0;
-    if (dropout) {
-        const uint64_t seed = philox.seed_ptr
-            ? static_cast<uint64_t>(*philox.seed_ptr)
-            : philox.seed;
-        const uint64_t offset = philox.offset
-            + (philox.offset_ptr ? static_cast<uint64_t>(*philox.offset_ptr) : 0);
-        key0 = static_cast<uint32_t>(seed);
-        key1 = static_cast<uint32_t>(seed >> 32);
-        position = offset / 4;
-    }
+    auto read_philox_state = [&]() {
+        if (dropout) {
+            const uint64_t seed = philox.seed_ptr
+                ? static_cast<uint64_t>(*philox.seed_ptr)
+                : philox.seed;
+            const uint64_t offset = philox.offset
+                + (philox.offset_ptr ? static_cast<uint64_t>(*philox.offset_ptr) : 0);
+            key0 = static_cast<uint32_t>(seed);
+            key1 = static_cast<uint32_t>(seed >> 32);
+            position = offset / 4;
+        }
+    };
     const bool reference_stream = kReferenceStream && dropout && philox.threads != 0;
 
     // Loads x and the branch of one row. The loads are unconditional (a row
@@ -1001,6 +1006,7 @@ void rln_forward_kernel(
     }
     ForwardRow<V, B> current;
     load_row(current, first + team.offset, false);
+    read_philox_state();
     uint32_t keep = reference_keep(first + team.offset);
     if (paced) {
         for (; first + stride < rows; first += stride) {
