@@ -78,3 +78,40 @@ def test_half_normalized_above_the_switch(hidden, rows, branch_dtype, normalized
     check_full_tensor(inputs, grads, outputs, gradients, 0.1, EPS, seed, offset,
                       what=f"{rows} x {hidden} {normalized_dtype}")
     check_parameter_gradients(outputs[0], grads[1], gradients)
+
+
+def _random_large_cases(count=8, seed=2302):
+    """Seeded (rows, hidden, branch, normalized, p) above the switch: hidden any
+    multiple of 64 up to 8192, 2^23-2^25 elements, every dtype pairing."""
+    import random
+
+    rng = random.Random(seed)
+    cases = []
+    for _ in range(count):
+        hidden = 64 * rng.randint(2, 128)
+        rows = rng.randint(SWITCH // hidden + 1, (1 << 25) // hidden)
+        cases.append((rows, hidden, rng.choice([torch.float16, torch.bfloat16, torch.float32]),
+                      rng.choice([None, torch.float16, torch.bfloat16]),
+                      rng.choice([0.0, 0.1, 0.15])))
+    return cases
+
+
+@pytest.mark.parametrize("rows,hidden,branch_dtype,normalized_dtype,dropout_p",
+                         _random_large_cases(), ids=lambda v: str(v).replace("torch.", ""))
+def test_seeded_random_shapes_above_the_switch(rows, hidden, branch_dtype, normalized_dtype,
+                                               dropout_p):
+    print(f"[launch shapes] rows={rows} H={hidden} {branch_dtype} -> {normalized_dtype} "
+          f"p={dropout_p}", flush=True)
+    inputs, grads = device_inputs(rows, hidden, branch_dtype, seed=rows + 7 * hidden)
+    if normalized_dtype is not None:
+        grads = (grads[0], grads[1].to(normalized_dtype))
+    torch.cuda.manual_seed(rows)
+    seed, offset = generator_state()
+    outputs = _C.residual_layer_norm_forward(*inputs, dropout_p, EPS, True, 128,
+                                             normalized_dtype=normalized_dtype)
+    gradients = _C.residual_layer_norm_backward(
+        grads[0], grads[1], outputs[0], inputs[2], outputs[2], outputs[3], outputs[4],
+        dropout_p, True, branch_dtype == torch.float16, 128, 64, 64, 1, True, branch_dtype)
+    check_full_tensor(inputs, grads, outputs, gradients, dropout_p, EPS, seed, offset,
+                      what=f"{rows} x {hidden}")
+    check_parameter_gradients(outputs[0], grads[1], gradients)
