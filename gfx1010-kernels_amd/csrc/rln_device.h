@@ -78,6 +78,15 @@
 #ifndef RLN_FWD_LARGE_MAX_BLOCKS
 #define RLN_FWD_LARGE_MAX_BLOCKS 24576
 #endif
+// Forward launches of multi-wave rows below these sizes (elements; the first
+// for rows of two or four waves, the second for eight) run a persistent grid
+// of eight waves per CU instead.
+#ifndef RLN_FWD_PERSISTENT_ELEMENTS
+#define RLN_FWD_PERSISTENT_ELEMENTS (1ll << 24)
+#endif
+#ifndef RLN_FWD_PERSISTENT_ELEMENTS_8
+#define RLN_FWD_PERSISTENT_ELEMENTS_8 (1ll << 27)
+#endif
 #ifndef RLN_BWD_MAX_BLOCKS
 #define RLN_BWD_MAX_BLOCKS 256
 #endif
@@ -109,6 +118,9 @@ constexpr int kBackwardThreads = RLN_BWD_THREADS;
 constexpr int64_t kForwardMaxBlocks = RLN_FWD_MAX_BLOCKS;
 constexpr int64_t kForwardLargeElements = RLN_FWD_LARGE_ELEMENTS;
 constexpr int64_t kForwardLargeMaxBlocks = RLN_FWD_LARGE_MAX_BLOCKS;
+constexpr int64_t kForwardPersistentElements = RLN_FWD_PERSISTENT_ELEMENTS;
+constexpr int64_t kForwardPersistentElements8 = RLN_FWD_PERSISTENT_ELEMENTS_8;
+constexpr int kForwardPersistentWavesPerCu = 8;
 constexpr int64_t kBackwardMaxBlocks = RLN_BWD_MAX_BLOCKS;
 constexpr int64_t kPacedElements = RLN_PACED_ELEMENTS;
 constexpr int64_t kPacedMinHidden = RLN_PACED_MIN_HIDDEN;
@@ -311,58 +323,6 @@ inline int64_t launch_blocks(int64_t rows, const ShapeInfo& info, int threads, i
     return blocks < cap ? blocks : cap;
 }
 
-// Small forward launches give each team at least two row steps so that its
-// look-ahead load overlaps a row's computation, with at most 2048 blocks,
-// and then a whole number of blocks per CU (`cus`, the device's compute
-// units; 0 = unknown): a launch whose block count is not a multiple of the
-// CU count leaves some CUs one block more, which then run alone at the end
-// (measured on MI355X: the C4 tail, [12291, 384], forward 14.8 us at 769
-// blocks, 14.1 us at 768). Rows owned by one whole wave of a specialized size
-// (768 and 1024 columns) run at most three blocks per CU: C1 [8192, 768]
-// 17.1 us against 17.4 us at four and 17.8 us at 2048 (one step per team);
-// the narrower shapes, two or four rows per wave, measured best at their own
-// count. Large launches (2^23 elements and up) instead run one row step per
-// team (two for eight-wave rows), up to 24576 blocks, again a whole number per
-// CU: the hardware keeps as many of them resident as registers allow and
-// starts the next as one ends, which streams faster than fewer teams walking
-// many rows. Measured at 262144 rows (forward, us, the small-launch grid
-// against one step per team, alternated in one run where marked *): H = 128
-// 99 -> 92, 256 179 -> 159, 384 258 -> 238, 512 352 -> 317, 768 541-550 ->
-// 491-495 *, 1024 681-758 -> 652-653 *; [65536, 1024] 166-169 -> 159 *,
-// [65536, 256] 44.7 -> 40.2, [16384, 768] 32.4 -> 31.9; run-time rows of
-// 640-4096 columns 3-6 % faster. Eight-wave rows (4097-8192 columns, one row
-// per 512-thread block and few blocks per CU) need the look-ahead of a second
-// step: one step per team took 387 us at [16384, 8192] against 321-342 us for
-// the persistent grid, two steps 331-334 us against 338-341 us alternated in
-// one run ([26214, 5120]: 328 us against 335 us). Every output of the forward is a
-// function of its row alone (the dropout mask of (seed, offset, row,
-// column)), so its grid may depend on the device.
-template <typename S>
-int64_t forward_blocks(int64_t rows, int64_t hidden, int cus) {
-    int64_t blocks;
-    if (rows * hidden >= kForwardLargeElements) {
-        blocks = launch_blocks(rows, info_of<S>(), S::kForwardThreads, kForwardLargeMaxBlocks,
-                               S::kParts < 8 ? 1 : 2);
-    } else {
-        blocks = launch_blocks(rows, info_of<S>(), S::kForwardThreads, kForwardMaxBlocks,
-                               RLN_FWD_GROUPS_PER_WAVE);
-        if (cus > 0 && S::kHidden > 0 && S::kLanes == kWaveSize && blocks > 3 * cus) {
-            blocks = 3 * cus;
-        }
-    }
-    if (cus > 0 && blocks > cus) {
-        blocks -= blocks % cus;
-    }
-    return blocks;
-}
-
-// The backward's grid is also the number of weight/bias partials: at most
-// 256 blocks of 8 waves (12 for three-wave rows), one block per CU.
-inline int64_t backward_blocks(int64_t rows, int64_t hidden) {
-    const ShapeInfo info = shape_info(hidden, Pass::kBackward, rows);
-    return launch_blocks(rows, info, info.backward_threads, kBackwardMaxBlocks, 1);
-}
-
 // 1 if a launch over rows x hidden walks its rows paced, 0 for look-ahead.
 // Measured on MI355X: paced is faster from about 8 M elements for one-wave
 // rows of 256 or more columns (backward up to 12 % at 200 M elements), and
@@ -385,6 +345,91 @@ inline int forward_paced(int64_t rows, int64_t hidden) {
 inline int backward_paced(int64_t rows, int64_t hidden) {
     return hidden >= kPacedMinHidden && rows * hidden >= kPacedElements
         && shape_info(hidden, Pass::kBackward, rows).parts == 1 ? 1 : 0;
+}
+
+// Small forward launches give each team at least two row steps so that its
+// look-ahead load overlaps a row's computation, with at most 2048 blocks,
+// and then a whole number of blocks per CU (`cus`, the device's compute
+// units; 0 = unknown): a launch whose block count is not a multiple of the
+// CU count leaves some CUs one block more, which then run alone at the end
+// (measured on MI355X: the C4 tail, [12291, 384], forward 14.8 us at 769
+// blocks, 14.1 us at 768). Rows owned by one whole wave of a specialized size
+// (768 and 1024 columns) run at most three blocks per CU: C1 [8192, 768]
+// 17.1 us against 17.4 us at four and 17.8 us at 2048 (one step per team);
+// the narrower shapes, two or four rows per wave, measured best at their own
+// count. Large launches (2^23 elements and up) instead run one row step per
+// team (two for eight-wave rows), up to 24576 blocks, again a whole number per
+// CU: the hardware keeps as many of them resident as registers allow and
+// starts the next as one ends, which streams faster than fewer teams walking
+// many rows. Measured at 262144 rows (forward, us, the small-launch grid
+// against one step per team, alternated in one run where marked *): H = 128
+// 99 -> 92, 256 179 -> 159, 384 258 -> 238, 512 352 -> 317, 768 541-550 ->
+// 491-495 *, 1024 681-758 -> 652-653 *; [65536, 1024] 166-169 -> 159 *,
+// [65536, 256] 44.7 -> 40.2, [16384, 768] 32.4 -> 31.9; run-time rows of
+// 640-4096 columns 3-6 % faster. Eight-wave rows (4097-8192 columns, one row
+// per 512-thread block and few blocks per CU) need the look-ahead of a second
+// step: one step per team took 387 us at [16384, 8192] against 321-342 us for
+// the small-launch grid, two steps 331-334 us against 338-341 us alternated in
+// one run ([26214, 5120]: 328 us against 335 us).
+//
+// Multi-wave rows (1025-8192 columns) below 2^24 elements (2^27 for eight-wave
+// rows walked with look-ahead) run neither grid but a persistent one of eight
+// waves per CU - two blocks of four waves, or one of eight - each team
+// walking its rows with look-ahead, or one block per row step when there are
+// fewer steps. The small-launch grid puts up to 2048 blocks of rows whose
+// kernels hold 124-163 VGPRs (3-4 resident blocks per CU, one for eight-wave
+// rows of four slots), so a few blocks run in a second round after the rest;
+// one step per team leaves the last round part-full. Measured on MI355X
+// (forward, us, the two grids above against the persistent one, alternated
+// in one run): [2048, 4096] 24.0 -> 22.5, [2730, 3072] 25.9 -> 22.1,
+// [4096, 2048] 23.6 -> 22.2, [4096, 1600] 21.6 -> 18.2, [5242, 1600] 26.2 ->
+// 23.3, [8192, 1600] 34.7 -> 33.6, [6553, 1280] 25.7 -> 22.9, [64, 4096] 6.2
+// -> 4.4; eight-wave rows [256, 8192] 9.0 -> 7.1, [4096, 8192] 84.5 -> 80.5,
+// [8192, 8192] 167.9 -> 161.5, [8192, 6144] 124.9 -> 120.0; within +-1.5 % at
+// most other sizes; slower by 2-3 % just below 2^24 for rows of 4096 and 2048
+// columns ([4095, 4096] 42.6 -> 43.4, [8191, 2048] 42.0 -> 43.1) and at
+// [3072, 2048] (16.5 -> 16.8), by 6 % at [1024, 6144] (17.5 -> 18.5); 2^24
+// elements and up one step per team is as fast or faster (2-6 % at 2^24 -
+// 2^25 for rows of 2048 and 4096 columns), and so are eight-wave rows walked
+// paced (4097-6144 columns from 2^26) and [16384, 8192] (332 against 340).
+// Twelve waves per CU were faster at a few sizes (2048 row steps) and slower
+// at most. Every output of the forward is a function of its row alone (the
+// dropout mask of (seed, offset, row, column)), so its grid may depend on
+// the device.
+template <typename S>
+int64_t forward_blocks(int64_t rows, int64_t hidden, int cus) {
+    const int64_t elements = rows * hidden;
+    if (S::kParts > 1 && cus > 0
+        && (S::kParts < 8 ? elements < kForwardPersistentElements
+                          : elements < kForwardPersistentElements8
+                                && forward_paced(rows, hidden) == 0)) {
+        const int64_t steps = launch_blocks(rows, info_of<S>(), S::kForwardThreads, INT64_MAX, 1);
+        const int64_t persistent =
+            static_cast<int64_t>(cus) * (kForwardPersistentWavesPerCu * kWaveSize / S::kForwardThreads);
+        return steps < persistent ? steps : persistent;
+    }
+    int64_t blocks;
+    if (elements >= kForwardLargeElements) {
+        blocks = launch_blocks(rows, info_of<S>(), S::kForwardThreads, kForwardLargeMaxBlocks,
+                               S::kParts < 8 ? 1 : 2);
+    } else {
+        blocks = launch_blocks(rows, info_of<S>(), S::kForwardThreads, kForwardMaxBlocks,
+                               RLN_FWD_GROUPS_PER_WAVE);
+        if (cus > 0 && S::kHidden > 0 && S::kLanes == kWaveSize && blocks > 3 * cus) {
+            blocks = 3 * cus;
+        }
+    }
+    if (cus > 0 && blocks > cus) {
+        blocks -= blocks % cus;
+    }
+    return blocks;
+}
+
+// The backward's grid is also the number of weight/bias partials: at most
+// 256 blocks of 8 waves (12 for three-wave rows), one block per CU.
+inline int64_t backward_blocks(int64_t rows, int64_t hidden) {
+    const ShapeInfo info = shape_info(hidden, Pass::kBackward, rows);
+    return launch_blocks(rows, info, info.backward_threads, kBackwardMaxBlocks, 1);
 }
 
 // ----------------------------------------------------------------------------

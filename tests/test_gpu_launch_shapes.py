@@ -1,13 +1,16 @@
-"""Both sides of the forward's launch-shape switch, every row class.
+"""Both sides of the forward's launch-shape switches, every row class.
 
-Forward launches below 2^23 elements run 2-3 persistent blocks per CU whose
-teams walk several rows; from 2^23 elements one row step per team (two for
-eight-wave rows) on up to 24576 blocks, rounded down to a whole number of
-blocks per CU, so that some teams take one step more. Each case runs a
-forward + backward just below and just above the switch, with ragged row
-counts, and checks every element against the oracle
-(parity.check_full_tensor): the whole mask bitwise, `updated` bitwise, the
-rest against float64 on the device, dW/db against a float64 reduction.
+Forward launches of one-wave rows below 2^23 elements run 2-3 blocks per CU
+whose teams walk several rows; from 2^23 elements one row step per team on up
+to 24576 blocks, rounded down to a whole number of blocks per CU, so that some
+teams take one step more. Multi-wave rows run a persistent grid of eight waves
+per CU (one block per row step when there are fewer) below 2^24 elements, or
+below 2^27 for eight-wave rows walked with look-ahead, and the one-step grid
+(two steps per team for eight-wave rows) above. Each case runs a forward +
+backward just below and just above a switch, with ragged row counts, and
+checks every element against the oracle (parity.check_full_tensor): the whole
+mask bitwise, `updated` bitwise, the rest against float64 on the device, dW/db
+against a float64 reduction.
 """
 
 import pytest
@@ -49,6 +52,57 @@ def test_forward_grid_switch(hidden, below, above, branch_dtype, side):
         grads[0], grads[1], outputs[0], inputs[2], outputs[2], outputs[3], outputs[4], 0.1, True,
         branch_dtype == torch.float16, 128, 64, 64, 1, True, branch_dtype)
     assert gradients[1].dtype == branch_dtype
+    check_full_tensor(inputs, grads, outputs, gradients, 0.1, EPS, seed, offset,
+                      what=f"{rows} x {hidden}")
+    check_parameter_gradients(outputs[0], grads[1], gradients)
+
+
+# (hidden, rows below, rows above, branch type) around the multi-wave switches:
+# rows of two and four waves at 2^24 elements (ragged and whole slots), eight
+# waves of three slots where their walk turns paced (2^26), eight waves of four
+# slots at 2^27.
+PERSISTENT_CASES = [
+    (2048, 8191, 8192, torch.float16),
+    (4096, 4095, 4096, torch.bfloat16),
+    (1600, 10485, 10486, torch.float16),
+    (6144, 10922, 10923, torch.float16),
+    (8192, 16383, 16384, torch.bfloat16),
+]
+PERSISTENT_SWITCH = {2048: 1 << 24, 4096: 1 << 24, 1600: 1 << 24, 6144: 1 << 26, 8192: 1 << 27}
+
+
+@pytest.mark.parametrize("side", ["below", "above"])
+@pytest.mark.parametrize("hidden,below,above,branch_dtype", PERSISTENT_CASES,
+                         ids=[f"H{case[0]}" for case in PERSISTENT_CASES])
+def test_multi_wave_persistent_switch(hidden, below, above, branch_dtype, side):
+    rows = below if side == "below" else above
+    assert (rows * hidden >= PERSISTENT_SWITCH[hidden]) == (side == "above")
+    print(f"[launch shapes] rows={rows} H={hidden} {branch_dtype}", flush=True)
+    inputs, grads = device_inputs(rows, hidden, branch_dtype, seed=5 * hidden + rows)
+    torch.cuda.manual_seed(5 * hidden + rows)
+    seed, offset = generator_state()
+    outputs = _C.residual_layer_norm_forward(*inputs, 0.1, EPS, True, 128)
+    gradients = _C.residual_layer_norm_backward(
+        grads[0], grads[1], outputs[0], inputs[2], outputs[2], outputs[3], outputs[4], 0.1, True,
+        branch_dtype == torch.float16, 128, 64, 64, 1, True, branch_dtype)
+    check_full_tensor(inputs, grads, outputs, gradients, 0.1, EPS, seed, offset,
+                      what=f"{rows} x {hidden}")
+    check_parameter_gradients(outputs[0], grads[1], gradients)
+
+
+@pytest.mark.parametrize("hidden,rows", [(4096, 1), (4096, 64), (2048, 1001), (8192, 3),
+                                         (8192, 255), (6144, 257), (1280, 513)])
+def test_multi_wave_fewer_steps_than_the_persistent_grid(hidden, rows):
+    """Row counts that give the persistent grid fewer row steps than its eight
+    waves per CU (one block per step), and just past one or two blocks per CU."""
+    print(f"[launch shapes] rows={rows} H={hidden}", flush=True)
+    inputs, grads = device_inputs(rows, hidden, torch.float16, seed=7 * hidden + rows)
+    torch.cuda.manual_seed(7 * hidden + rows)
+    seed, offset = generator_state()
+    outputs = _C.residual_layer_norm_forward(*inputs, 0.1, EPS, True, 128)
+    gradients = _C.residual_layer_norm_backward(
+        grads[0], grads[1], outputs[0], inputs[2], outputs[2], outputs[3], outputs[4], 0.1, True,
+        True, 128, 64, 64, 1, True, torch.float16)
     check_full_tensor(inputs, grads, outputs, gradients, 0.1, EPS, seed, offset,
                       what=f"{rows} x {hidden}")
     check_parameter_gradients(outputs[0], grads[1], gradients)
