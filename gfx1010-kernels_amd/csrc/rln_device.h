@@ -357,7 +357,14 @@ inline int backward_paced(int64_t rows, int64_t hidden) {
 // (768 and 1024 columns) run at most three blocks per CU: C1 [8192, 768]
 // 17.1 us against 17.4 us at four and 17.8 us at 2048 (one step per team);
 // the narrower shapes, two or four rows per wave, measured best at their own
-// count. Large launches (2^23 elements and up) instead run one row step per
+// count. A count between one and two rounds of the blocks a CU holds at once
+// (`resident`, asked of the runtime for the kernel instance) becomes one
+// round, so that no part-full second round runs after the first: measured
+// (us, alternated in one run) [16383, 512] 25.3 -> 21.8, [8192, 640] 17.0 ->
+// 14.3, [24576, 256] 19.8 -> 17.4, [21845, 384] 25.7 -> 23.9, [8738, 960]
+// 26.5 -> 24.6, [49152, 128] 21.6 -> 20.8, and [65535, 128] 26.9 -> 27.6;
+// [4096, 768], [8192, 768] and [12291, 384] stay below one round, unchanged.
+// Large launches (2^23 elements and up) instead run one row step per
 // team (two for eight-wave rows), up to 24576 blocks, again a whole number per
 // CU: the hardware keeps as many of them resident as registers allow and
 // starts the next as one ends, which streams faster than fewer teams walking
@@ -397,7 +404,7 @@ inline int backward_paced(int64_t rows, int64_t hidden) {
 // dropout mask of (seed, offset, row, column)), so its grid may depend on
 // the device.
 template <typename S>
-int64_t forward_blocks(int64_t rows, int64_t hidden, int cus) {
+int64_t forward_blocks(int64_t rows, int64_t hidden, int cus, int resident) {
     const int64_t elements = rows * hidden;
     if (S::kParts > 1 && cus > 0
         && (S::kParts < 8 ? elements < kForwardPersistentElements
@@ -417,6 +424,12 @@ int64_t forward_blocks(int64_t rows, int64_t hidden, int cus) {
                                RLN_FWD_GROUPS_PER_WAVE);
         if (cus > 0 && S::kHidden > 0 && S::kLanes == kWaveSize && blocks > 3 * cus) {
             blocks = 3 * cus;
+        }
+        // No part-full second round: between one and two rounds of resident
+        // blocks, one round.
+        const int64_t round = static_cast<int64_t>(resident) * cus;
+        if (round > 0 && blocks > round && blocks < 2 * round) {
+            blocks = round;
         }
     }
     if (cus > 0 && blocks > cus) {
@@ -1396,10 +1409,27 @@ int check_shape(const S& shape, Pass pass, int64_t rows) {
     return RLN_OK;
 }
 
+// Blocks of one forward kernel instance a CU holds at once (registers and
+// LDS permitting), asked of the runtime once per instance; 0 if it cannot say.
+template <typename S, typename B, typename N, bool Aligned>
+int forward_resident_blocks() {
+    static const int resident = [] {
+        int blocks = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &blocks, reinterpret_cast<const void*>(&rln_forward_kernel<S, B, N, Aligned>),
+                S::kForwardThreads, 0) != hipSuccess) {
+            hipGetLastError();
+            return 0;
+        }
+        return blocks;
+    }();
+    return resident;
+}
+
 template <typename S, typename B, typename N, bool Aligned>
 int launch_forward(const ForwardArgs& a, S shape) {
-    const dim3 grid(
-        static_cast<unsigned>(forward_blocks<S>(a.rows, shape.hidden(), a.compute_units)));
+    const dim3 grid(static_cast<unsigned>(forward_blocks<S>(
+        a.rows, shape.hidden(), a.compute_units, forward_resident_blocks<S, B, N, Aligned>())));
     rln_forward_kernel<S, B, N, Aligned><<<grid, S::kForwardThreads, 0, a.stream>>>(
         a.x,
         static_cast<const B*>(a.branch),

@@ -96,3 +96,60 @@ def test_captured_calls_draw_the_reference_stream_at_consecutive_offsets(hidden,
             check_forward(output, inputs, 0.2, True, EPS, seed, offset + index * increment,
                           f"replay {replay} call {index}", threads=threads)
         assert generator_state()[1] == offset + 2 * increment
+
+
+FIRST_CALL_UNDER_CAPTURE = r"""
+import sys
+import torch
+sys.path.insert(0, sys.argv[1])
+from gfx1010_kernels import _C
+
+rows, hidden = 3001, 896
+generator = torch.Generator(device="cuda").manual_seed(5)
+x = torch.randn(rows, hidden, device="cuda", generator=generator)
+branch = torch.randn(rows, hidden, device="cuda", generator=generator).half()
+weight = torch.randn(hidden, device="cuda", generator=generator)
+bias = torch.randn(hidden, device="cuda", generator=generator)
+grad = torch.randn(rows, hidden, device="cuda", generator=generator)
+torch.cuda.synchronize()
+
+def step():
+    out = _C.residual_layer_norm_forward(x, branch, weight, bias, 0.0, 1e-5, True, 128)
+    grads = _C.residual_layer_norm_backward(grad, grad, out[0], weight, out[2], out[3], out[4],
+                                            0.0, True, True, 128, 64, 64, 1, True)
+    return out, grads
+
+graph = torch.cuda.CUDAGraph()
+side = torch.cuda.Stream()
+side.wait_stream(torch.cuda.current_stream())
+with torch.cuda.stream(side):
+    with torch.cuda.graph(graph, stream=side):
+        captured = step()
+torch.cuda.current_stream().wait_stream(side)
+for replay in range(3):
+    graph.replay()
+    torch.cuda.synchronize()
+    eager = step()
+    torch.cuda.synchronize()
+    for a, b in zip(list(captured[0][:4]) + list(captured[1][:2]),
+                    list(eager[0][:4]) + list(eager[1][:2])):
+        assert torch.equal(a, b), f"replay {replay} differs from the eager call"
+print("first call under capture: ok", flush=True)
+"""
+
+
+def test_first_call_of_a_process_under_capture():
+    """The first forward and backward of a process captured into a graph: the
+    library's one-time device queries (compute units, the forward kernel's
+    resident blocks per CU) then run during capture, and must neither break
+    it nor change results (replays against eager calls, bitwise; p = 0)."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    package = Path(__file__).resolve().parents[1] / "gfx1010-kernels_amd"
+    print("[graphs] first call under capture (child process)", flush=True)
+    result = subprocess.run([sys.executable, "-c", FIRST_CALL_UNDER_CAPTURE, str(package)],
+                            capture_output=True, text=True, timeout=240)
+    assert result.returncode == 0, result.stdout + result.stderr
+    assert "first call under capture: ok" in result.stdout
