@@ -362,8 +362,17 @@ inline int backward_paced(int64_t rows, int64_t hidden) {
 // round, so that no part-full second round runs after the first: measured
 // (us, alternated in one run) [16383, 512] 25.3 -> 21.8, [8192, 640] 17.0 ->
 // 14.3, [24576, 256] 19.8 -> 17.4, [21845, 384] 25.7 -> 23.9, [8738, 960]
-// 26.5 -> 24.6, [49152, 128] 21.6 -> 20.8, and [65535, 128] 26.9 -> 27.6;
-// [4096, 768], [8192, 768] and [12291, 384] stay below one round, unchanged.
+// 26.5 -> 24.6, [49152, 128] 21.6 -> 20.8, and [65535, 128] 26.9 -> 27.6.
+// Rows of two or four per wave (128-512 columns) also run one round when
+// they have at least a round of row steps, where two steps per team and the
+// rounding to whole blocks per CU left fewer blocks: [6144, 512] 13.0 ->
+// 8.4, [8192, 512] 12.3 -> 10.7, [10240, 256] 10.9 -> 7.6, [16384, 256] 13.6
+// -> 11.6, [32768, 128] 16.2 -> 13.1, [8192, 384] 10.4 -> 8.3; [12291, 384]
+// 13.6 -> 13.0 (fp16 branch, p = 0.1), and with an fp32 branch (the C4 tail)
+// 14.0 -> 14.3 at p = 0 (step 34.8 -> 35.0) and 14.8 -> 14.6 at p = 0.1
+// (step 35.2 -> 35.0). Rows of one wave stay at their count: [4096, 768] at
+// one round was 7 % slower, and [8192, 768] at four blocks per CU runs its
+// forward 0.4 us faster but the forward + backward step 0.3 us slower.
 // Large launches (2^23 elements and up) instead run one row step per
 // team (two for eight-wave rows), up to 24576 blocks, again a whole number per
 // CU: the hardware keeps as many of them resident as registers allow and
@@ -429,6 +438,12 @@ int64_t forward_blocks(int64_t rows, int64_t hidden, int cus, int resident) {
         // blocks, one round.
         const int64_t round = static_cast<int64_t>(resident) * cus;
         if (round > 0 && blocks > round && blocks < 2 * round) {
+            blocks = round;
+        }
+        // Rows of two or four per wave with a round's worth of row steps: one
+        // round.
+        if (round > 0 && S::kRowsPerWave > 1 && blocks < round
+            && launch_blocks(rows, info_of<S>(), S::kForwardThreads, INT64_MAX, 1) >= round) {
             blocks = round;
         }
     }

@@ -108,6 +108,27 @@ def test_multi_wave_fewer_steps_than_the_persistent_grid(hidden, rows):
     check_parameter_gradients(outputs[0], grads[1], gradients)
 
 
+@pytest.mark.parametrize("hidden,rows,branch_dtype", [
+    (512, 6144, torch.float16), (256, 10240, torch.bfloat16), (128, 32768, torch.float16),
+    (384, 8192, torch.float32), (512, 16383, torch.float16), (640, 8192, torch.float16),
+    (960, 8738, torch.bfloat16)], ids=lambda v: str(v).replace("torch.", ""))
+def test_small_launches_at_one_round_of_resident_blocks(hidden, rows, branch_dtype):
+    """Small forwards whose grid is one round of the blocks a CU holds at once
+    (raised to it for rows of two or four per wave, lowered to it from between
+    one and two rounds), whole tensors."""
+    print(f"[launch shapes] rows={rows} H={hidden} {branch_dtype}", flush=True)
+    inputs, grads = device_inputs(rows, hidden, branch_dtype, seed=11 * hidden + rows)
+    torch.cuda.manual_seed(11 * hidden + rows)
+    seed, offset = generator_state()
+    outputs = _C.residual_layer_norm_forward(*inputs, 0.1, EPS, True, 128)
+    gradients = _C.residual_layer_norm_backward(
+        grads[0], grads[1], outputs[0], inputs[2], outputs[2], outputs[3], outputs[4], 0.1, True,
+        branch_dtype == torch.float16, 128, 64, 64, 1, True, branch_dtype)
+    check_full_tensor(inputs, grads, outputs, gradients, 0.1, EPS, seed, offset,
+                      what=f"{rows} x {hidden}")
+    check_parameter_gradients(outputs[0], grads[1], gradients)
+
+
 @pytest.mark.parametrize("hidden,rows,branch_dtype,normalized_dtype", [
     (768, 10923, torch.bfloat16, torch.bfloat16),
     (256, 32769, torch.float16, torch.float16),
