@@ -1,9 +1,10 @@
 """Both sides of the forward's launch-shape switches, every row class.
 
-Forward launches of one-wave rows below 2^23 elements run 2-3 blocks per CU
-whose teams walk several rows; from 2^23 elements one row step per team on up
-to 24576 blocks, rounded down to a whole number of blocks per CU, so that some
-teams take one step more. Multi-wave rows run a persistent grid of eight waves
+Forward launches of one-wave rows below 2^23 elements run 2-5 blocks per CU
+whose teams walk several rows (2^24 for the four-slot rows of 512 and 1024
+columns); above, one row step per team on up to 24576 blocks, rounded down to
+a whole number of blocks per CU, so that some teams take one step more.
+Multi-wave rows run a persistent grid of eight waves
 per CU (one block per row step when there are fewer) below 2^24 elements, or
 below 2^27 for eight-wave rows walked with look-ahead, and the one-step grid
 (two steps per team for eight-wave rows) above. Each case runs a forward +
@@ -57,24 +58,30 @@ def test_forward_grid_switch(hidden, below, above, branch_dtype, side):
     check_parameter_gradients(outputs[0], grads[1], gradients)
 
 
-# (hidden, rows below, rows above, branch type) around the multi-wave switches:
-# rows of two and four waves at 2^24 elements (ragged and whole slots), eight
-# waves of three slots where their walk turns paced (2^26), eight waves of four
-# slots at 2^27.
+# (hidden, rows below, rows above, branch type) around the switches from a
+# persistent grid to one step per team: rows of two and four waves at 2^24
+# elements (ragged and whole slots), eight waves of three slots where their walk
+# turns paced (2^26), eight waves of four slots at 2^27, and the specialized
+# four-slot rows (512, 1024 columns) at 2^24.
 PERSISTENT_CASES = [
     (2048, 8191, 8192, torch.float16),
     (4096, 4095, 4096, torch.bfloat16),
     (1600, 10485, 10486, torch.float16),
     (6144, 10922, 10923, torch.float16),
     (8192, 16383, 16384, torch.bfloat16),
+    # specialized rows of four slots per lane: one round of resident blocks below
+    # 2^24 elements, one step per team above
+    (1024, 16383, 16385, torch.float16),
+    (512, 32767, 32768, torch.bfloat16),
 ]
-PERSISTENT_SWITCH = {2048: 1 << 24, 4096: 1 << 24, 1600: 1 << 24, 6144: 1 << 26, 8192: 1 << 27}
+PERSISTENT_SWITCH = {2048: 1 << 24, 4096: 1 << 24, 1600: 1 << 24, 6144: 1 << 26, 8192: 1 << 27,
+                     1024: 1 << 24, 512: 1 << 24}
 
 
 @pytest.mark.parametrize("side", ["below", "above"])
 @pytest.mark.parametrize("hidden,below,above,branch_dtype", PERSISTENT_CASES,
                          ids=[f"H{case[0]}" for case in PERSISTENT_CASES])
-def test_multi_wave_persistent_switch(hidden, below, above, branch_dtype, side):
+def test_persistent_grid_switch(hidden, below, above, branch_dtype, side):
     rows = below if side == "below" else above
     assert (rows * hidden >= PERSISTENT_SWITCH[hidden]) == (side == "above")
     print(f"[launch shapes] rows={rows} H={hidden} {branch_dtype}", flush=True)
