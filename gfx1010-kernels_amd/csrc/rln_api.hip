@@ -109,14 +109,14 @@ int compute_units() {
     static int units[kMaxDevices];
     int device = -1;
     if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) {
-        hipGetLastError();
+        static_cast<void>(hipGetLastError());  // clear the failed call's error
         return 0;
     }
     std::call_once(once[device], [device] {
         int count = 0;
         if (hipDeviceGetAttribute(&count, hipDeviceAttributeMultiprocessorCount, device)
             != hipSuccess) {
-            hipGetLastError();
+            static_cast<void>(hipGetLastError());  // clear the failed call's error
             count = 0;
         }
         units[device] = count;

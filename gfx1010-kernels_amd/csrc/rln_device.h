@@ -1447,7 +1447,7 @@ int forward_resident_blocks() {
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
                 &blocks, reinterpret_cast<const void*>(&rln_forward_kernel<S, B, N, Aligned>),
                 S::kForwardThreads, 0) != hipSuccess) {
-            hipGetLastError();
+            static_cast<void>(hipGetLastError());  // clear the failed call's error
             return 0;
         }
         return blocks;
