@@ -281,8 +281,10 @@ def residual_layer_norm(
         if status.architecture == TARGET_ARCHITECTURE:
             raise RuntimeError(f"{_UNAVAILABLE}: {status.reason}")
         return _fall_back(status.reason, *args)
-    with torch.cuda.device(x.device):
-        return native_residual_layer_norm(
-            x, branch, weight, bias, float(dropout_p), float(eps), bool(training),
-            normalized_dtype=normalized_dtype,
-        )
+    # The extension guards x's device itself (the reference wraps this call in
+    # torch.cuda.device, normalization.py:289, which costs two device switches
+    # per call here).
+    return native_residual_layer_norm(
+        x, branch, weight, bias, float(dropout_p), float(eps), bool(training),
+        normalized_dtype=normalized_dtype,
+    )
