@@ -1156,12 +1156,16 @@ def gbps(nbytes: int, ms: float) -> float:
 SPECIALIZED_HIDDEN = (128, 256, 384, 512, 768, 1024)
 
 
-def wide_parts(hidden: int, kernel: str) -> int:
-    """Waves per row of a run-time row length (rln_device.h wide_parts)."""
+def wide_parts(hidden: int, kernel: str, rows: int = 0) -> int:
+    """Waves per row of a run-time row length (rln_device.h wide_parts, and
+    shape_info's sixteen-wave backward of large launches)."""
     if kernel == "rln_forward_kernel":
         return 1 if hidden <= 1024 else 2 if hidden <= 2048 else 4 if hidden <= 4096 else 8
-    return (1 if hidden <= 704 else 3 if hidden <= 768 else 4 if hidden <= 1024 else
-            2 if hidden <= 1216 else 4 if hidden <= 2432 else 8)
+    parts = (1 if hidden <= 704 else 3 if hidden <= 768 else 4 if hidden <= 1024 else
+             2 if hidden <= 1216 else 4 if hidden <= 2432 else 8)
+    if parts == 8 and hidden >= 6657 and rows * hidden >= 1 << 26:
+        return 16
+    return parts
 
 
 def kernel_name(kernel: str, workload: Workload) -> str:
@@ -1170,7 +1174,8 @@ def kernel_name(kernel: str, workload: Workload) -> str:
     aligned access path. Mirrors the dispatch of rln_device.h: the specialized
     sizes' lanes per row (the forward's forward_lanes), and the run-time-length
     shapes each pass runs, 1024's backward and that of 768 columns from 65536
-    rows among them (backward_runs_wide)."""
+    rows among them (backward_runs_wide), and the sixteen-wave backward of
+    large launches of 6657-8192 columns."""
     forward = kernel == "rln_forward_kernel"
     hidden = workload.hidden
     runs_wide = hidden == 1024 or (hidden == 768 and workload.rows >= 65536)
@@ -1180,7 +1185,7 @@ def kernel_name(kernel: str, workload: Workload) -> str:
             lanes = {128: 16, 768: 64, 1024: 64}.get(hidden, 32)
         shape = f"rln::FixedShape<{hidden}, {lanes}>"
     else:
-        parts = wide_parts(hidden, kernel)
+        parts = wide_parts(hidden, kernel, workload.rows)
         vectors = -(-hidden // (256 * parts))
         shape = f"rln::WideShape<{vectors}, {parts}>"
     types = {"f32": "float", "f16": "_Float16", "bf16": "__bf16"}

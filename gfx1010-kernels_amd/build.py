@@ -57,13 +57,14 @@ HIP_FLAGS = [
 # the run-time-length kernels that serve every other multiple of 64 up to
 # 8192, per pass (the lists RLN_FOR_EACH_WIDE_FORWARD / _BACKWARD in
 # rln_device.h; the link fails on a pair missing here). The backward of 1024
-# columns runs the (1, 4) run-time-length kernel, and that of large 768-column
-# launches the (1, 3) one (backward_runs_wide).
+# columns runs the (1, 4) run-time-length kernel, that of large 768-column
+# launches the (1, 3) one (backward_runs_wide), and that of large launches of
+# 6657-8192 columns the (2, 16) one.
 HIDDEN_SIZES = (128, 256, 384, 512, 768, 1024)
 FIXED_BACKWARD = (128, 256, 384, 512, 768)
 WIDE_FORWARD = ((1, 1), (2, 1), (3, 1), (4, 1), (3, 2), (4, 2), (3, 4), (4, 4), (3, 8), (4, 8))
 WIDE_BACKWARD = ((1, 1), (2, 1), (3, 1), (1, 3), (1, 4), (3, 2), (2, 4), (3, 4), (2, 8), (3, 8),
-                 (4, 8))
+                 (4, 8), (2, 16))
 BUILD_DIR = ROOT / "_build"
 
 

@@ -212,11 +212,13 @@ struct WideShape {
     static constexpr int kRowsPerWave = 1;
     static constexpr bool kRagged = true;
     // Three-wave rows (the backward of large 768-column launches) run in
-    // 12-wave blocks, so that a block still holds whole rows and the grid
-    // keeps one weight/bias partial per CU.
+    // 12-wave blocks and sixteen-wave rows (the backward of large launches of
+    // 6657-8192 columns) in 16-wave blocks, so that a block still holds whole
+    // rows and the grid keeps one weight/bias partial per CU.
     static constexpr int kForwardThreads = P == 3 ? 6 * kWaveSize : P > 4 ? P * kWaveSize : 256;
-    static constexpr int kBackwardBlockThreads = P == 3 ? 12 * kWaveSize : kBackwardThreads;
-    static_assert(P == 1 || P == 2 || P == 3 || P == 4 || P == 8, "parts per row");
+    static constexpr int kBackwardBlockThreads =
+        P == 3 ? 12 * kWaveSize : P == 16 ? 16 * kWaveSize : kBackwardThreads;
+    static_assert(P == 1 || P == 2 || P == 3 || P == 4 || P == 8 || P == 16, "parts per row");
     int64_t hidden_;
     float inv_hidden_;  // 1.0f / hidden, rounded once on the host
     __host__ __device__ int64_t hidden() const { return hidden_; }
@@ -296,6 +298,15 @@ inline bool backward_runs_wide(int64_t hidden, int64_t rows) {
     return hidden == 1024 || (hidden == 768 && rows >= kWide768BackwardRows);
 }
 
+// Backward launches of at least this many elements run rows of 6657-8192
+// columns on sixteen waves of two slots (1024-thread blocks) instead of eight
+// of four: measured 2-4.5 % faster from 2^26 elements ([16384, 8192] 416
+// against 424-436 us, [18724, 7168] 425-427 against 437-441 us, [8192, 8192]
+// 209 against 212-214 us, alternated in one run), and 1-4.5 % slower at
+// 2^24-2^25; equal at 6656 columns.
+constexpr int64_t kSixteenWaveBackwardElements = 1ll << 26;
+constexpr int64_t kSixteenWaveBackwardMinHidden = 6657;
+
 // The shape of a supported hidden size in one pass over `rows`.
 inline ShapeInfo shape_info(int64_t hidden, Pass pass, int64_t rows) {
     if (specialized_hidden(hidden)
@@ -304,11 +315,15 @@ inline ShapeInfo shape_info(int64_t hidden, Pass pass, int64_t rows) {
         return {kWaveSize / lanes, 1, static_cast<int>(hidden / 4 / lanes), 256,
                 kBackwardThreads};
     }
-    const int parts = wide_parts(hidden, pass);
+    int parts = wide_parts(hidden, pass);
+    if (pass == Pass::kBackward && parts == 8 && hidden >= kSixteenWaveBackwardMinHidden
+        && rows * hidden >= kSixteenWaveBackwardElements) {
+        parts = 16;
+    }
     const int64_t per_slot = 4 * kWaveSize * parts;
     const int vectors = static_cast<int>((hidden + per_slot - 1) / per_slot);
     return {1, parts, vectors, parts == 3 ? 6 * kWaveSize : parts > 4 ? parts * kWaveSize : 256,
-            parts == 3 ? 12 * kWaveSize : kBackwardThreads};
+            parts == 3 ? 12 * kWaveSize : parts == 16 ? 16 * kWaveSize : kBackwardThreads};
 }
 
 // Blocks for a launch over `rows`: each block works on
@@ -1178,12 +1193,17 @@ void rln_backward_kernel(
     const bool dropout = flags & kDropout;
     const bool parameters = flags & kParameters;
 
-    f32x4 w[V];
+    // Sixteen-wave blocks (128 VGPRs) read the weight per row instead of
+    // holding it: 4 VGPRs spilled instead of 15.
+    constexpr bool kWeightPerRow = P == 16;
+    f32x4 held_weight[kWeightPerRow ? 1 : V];
     f32x4 acc_w[V];
     f32x4 acc_b[V];
 #pragma unroll
     for (int v = 0; v < V; ++v) {
-        w[v] = load_parameter4<Aligned>(weight + slots.column(v));
+        if constexpr (!kWeightPerRow) {
+            held_weight[v] = load_parameter4<Aligned>(weight + slots.column(v));
+        }
         acc_w[v] = zero4();
         acc_b[v] = zero4();
     }
@@ -1220,6 +1240,15 @@ void rln_backward_kernel(
 
     // Input gradients of one row and its contribution to the parameter sums.
     auto process_row = [&](const BackwardRow<V, GY>& r, int64_t row) {
+        f32x4 w[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+            if constexpr (kWeightPerRow) {
+                w[v] = load_parameter4<Aligned>(weight + slots.column(v));
+            } else {
+                w[v] = held_weight[v];
+            }
+        }
         const bool valid = row < rows;
         const int64_t base = row * hidden;
         f32x4 xhat[V];
@@ -1563,7 +1592,8 @@ int launch_backward_shape(const BackwardArgs& a, S shape, int branch_dtype,
 #define RLN_FOR_EACH_WIDE_FORWARD(X) \
     X(1, 1) X(2, 1) X(3, 1) X(4, 1) X(3, 2) X(4, 2) X(3, 4) X(4, 4) X(3, 8) X(4, 8)
 #define RLN_FOR_EACH_WIDE_BACKWARD(X) \
-    X(1, 1) X(2, 1) X(3, 1) X(1, 3) X(1, 4) X(3, 2) X(2, 4) X(3, 4) X(2, 8) X(3, 8) X(4, 8)
+    X(1, 1) X(2, 1) X(3, 1) X(1, 3) X(1, 4) X(3, 2) X(2, 4) X(3, 4) X(2, 8) X(3, 8) X(4, 8) \
+    X(2, 16)
 
 #define RLN_WIDE_CASE(V, P) \
     case P * 16 + V: return launch(WideShape<V, P>{hidden, inv_hidden});

@@ -197,3 +197,58 @@ def test_seeded_random_shapes_above_the_switch(rows, hidden, branch_dtype, norma
     check_full_tensor(inputs, grads, outputs, gradients, dropout_p, EPS, seed, offset,
                       what=f"{rows} x {hidden}")
     check_parameter_gradients(outputs[0], grads[1], gradients)
+
+
+# (hidden, rows below 2^26 elements, rows at or above, branch type): the
+# backward's switch from eight waves of four slots to sixteen waves of two for
+# rows of 6657-8192 columns.
+SIXTEEN_WAVE_CASES = [
+    (8192, 8191, 8192, torch.float16),
+    (7168, 9362, 9363, torch.bfloat16),
+    (6720, 9986, 9987, torch.float32),
+]
+
+
+@pytest.mark.parametrize("side", ["below", "above"])
+@pytest.mark.parametrize("hidden,below,above,branch_dtype", SIXTEEN_WAVE_CASES,
+                         ids=[f"H{case[0]}" for case in SIXTEEN_WAVE_CASES])
+def test_sixteen_wave_backward_switch(hidden, below, above, branch_dtype, side):
+    rows = below if side == "below" else above
+    assert (rows * hidden >= 1 << 26) == (side == "above")
+    print(f"[launch shapes] rows={rows} H={hidden} {branch_dtype}", flush=True)
+    inputs, grads = device_inputs(rows, hidden, branch_dtype, seed=13 * hidden + rows)
+    torch.cuda.manual_seed(13 * hidden + rows)
+    seed, offset = generator_state()
+    outputs = _C.residual_layer_norm_forward(*inputs, 0.1, EPS, True, 128)
+    gradients = _C.residual_layer_norm_backward(
+        grads[0], grads[1], outputs[0], inputs[2], outputs[2], outputs[3], outputs[4], 0.1, True,
+        branch_dtype == torch.float16, 128, 64, 64, 1, True, branch_dtype)
+    check_full_tensor(inputs, grads, outputs, gradients, 0.1, EPS, seed, offset,
+                      what=f"{rows} x {hidden}")
+    check_parameter_gradients(outputs[0], grads[1], gradients)
+
+
+def test_sixteen_wave_backward_deterministic_and_half_gradient():
+    """The sixteen-wave backward's fixed-order weight/bias reduction (bitwise
+    equal over three runs) with a bf16 upstream gradient, whole tensors."""
+    from test_gpu_backward import deterministic_algorithms
+
+    rows, hidden = 8200, 8192
+    print(f"[launch shapes] deterministic rows={rows} H={hidden}", flush=True)
+    inputs, grads = device_inputs(rows, hidden, torch.bfloat16, seed=8200)
+    grads = (grads[0], grads[1].to(torch.bfloat16))
+    torch.cuda.manual_seed(8200)
+    seed, offset = generator_state()
+    outputs = _C.residual_layer_norm_forward(*inputs, 0.15, EPS, True, 128,
+                                             normalized_dtype=torch.bfloat16)
+    with deterministic_algorithms(True):
+        runs = [_C.residual_layer_norm_backward(
+            grads[0], grads[1], outputs[0], inputs[2], outputs[2], outputs[3], outputs[4], 0.15,
+            True, False, 128, 64, 64, 1, True, torch.bfloat16) for _ in range(3)]
+    for other in runs[1:]:
+        for a, b in zip(runs[0], other):
+            assert torch.equal(a.view(torch.int32) if a.dtype == torch.float32 else a,
+                               b.view(torch.int32) if b.dtype == torch.float32 else b)
+    check_full_tensor(inputs, grads, outputs, runs[0], 0.15, EPS, seed, offset,
+                      what=f"{rows} x {hidden} deterministic")
+    check_parameter_gradients(outputs[0], grads[1], runs[0])
