@@ -435,8 +435,18 @@ int64_t forward_blocks(int64_t rows, int64_t hidden, int cus, int resident) {
                           : elements < kForwardPersistentElements8
                                 && forward_paced(rows, hidden) == 0)) {
         const int64_t steps = launch_blocks(rows, info_of<S>(), S::kForwardThreads, INT64_MAX, 1);
-        const int64_t persistent =
-            static_cast<int64_t>(cus) * (kForwardPersistentWavesPerCu * kWaveSize / S::kForwardThreads);
+        int64_t per_cu = kForwardPersistentWavesPerCu * kWaveSize / S::kForwardThreads;
+        // Rows of two or four waves with more than 6 and at most 8 row steps
+        // per CU: twelve waves per CU (three blocks, when they fit). Measured
+        // (forward us, alternated in one run): [4096, 1280] 15.3 -> 14.0,
+        // [2048, 2560] 15.5 -> 14.3, [2048, 4096] 22.3 -> 21.6, [4096, 2048]
+        // 22.1 -> 21.2, [4096, 1600] 18.3 -> 18.0; at 9 steps per CU 2.5-3.5 %
+        // slower ([4608, 2048], [2304, 4096]) and at 6 mixed (+-2.7 %).
+        if (S::kParts < 8 && steps > 6 * static_cast<int64_t>(cus)
+            && steps <= 8 * static_cast<int64_t>(cus) && resident >= 3) {
+            per_cu = 3;
+        }
+        const int64_t persistent = static_cast<int64_t>(cus) * per_cu;
         return steps < persistent ? steps : persistent;
     }
     // Specialized rows of four slots per lane (512 and 1024 columns) keep one

@@ -98,10 +98,12 @@ def test_persistent_grid_switch(hidden, below, above, branch_dtype, side):
 
 
 @pytest.mark.parametrize("hidden,rows", [(4096, 1), (4096, 64), (2048, 1001), (8192, 3),
-                                         (8192, 255), (6144, 257), (1280, 513)])
-def test_multi_wave_fewer_steps_than_the_persistent_grid(hidden, rows):
+                                         (8192, 255), (6144, 257), (1280, 513),
+                                         (1280, 3074), (4096, 2048), (2560, 1537), (1600, 4097)])
+def test_multi_wave_persistent_grid_row_counts(hidden, rows):
     """Row counts that give the persistent grid fewer row steps than its eight
-    waves per CU (one block per step), and just past one or two blocks per CU."""
+    waves per CU (one block per step), just past one or two blocks per CU, and
+    inside the band of 6-8 row steps per CU that runs twelve waves per CU."""
     print(f"[launch shapes] rows={rows} H={hidden}", flush=True)
     inputs, grads = device_inputs(rows, hidden, torch.float16, seed=7 * hidden + rows)
     torch.cuda.manual_seed(7 * hidden + rows)
