@@ -117,3 +117,54 @@ def test_two_equal_dropout_calls_in_one_compiled_graph(backend):
     for index, (expected, actual) in enumerate(zip(eager, traced)):
         assert_bitwise(actual, expected, f"compiled output {index} vs eager")
     assert offsets[1] == offsets[0]
+
+
+def test_reduce_overhead_training_step_replays():
+    """torch.compile(mode="reduce-overhead"): inductor captures the compiled
+    training step, custom ops included, into CUDA/HIP graphs and replays them.
+    Without dropout every replay, on inputs that change between replays, equals
+    the eager step on the same inputs bit for bit (weight gradient in
+    deterministic mode); with dropout each replay draws a fresh mask and
+    `updated` keeps about 1 - p of the branch."""
+    shape = (4, 64, 768)
+    inputs = make_inputs(shape, torch.float16, seed=31)
+    grads = make_grads(shape, seed=32)
+    params = [t.detach().clone().requires_grad_(True) for t in inputs[2:]]
+
+    def body(x, branch):
+        return residual_layer_norm(x, branch, params[0], params[1], dropout_p=0.0,
+                                   implementation="gfx950")
+
+    def run(function, replay):
+        for p in params:
+            p.grad = None
+        x = (inputs[0] * (1.0 + 0.25 * replay)).detach().requires_grad_(True)
+        torch.compiler.cudagraph_mark_step_begin()
+        updated, normalized = function(x, inputs[1])
+        torch.autograd.backward((updated, normalized), grads)
+        torch.cuda.synchronize()
+        return host(updated).copy(), host(params[0].grad).copy()
+
+    with deterministic_algorithms():
+        compiled = torch.compile(body, mode="reduce-overhead", fullgraph=True)
+        for replay in range(5):
+            expected = run(body, replay)
+            actual = run(compiled, replay)
+            assert_bitwise(actual[0], expected[0], f"replay {replay} updated")
+            assert_bitwise(actual[1], expected[1], f"replay {replay} grad_weight")
+
+    def dropped(x, branch):
+        return residual_layer_norm(x, branch, params[0], params[1], dropout_p=0.3,
+                                   implementation="gfx950")
+
+    compiled_dropout = torch.compile(dropped, mode="reduce-overhead", fullgraph=True)
+    updates = []
+    for replay in range(5):
+        torch.compiler.cudagraph_mark_step_begin()
+        with torch.no_grad():
+            updated, _ = compiled_dropout(inputs[0], inputs[1])
+        torch.cuda.synchronize()
+        kept = (host(updated) != host(inputs[0])).mean()
+        assert 0.6 < kept < 0.8, f"replay {replay}: kept {kept}"
+        updates.append(host(updated).copy())
+    assert not np.array_equal(updates[3], updates[4])
