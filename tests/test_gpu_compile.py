@@ -168,3 +168,36 @@ def test_reduce_overhead_training_step_replays():
         assert 0.6 < kept < 0.8, f"replay {replay}: kept {kept}"
         updates.append(host(updated).copy())
     assert not np.array_equal(updates[3], updates[4])
+
+
+@pytest.mark.parametrize("strict", [False, True], ids=["non-strict", "strict"])
+def test_torch_export_keeps_the_fused_op(strict):
+    """torch.export of a module that calls residual_layer_norm: the exported
+    graph holds the registered custom op (no decomposition), and the exported
+    program's outputs equal the module's bit for bit (eval mode; the reference
+    does not support export, docs/residual_layer_norm.md:301-302)."""
+
+    class Block(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.norm = torch.nn.LayerNorm(768)
+
+        def forward(self, x, branch):
+            return residual_layer_norm(x, branch, self.norm.weight, self.norm.bias,
+                                       dropout_p=0.1, training=self.training,
+                                       implementation="gfx950")
+
+    model = Block().cuda().eval()
+    with torch.no_grad():
+        model.norm.weight.normal_(1.0, 0.02)
+        model.norm.bias.normal_(0.0, 0.02)
+    inputs = make_inputs((2, 37, 768), torch.float16, seed=41)[:2]
+    exported = torch.export.export(model, inputs, strict=strict)
+    targets = [str(node.target) for node in exported.graph.nodes if node.op == "call_function"]
+    assert any("gfx1010_kernels.rln_forward" in target for target in targets), targets
+    assert not any("layer_norm" in target for target in targets), targets
+    with torch.no_grad():
+        expected = model(*inputs)
+        actual = exported.module()(*inputs)
+    for index, (a, b) in enumerate(zip(actual, expected)):
+        assert_bitwise(host(a), host(b), f"exported output {index}")
