@@ -387,6 +387,63 @@ def test_half_precision_rounding_matches_torch(torch_dtype, rounding):
     assert np.isnan(nan).all()
 
 
+def test_special_values_follow_the_reference_products():
+    """The oracle gives infinities and NaNs the reference's arithmetic gives
+    them. The dropped branch has known answers from IEEE 754: inf * 0 is NaN,
+    and 65504 (the largest fp16) times 1/(1 - 0.1) rounds to inf in fp16. The
+    LayerNorm and its gradient match torch's float64 F.layer_norm and
+    autograd: a row holding an inf or a NaN is NaN in every column, an inf or a
+    NaN upstream gradient makes every input gradient of its row non-finite, and
+    it reaches the weight/bias sums in its own column only."""
+    _, scale, _ = oracle.dropout_constants(0.1)
+    branch = np.array([np.inf, -np.inf, np.nan, 65504.0, 1.0, np.inf], np.float16)
+    keep = np.array([False, True, False, True, False, True])
+    with np.errstate(all="ignore"):
+        dropped = oracle.dropped_branch(branch, keep, scale, "f16")
+    expected = np.array([np.nan, -np.inf, np.nan, np.inf, 0.0, np.inf], np.float32)
+    assert np.array_equal(dropped, expected, equal_nan=True)
+
+    generator = torch.Generator().manual_seed(11)
+    hidden = 64
+
+    def randn(*shape):
+        return torch.randn(*shape, generator=generator, dtype=torch.float64)
+
+    u = randn(3, hidden)
+    u[0, 5] = float("inf")
+    u[1, 9] = float("nan")
+    weight, bias = 1.0 + 0.02 * randn(hidden), 0.02 * randn(hidden)
+    with np.errstate(all="ignore"):
+        mean, rstd, normalized = oracle.layer_norm_forward(u.numpy(), weight.numpy(),
+                                                           bias.numpy(), 1e-5)
+    reference = torch.nn.functional.layer_norm(u, (hidden,), weight, bias, 1e-5)
+    assert np.isnan(normalized[:2]).all() and torch.isnan(reference[:2]).all()
+    assert np.allclose(normalized[2], reference[2].numpy(), rtol=0, atol=1e-12)
+    assert mean[0] == np.inf and np.isnan(mean[1]) and np.isnan(rstd[:2]).all()
+
+    u = randn(3, hidden)
+    grad_updated, grad_normalized = randn(3, hidden), randn(3, hidden)
+    grad_normalized[0, 7] = float("inf")
+    grad_normalized[1, 11] = float("nan")
+    with np.errstate(all="ignore"):
+        got = oracle.backward(grad_updated.numpy(), grad_normalized.numpy(), u.numpy(),
+                              weight.numpy(), 1e-5)
+    leaves = [t.clone().requires_grad_(True) for t in (u, weight, bias)]
+    out = torch.nn.functional.layer_norm(leaves[0], (hidden,), leaves[1], leaves[2], 1e-5)
+    torch.autograd.backward((out, leaves[0]), (grad_normalized, grad_updated))
+    grad_x, grad_weight, grad_bias = (t.grad.numpy() for t in leaves)
+    for row in (0, 1):
+        assert not np.isfinite(got["grad_x"][row]).any() and not np.isfinite(grad_x[row]).any()
+    assert np.allclose(got["grad_x"][2], grad_x[2], rtol=0, atol=1e-12)
+    for mine, torchs in ((got["grad_weight"], grad_weight), (got["grad_bias"], grad_bias)):
+        assert np.array_equal(mine[[7, 11]], torchs[[7, 11]], equal_nan=True)
+        assert np.isinf(mine[7]) and np.isnan(mine[11])
+        others = np.ones(hidden, dtype=bool)
+        others[[7, 11]] = False
+        assert np.allclose(mine[others], torchs[others], rtol=0, atol=1e-12)
+    assert got["grad_bias"][7] == np.inf
+
+
 def test_dropped_bfloat16_branch_rounds_fp32_product_once():
     branch = oracle.round_to_bfloat16(np.array([1.0, 0.3, -2.7, 1e-3], np.float32))
     keep = np.array([True, True, False, True])
