@@ -297,3 +297,55 @@ def test_backward_of_a_non_finite_forward(case):
             assert np.isnan(host(poisoned[name][row])).all(), f"{name} row {row}"
     assert np.isnan(host(poisoned["grad_weight"])).all()
     assert torch.equal(bits(poisoned["grad_bias"]), bits(clean["grad_bias"]))
+
+
+def test_grad_scaler_skips_an_overflowed_step_and_takes_a_clean_one():
+    """torch.amp.GradScaler through the public API. An fp16 branch that
+    overflowed makes `normalized` NaN in its rows, so the weight/bias
+    gradients of the op and the gradient it hands the branch's producer are
+    not finite: the scaler skips the optimizer step and halves its scale. The
+    same step on a finite branch updates every parameter."""
+    from gfx1010_kernels import residual_layer_norm
+
+    torch.manual_seed(3)
+    hidden = 768
+    x = torch.randn(4, 64, hidden, device="cuda")
+    linear = torch.nn.Linear(hidden, hidden).cuda()
+    weight = torch.nn.Parameter(1.0 + 0.02 * torch.randn(hidden, device="cuda"))
+    bias = torch.nn.Parameter(0.02 * torch.randn(hidden, device="cuda"))
+    parameters = [linear.weight, linear.bias, weight, bias]
+    optimizer = torch.optim.SGD(parameters, lr=0.1)
+    scaler = torch.amp.GradScaler("cuda", init_scale=2.0 ** 10)
+
+    def step():
+        optimizer.zero_grad(set_to_none=True)
+        with torch.autocast("cuda", dtype=torch.float16):
+            branch = linear(x)
+        assert branch.dtype == torch.float16
+        updated, normalized = residual_layer_norm(x, branch, weight, bias, dropout_p=0.1,
+                                                  implementation="gfx950")
+        loss = normalized.square().mean() + 0.1 * updated.mean()
+        scaler.scale(loss).backward()
+        finite = [bool(torch.isfinite(p.grad).all()) for p in parameters]
+        before = [p.detach().clone() for p in parameters]
+        scaler.step(optimizer)
+        scaler.update()
+        return branch, finite, before
+
+    saved = linear.weight.detach().clone()
+    with torch.no_grad():
+        linear.weight.mul_(1e5)  # outputs of order 6e4 and above: fp16 overflows
+    branch, finite, before = step()
+    assert not torch.isfinite(branch).all()
+    assert finite == [False] * 4, "an overflowed branch left a gradient finite"
+    for parameter, old in zip(parameters, before):
+        assert torch.equal(parameter.detach(), old), "the scaler took an overflowed step"
+    assert scaler.get_scale() == 2.0 ** 9
+
+    with torch.no_grad():
+        linear.weight.copy_(saved)
+    branch, finite, before = step()
+    assert torch.isfinite(branch).all() and finite == [True] * 4
+    for parameter, old in zip(parameters, before):
+        assert not torch.equal(parameter.detach(), old), "a clean step left a parameter unchanged"
+    assert scaler.get_scale() == 2.0 ** 9
