@@ -6,6 +6,7 @@ which happens before any HIP call.
 
 import ctypes
 import re
+import threading
 from pathlib import Path
 
 import pytest
@@ -199,3 +200,39 @@ def test_noalloc_backward_refuses_partials_above_its_scratch_before_any_gpu_work
         _cabi.backward_noalloc(fake, fake, None, fake, fake, fake, fake, fake, fake,
                                _cabi.RLN_DTYPE_F16, fake, fake, rows, hidden, 0.1, True, True)
     assert "backward tensors must not be null" in str(caught.value)
+
+
+def test_last_error_is_kept_per_thread():
+    """rln_last_error() is thread-local (include/rln.h): a failure on one
+    thread neither overwrites nor clears the message another thread reads
+    afterwards, and a successful call clears only its own thread's message.
+    The two threads take turns at barriers, so each reads its message after
+    the other thread's failing call."""
+    library = _cabi.library()
+    barrier = threading.Barrier(2, timeout=30)
+    seen = {}
+
+    def first():
+        seen["first status"] = library.rln_philox_increment(100, 0)
+        barrier.wait()  # the second thread fails now
+        barrier.wait()
+        seen["first"] = library.rln_last_error().decode()
+
+    def second():
+        barrier.wait()
+        seen["second status"] = library.rln_philox_increment(768, 64)
+        barrier.wait()
+        seen["second"] = library.rln_last_error().decode()
+        seen["success"] = library.rln_philox_increment(768, 0)
+        seen["cleared"] = library.rln_last_error().decode()
+
+    threads = [threading.Thread(target=first), threading.Thread(target=second)]
+    for thread in threads:
+        thread.start()
+    for thread in threads:
+        thread.join(timeout=60)
+    assert seen == {
+        "first status": 0, "first": "unsupported hidden size 100",
+        "second status": 0, "second": "threads must be 0, 128, 192 or 256",
+        "success": 4, "cleared": "",
+    }

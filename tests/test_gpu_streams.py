@@ -15,9 +15,13 @@ follow:
 * the results are those of the new inputs, bit for bit against the same call
   made on settled data, so the launch was ordered after the write on that
   stream (a launch on another stream would have read the old values).
+
+A last test calls the C ABI from two host threads at once, each on its own
+stream, against the same calls made alone.
 """
 
 import contextlib
+import threading
 
 import pytest
 import torch
@@ -110,59 +114,119 @@ def test_raw_entry_points_run_on_the_current_stream_without_waiting():
 
 
 CODE = {torch.float32: _cabi.RLN_DTYPE_F32, torch.float16: _cabi.RLN_DTYPE_F16}
+PHILOX = _cabi.RlnPhilox(0xABCDEF, 1 << 8, None, None, 0)
+
+
+def c_abi_case(rows, hidden, seed):
+    x, branch, weight, bias = make_inputs((rows, hidden), torch.float16, seed=seed)
+    grad_updated, grad_normalized = make_grads((rows, hidden), seed=seed + 1)
+    return dict(x=x, branch=branch, weight=weight, bias=bias, grad_updated=grad_updated,
+                grad_normalized=grad_normalized)
+
+
+def c_abi_buffers(case):
+    rows, hidden = case["x"].shape
+    workspace_bytes = _cabi.backward_workspace_bytes(rows, hidden, True)
+    return dict(
+        updated=torch.empty(rows, hidden, device="cuda"),
+        normalized=torch.empty(rows, hidden, device="cuda"),
+        mean=torch.empty(rows, device="cuda"), rstd=torch.empty(rows, device="cuda"),
+        mask=torch.zeros(_cabi.mask_words(rows, hidden), device="cuda", dtype=torch.int32),
+        grad_x=torch.empty(rows, hidden, device="cuda"),
+        grad_branch=torch.empty(rows, hidden, device="cuda", dtype=case["branch"].dtype),
+        sums=torch.empty(2, hidden, device="cuda"),
+        workspace=torch.empty(workspace_bytes, device="cuda", dtype=torch.uint8))
+
+
+C_ABI_OUTPUTS = ("updated", "normalized", "mean", "rstd", "mask", "grad_x", "grad_branch", "sums")
+
+
+def c_abi_step(case, out, x, grad_normalized, stream):
+    """rln_forward then rln_backward (p = 0.1, the library's own dropout layout,
+    deterministic weight/bias sums) on `stream`."""
+    rows, hidden = x.shape
+    branch, weight = case["branch"], case["weight"]
+    _cabi.forward(x.data_ptr(), branch.data_ptr(), CODE[branch.dtype], weight.data_ptr(),
+                  case["bias"].data_ptr(), out["updated"].data_ptr(),
+                  out["normalized"].data_ptr(), out["mean"].data_ptr(), out["rstd"].data_ptr(),
+                  out["mask"].data_ptr(), rows, hidden, 0.1, EPS, True, PHILOX, stream)
+    _cabi.backward(case["grad_updated"].data_ptr(), grad_normalized.data_ptr(),
+                   out["updated"].data_ptr(), weight.data_ptr(), out["mean"].data_ptr(),
+                   out["rstd"].data_ptr(), out["mask"].data_ptr(), out["grad_x"].data_ptr(),
+                   out["grad_branch"].data_ptr(), CODE[branch.dtype], out["sums"][0].data_ptr(),
+                   out["sums"][1].data_ptr(), rows, hidden, 0.1, True, True,
+                   out["workspace"].data_ptr(), out["workspace"].numel(), stream)
 
 
 @pytest.mark.parametrize("hidden,rows", [(768, 4096), (2048, 1024)])
 def test_c_abi_runs_on_the_stream_it_is_given(hidden, rows):
     """rln_forward / rln_backward with an explicit side stream while the
-    default stream is current (the library's own dropout layout, p = 0.1)."""
-    x, branch, weight, bias = make_inputs((rows, hidden), torch.float16, seed=44)
-    grad_updated, grad_normalized = make_grads((rows, hidden), seed=45)
-    fresh_x = x * 0.5 + 1.0
-    fresh_grad = grad_normalized - 1.0
-    philox = _cabi.RlnPhilox(0xABCDEF, 1 << 8, None, None, 0)
-    workspace_bytes = _cabi.backward_workspace_bytes(rows, hidden, True)
-
-    def buffers():
-        return dict(
-            updated=torch.empty(rows, hidden, device="cuda"),
-            normalized=torch.empty(rows, hidden, device="cuda"),
-            mean=torch.empty(rows, device="cuda"), rstd=torch.empty(rows, device="cuda"),
-            mask=torch.zeros(_cabi.mask_words(rows, hidden), device="cuda", dtype=torch.int32),
-            grad_x=torch.empty(rows, hidden, device="cuda"),
-            grad_branch=torch.empty(rows, hidden, device="cuda", dtype=branch.dtype),
-            sums=torch.empty(2, hidden, device="cuda"),
-            workspace=torch.empty(workspace_bytes, device="cuda", dtype=torch.uint8))
-
-    def launch(out, x_values, grad_values, stream):
-        _cabi.forward(x_values.data_ptr(), branch.data_ptr(), CODE[branch.dtype],
-                      weight.data_ptr(), bias.data_ptr(), out["updated"].data_ptr(),
-                      out["normalized"].data_ptr(), out["mean"].data_ptr(),
-                      out["rstd"].data_ptr(), out["mask"].data_ptr(), rows, hidden, 0.1, EPS,
-                      True, philox, stream)
-        _cabi.backward(grad_updated.data_ptr(), grad_values.data_ptr(),
-                       out["updated"].data_ptr(), weight.data_ptr(), out["mean"].data_ptr(),
-                       out["rstd"].data_ptr(), out["mask"].data_ptr(), out["grad_x"].data_ptr(),
-                       out["grad_branch"].data_ptr(), CODE[branch.dtype],
-                       out["sums"][0].data_ptr(), out["sums"][1].data_ptr(), rows, hidden, 0.1,
-                       True, True, out["workspace"].data_ptr(), workspace_bytes, stream)
-
-    expected = buffers()
-    launch(expected, fresh_x, fresh_grad, torch.cuda.current_stream().cuda_stream)
+    default stream is current."""
+    case = c_abi_case(rows, hidden, seed=44)
+    fresh_x = case["x"] * 0.5 + 1.0
+    fresh_grad = case["grad_normalized"] - 1.0
+    expected = c_abi_buffers(case)
+    c_abi_step(case, expected, fresh_x, fresh_grad, torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
 
-    actual = buffers()
-    x_target, grad_target = x.clone(), grad_normalized.clone()
+    actual = c_abi_buffers(case)
+    x_target, grad_target = case["x"].clone(), case["grad_normalized"].clone()
     torch.cuda.synchronize()
     side = torch.cuda.Stream()
     queue_write_behind_spin(side, x_target, fresh_x)
     with torch.cuda.stream(side):
         grad_target.copy_(fresh_grad)
     assert torch.cuda.current_stream() == torch.cuda.default_stream()
-    launch(actual, x_target, grad_target, side.cuda_stream)
+    c_abi_step(case, actual, x_target, grad_target, side.cuda_stream)
     waiting = not side.query()
     side.synchronize()
     assert waiting, "the C ABI waited for the GPU"
-    for name in ("updated", "normalized", "mean", "rstd", "mask", "grad_x", "grad_branch",
-                 "sums"):
+    for name in C_ABI_OUTPUTS:
         assert_same(actual[name], expected[name], name)
+
+
+def test_c_abi_calls_from_two_host_threads_at_once():
+    """Two host threads, each with its own stream, buffers and row shape, call
+    rln_forward / rln_backward 12 times each at the same time (ctypes releases
+    the GIL during the calls). Every result equals, bit for bit, the same call
+    made alone: the library keeps no state that one call could leave for
+    another (the error message is per thread, the device queries are made
+    once)."""
+    cases = [c_abi_case(2048, 768, seed=46), c_abi_case(512, 1600, seed=48)]
+    expected = []
+    for case in cases:
+        out = c_abi_buffers(case)
+        c_abi_step(case, out, case["x"], case["grad_normalized"],
+                   torch.cuda.current_stream().cuda_stream)
+        expected.append(out)
+    torch.cuda.synchronize()
+
+    barrier = threading.Barrier(len(cases), timeout=60)
+    snapshots = [[] for _ in cases]
+    errors = []
+
+    def worker(index):
+        try:
+            case = cases[index]
+            stream = torch.cuda.Stream()
+            out = c_abi_buffers(case)
+            barrier.wait()
+            with torch.cuda.stream(stream):
+                for _ in range(12):
+                    c_abi_step(case, out, case["x"], case["grad_normalized"], stream.cuda_stream)
+                    snapshots[index].append({name: out[name].clone() for name in C_ABI_OUTPUTS})
+            stream.synchronize()
+        except Exception as error:  # reported on the main thread
+            errors.append(error)
+
+    threads = [threading.Thread(target=worker, args=(index,)) for index in range(len(cases))]
+    for thread in threads:
+        thread.start()
+    for thread in threads:
+        thread.join(timeout=120)
+    assert not errors, errors
+    for index, case in enumerate(cases):
+        assert len(snapshots[index]) == 12
+        for step, snapshot in enumerate(snapshots[index]):
+            for name in C_ABI_OUTPUTS:
+                assert_same(snapshot[name], expected[index][name], f"case {index} step {step} {name}")
