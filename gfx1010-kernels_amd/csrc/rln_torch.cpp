@@ -444,7 +444,9 @@ std::vector<at::Tensor> backward_impl(
 // Autograd contract of csrc/residual_layer_norm_bindings.cpp:10-98: saves
 // updated, weight, mean, rstd and mask (the last three in one row-statistics
 // tensor), does not materialize missing output gradients, and returns
-// weight/bias gradients only when `normalized` received a gradient. Missing
+// weight/bias gradients only when `normalized` received a gradient (and, here,
+// only when the backward pass needs one of them; the reference computes them
+// whenever `normalized` has a gradient). Missing
 // gradients are passed to the kernel as null pointers instead of materialized
 // zeros. The forward's host cost is kept low on purpose (three allocations
 // and two more for the gradient sums, one saved_data entry): small calls are
@@ -508,10 +510,15 @@ class ResidualLayerNormFunction : public torch::autograd::Function<ResidualLayer
                 at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor(),
                 at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor(), at::Tensor()};
         }
-        // Sums zeroed by the forward serve the first backward only.
+        // The weight/bias sums only when this backward pass asks for them
+        // (edges 2 and 3): frozen parameters, or torch.autograd.grad over the
+        // inputs alone, skip their reduction entirely.
+        const bool parameter_gradients = has_grad_normalized
+            && (ctx->needs_input_grad(2) || ctx->needs_input_grad(3));
+        // Sums zeroed by the forward serve the first backward that computes them.
         at::Tensor grad_weight_sum;
         at::Tensor grad_bias_sum;
-        if (ctx->saved_data.find("sums_used") == ctx->saved_data.end()) {
+        if (parameter_gradients && ctx->saved_data.find("sums_used") == ctx->saved_data.end()) {
             grad_weight_sum = saved[3];
             grad_bias_sum = saved[4];
             ctx->saved_data["sums_used"] = true;
@@ -542,15 +549,15 @@ class ResidualLayerNormFunction : public torch::autograd::Function<ResidualLayer
             state[3],
             state[4],
             state[5],
-            has_grad_normalized,
+            parameter_gradients,
             branch_dtype,
             &grad_weight_sum,
             &grad_bias_sum);
         return {
             gradients[0],
             gradients[1],
-            has_grad_normalized ? gradients[2] : at::Tensor(),
-            has_grad_normalized ? gradients[3] : at::Tensor(),
+            parameter_gradients ? gradients[2] : at::Tensor(),
+            parameter_gradients ? gradients[3] : at::Tensor(),
             at::Tensor(),
             at::Tensor(),
             at::Tensor(),

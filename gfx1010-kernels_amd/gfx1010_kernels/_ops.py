@@ -20,10 +20,13 @@ fused op instead of breaking around it (the reference does not support
   subexpression pass merges identical calls of a functional custom op, but
   never two ``aten.empty`` nodes, so each call's nonce differs.
 * ``gfx1010_kernels::rln_backward(grad_updated, grad_normalized, updated, weight,
-  mean, rstd, mask, dropout_p, training, branch_dtype)
+  mean, rstd, mask, dropout_p, training, branch_dtype, compute_parameters)
   -> (grad_x, grad_branch, grad_weight, grad_bias)`` runs
   ``_C.residual_layer_norm_backward``; a missing upstream gradient counts as
   zero, and the weight/bias gradients are zero when ``grad_normalized`` is.
+  With ``compute_parameters`` false (the backward pass needs neither weight
+  nor bias gradient: frozen parameters, or gradients taken for the inputs
+  only) the weight/bias sums are skipped and those two outputs are empty.
 """
 
 from __future__ import annotations
@@ -98,19 +101,23 @@ def rln_backward(
     dropout_p: float,
     training: bool,
     branch_dtype: torch.dtype,
+    compute_parameters: bool = True,
 ) -> tuple[Tensor, Tensor, Tensor, Tensor]:
     grad_x, grad_branch, grad_weight, grad_bias = _native().residual_layer_norm_backward(
         grad_updated, grad_normalized, updated, weight, mean, rstd, mask, float(dropout_p),
-        bool(training), branch_dtype == torch.float16, *_BACKWARD_HINTS, True,
-        branch_dtype=branch_dtype,
+        bool(training), branch_dtype == torch.float16, *_BACKWARD_HINTS,
+        bool(compute_parameters), branch_dtype=branch_dtype,
     )
+    if not compute_parameters:
+        grad_weight = updated.new_empty((0,))
+        grad_bias = updated.new_empty((0,))
     return grad_x, grad_branch, grad_weight, grad_bias
 
 
 @rln_backward.register_fake
 def _rln_backward_fake(grad_updated, grad_normalized, updated, weight, mean, rstd, mask,
-                       dropout_p, training, branch_dtype):
-    hidden = updated.shape[-1]
+                       dropout_p, training, branch_dtype, compute_parameters=True):
+    hidden = updated.shape[-1] if compute_parameters else 0
     return (
         torch.empty_like(updated, memory_format=torch.contiguous_format),
         torch.empty_like(updated, dtype=branch_dtype, memory_format=torch.contiguous_format),
@@ -138,11 +145,14 @@ def _backward(ctx, grad_updated, grad_normalized, _grad_mean, _grad_rstd, _grad_
         grad_updated = grad_updated.contiguous()
     if grad_normalized is not None:
         grad_normalized = grad_normalized.contiguous()
+    # Weight/bias sums only when this backward pass asks for them.
+    parameters = grad_normalized is not None and (ctx.needs_input_grad[2]
+                                                  or ctx.needs_input_grad[3])
     grad_x, grad_branch, grad_weight, grad_bias = rln_backward(
         grad_updated, grad_normalized, updated, weight, mean, rstd, mask, ctx.dropout_p,
-        ctx.training, ctx.branch_dtype,
+        ctx.training, ctx.branch_dtype, parameters,
     )
-    if grad_normalized is None:
+    if not parameters:
         grad_weight = grad_bias = None
     return grad_x, grad_branch, grad_weight, grad_bias, None, None, None, None, None
 

@@ -230,3 +230,49 @@ def test_repeated_backward_of_one_forward(deterministic):
         else:
             assert torch.allclose(a.float(), b.float(), rtol=1e-5, atol=1e-5), name
     assert first[2].data_ptr() != second[2].data_ptr()
+
+
+@pytest.mark.parametrize("path", ["eager", "custom_op"])
+def test_backward_skips_the_parameter_sums_it_does_not_need(path):
+    """A backward pass that needs no weight/bias gradient (frozen LayerNorm
+    parameters, or torch.autograd.grad over x and branch alone) skips their
+    reduction. Its input gradients equal the full backward's bit for bit, it
+    produces no parameter gradient, and a later pass over the same graph
+    (retain_graph) that asks for them gets the full backward's (deterministic
+    sums, bitwise). Both the C++ autograd function (eager calls) and the
+    registered custom op (torch.compile's path) are checked."""
+    from gfx1010_kernels._ops import residual_layer_norm_op
+
+    def call(x, branch, weight, bias):
+        if path == "eager":
+            return residual_layer_norm(x, branch, weight, bias, dropout_p=0.1,
+                                       implementation="gfx950")
+        return residual_layer_norm_op(x, branch, weight, bias, 0.1, 1e-5, True)
+
+    inputs = make_inputs((3, 171, 768), torch.float16, seed=61)
+    grads = make_grads((3, 171, 768), seed=62)
+
+    def leaves(*requires):
+        return [t.detach().clone().requires_grad_(r) for t, r in zip(inputs, requires)]
+
+    with deterministic_algorithms(True):
+        torch.cuda.manual_seed(5)
+        full_leaves = leaves(True, True, True, True)
+        full = torch.autograd.grad(call(*full_leaves), full_leaves, grads)
+
+        torch.cuda.manual_seed(5)
+        split_leaves = leaves(True, True, True, True)
+        out = call(*split_leaves)
+        inputs_only = torch.autograd.grad(out, split_leaves[:2], grads, retain_graph=True)
+        parameters = torch.autograd.grad(out, split_leaves[2:], grads)
+
+        torch.cuda.manual_seed(5)
+        frozen = leaves(True, True, False, False)
+        torch.autograd.backward(call(*frozen), grads)
+
+    for name, actual, expected in zip(("grad_x", "grad_branch", "grad_weight", "grad_bias"),
+                                      (*inputs_only, *parameters), full):
+        assert_bitwise(host(actual), host(expected), f"split pass {name}")
+    assert_bitwise(host(frozen[0].grad), host(full[0]), "frozen grad_x")
+    assert_bitwise(host(frozen[1].grad), host(full[1]), "frozen grad_branch")
+    assert frozen[2].grad is None and frozen[3].grad is None
