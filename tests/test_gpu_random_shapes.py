@@ -6,7 +6,11 @@ mode, then checks the forward and the backward against the fp64 oracle. The
 draws are fixed by the case index, so every run checks the same cases. A
 second set draws from the reference's six hidden sizes only, with a random
 `threads` (the reference's dropout stream of a 128-, 192- or 256-thread
-launch) and a random generator offset.
+launch) and a random generator offset. A third set draws large launches
+(2^22 to 2^26 elements, any hidden size), where the grid and schedule rules
+of large launches apply, and checks every element of every output
+(parity.check_full_tensor) and the weight/bias sums against a float64
+reduction.
 """
 
 import numpy as np
@@ -23,7 +27,9 @@ from parity import (
     make_grads,
     make_inputs,
 )
+from parity import check_full_tensor
 from test_gpu_backward import deterministic_algorithms, raw_backward
+from test_gpu_configs import check_parameter_gradients, device_inputs
 
 pytestmark = pytest.mark.gpu
 EPS = 1e-5
@@ -49,7 +55,7 @@ def draw(case, sizes=NATIVE_HIDDEN_SIZES):
     )
 
 
-@pytest.mark.parametrize("case", range(32))
+@pytest.mark.parametrize("case", range(128))
 def test_random_configuration_matches_oracle(case):
     c = draw(case)
     print(f"[random] case {case}: {c}", flush=True)
@@ -69,7 +75,7 @@ def test_random_configuration_matches_oracle(case):
                    scale, f"case {case}")
 
 
-@pytest.mark.parametrize("case", range(100, 124))
+@pytest.mark.parametrize("case", [*range(100, 124), *range(200, 240)])
 def test_random_reference_stream_configuration_matches_oracle(case):
     c = draw(case, SPECIALIZED_HIDDEN_SIZES)
     c["dropout_p"] = c["dropout_p"] or 0.25
@@ -91,3 +97,25 @@ def test_random_reference_stream_configuration_matches_oracle(case):
                                  c["dropout_p"], c["branch"], training=True)
     check_backward(gradients, grad_updated, grad_normalized, outputs[0], inputs[2], EPS, keep,
                    scale, f"case {case}")
+
+
+@pytest.mark.parametrize("case", range(300, 316))
+def test_random_large_configuration_matches_oracle(case):
+    rng = np.random.default_rng(1000 + case)
+    hidden = int(rng.integers(2, 129)) * 64
+    rows = max(1, int(2 ** rng.uniform(22, 26)) // hidden + int(rng.integers(-3, 4)))
+    branch_dtype = DTYPES[int(rng.integers(3))]
+    dropout_p = float(rng.choice([0.1, 0.15, 0.5]))
+    deterministic = bool(rng.integers(2))
+    threads = 192 if hidden == 1024 else 128
+    print(f"[random-large] case {case}: rows={rows} H={hidden} {branch_dtype} p={dropout_p} "
+          f"deterministic={deterministic}", flush=True)
+    inputs, grads = device_inputs(rows, hidden, branch_dtype, seed=case)
+    torch.cuda.manual_seed(case)
+    seed, offset = generator_state()
+    outputs = _C.residual_layer_norm_forward(*inputs, dropout_p, EPS, True, threads)
+    with deterministic_algorithms(deterministic):
+        gradients = raw_backward(grads[0], grads[1], outputs, inputs[2], dropout_p, branch_dtype)
+    check_full_tensor(inputs, grads, outputs, gradients, dropout_p, EPS, seed, offset,
+                      threads=threads, what=f"case {case}: {rows} x {hidden}")
+    check_parameter_gradients(outputs[0], grads[1], gradients)
