@@ -583,6 +583,18 @@ torch::autograd::variable_list residual_layer_norm_autograd(
     int64_t parameter_threads,
     int64_t parameter_groups,
     std::optional<at::ScalarType> normalized_dtype) {
+    // Nothing to record (grad mode off, as under torch.no_grad() and
+    // inference_mode, or no input requires grad): the forward alone, without
+    // the autograd node, its saved state and the gradient sums. Small calls,
+    // such as the decode steps of a served model, are bound by this host cost.
+    if (!at::GradMode::is_enabled()
+        || !(x.requires_grad() || branch.requires_grad() || weight.requires_grad()
+             || bias.requires_grad())) {
+        at::Tensor row_stats;
+        auto result = forward_impl(x, branch, weight, bias, dropout_p, eps, training, threads,
+                                   normalized_dtype, nullptr, nullptr, &row_stats);
+        return {std::get<0>(result), std::get<1>(result)};
+    }
     return ResidualLayerNormFunction::apply(
         x,
         branch,

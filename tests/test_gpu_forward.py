@@ -113,3 +113,31 @@ def test_raw_forward_rejects_invalid_inputs_on_gpu():
         _C.residual_layer_norm_forward(strided, branch, weight, bias, 0.0, 1e-5, True, 128)
     with pytest.raises(RuntimeError, match="x must use float32"):
         _C.residual_layer_norm_forward(x.half(), branch, weight, bias, 0.0, 1e-5, True, 128)
+
+
+@pytest.mark.parametrize("mode", ["no_grad", "inference_mode", "no_input_requires_grad"])
+def test_forward_without_a_graph_equals_the_recorded_forward(mode):
+    """A call with nothing to record (grad mode off, or no input requiring
+    grad) runs the forward alone, without the autograd node or the gradient
+    sums. Its outputs equal the recorded call's bit for bit, it draws the same
+    dropout mask from the same generator state and advances the generator by
+    the same offset, and its outputs carry no graph."""
+    inputs = make_inputs((5, 77, 768), torch.float16, seed=71)
+    recorded_leaves = [t.detach().clone().requires_grad_(True) for t in inputs]
+    torch.cuda.manual_seed(9)
+    recorded = residual_layer_norm(*recorded_leaves, dropout_p=0.1, implementation="gfx950")
+    recorded_offset = torch.cuda.default_generators[0].get_offset()
+    assert all(t.grad_fn is not None for t in recorded)
+
+    torch.cuda.manual_seed(9)
+    if mode == "no_input_requires_grad":
+        bare = residual_layer_norm(*inputs, dropout_p=0.1, implementation="gfx950")
+    else:
+        context = torch.no_grad() if mode == "no_grad" else torch.inference_mode()
+        leaves = [t.detach().clone().requires_grad_(True) for t in inputs]
+        with context:
+            bare = residual_layer_norm(*leaves, dropout_p=0.1, implementation="gfx950")
+    assert torch.cuda.default_generators[0].get_offset() == recorded_offset
+    for actual, expected in zip(bare, recorded):
+        assert actual.grad_fn is None and not actual.requires_grad
+        assert_bitwise(host(actual), host(expected.detach()))
