@@ -610,6 +610,65 @@ torch::autograd::variable_list residual_layer_norm_autograd(
         normalized_dtype);
 }
 
+// True when the fused kernels serve these inputs: the conditions under which
+// the Python `_input_reason` (the reference's gfx1010_kernels/normalization.py:97-132,
+// widened to this library's sizes and dtypes) finds no reason and the hidden
+// size is native. One C++ call instead of ~20 Python attribute reads; the
+// reason itself is only worked out, in Python, when this is false.
+bool fused_inputs_supported(const at::Tensor& x, const at::Tensor& branch,
+                            const at::Tensor& weight, const at::Tensor& bias, double dropout_p,
+                            double eps) {
+    if (!x.is_cuda() || !branch.is_cuda() || !weight.is_cuda() || !bias.is_cuda()) {
+        return false;
+    }
+    const auto device = x.device();
+    if (branch.device() != device || weight.device() != device || bias.device() != device) {
+        return false;
+    }
+    if (x.dim() < 2 || branch.sizes() != x.sizes()) {
+        return false;
+    }
+    const int64_t hidden = x.size(-1);
+    // Native sizes are multiples of 64 from 128 up: within the Python range
+    // and divisible by 8.
+    if (!native_hidden(hidden) || weight.sizes() != at::IntArrayRef({hidden})
+        || bias.sizes() != at::IntArrayRef({hidden})) {
+        return false;
+    }
+    if (x.scalar_type() != at::kFloat || !supported_dtype(branch.scalar_type())
+        || weight.scalar_type() != at::kFloat || bias.scalar_type() != at::kFloat) {
+        return false;
+    }
+    if (!(x.is_contiguous() && branch.is_contiguous() && weight.is_contiguous()
+          && bias.is_contiguous())) {
+        return false;
+    }
+    return dropout_p >= 0.0 && dropout_p < 1.0 && eps > 0.0 && x.numel() > 0;
+}
+
+// `residual_layer_norm` for inputs the fused kernels serve, else None (no
+// exception): the auto path's common case in one call.
+std::optional<torch::autograd::variable_list> residual_layer_norm_if_supported(
+    const at::Tensor& x,
+    const at::Tensor& branch,
+    const at::Tensor& weight,
+    const at::Tensor& bias,
+    double dropout_p,
+    double eps,
+    bool training,
+    int64_t threads,
+    int64_t block_rows,
+    int64_t parameter_threads,
+    int64_t parameter_groups,
+    std::optional<at::ScalarType> normalized_dtype) {
+    if (!fused_inputs_supported(x, branch, weight, bias, dropout_p, eps)) {
+        return std::nullopt;
+    }
+    return residual_layer_norm_autograd(x, branch, weight, bias, dropout_p, eps, training,
+                                        threads, block_rows, parameter_threads,
+                                        parameter_groups, normalized_dtype);
+}
+
 }  // namespace
 
 PYBIND11_MODULE(_C, module) {
@@ -629,6 +688,8 @@ PYBIND11_MODULE(_C, module) {
         pybind11::arg("parameter_threads"),
         pybind11::arg("parameter_groups"),
         pybind11::arg("normalized_dtype") = pybind11::none());
+    module.def("residual_layer_norm_if_supported", &residual_layer_norm_if_supported);
+    module.def("fused_inputs_supported", &fused_inputs_supported);
     module.def(
         "residual_layer_norm_forward",
         [](const at::Tensor& x, const at::Tensor& branch, const at::Tensor& weight,

@@ -94,6 +94,36 @@ def native_residual_layer_norm(
     )
 
 
+def native_residual_layer_norm_if_supported(
+    x,
+    branch,
+    weight,
+    bias,
+    dropout_p,
+    eps,
+    training,
+    normalized_dtype=None,
+):
+    """``native_residual_layer_norm`` when the fused kernels serve the inputs
+    (checked in C++, the conditions of ``normalization._input_reason`` plus a
+    native hidden size), else None. For callers that already know the
+    extension is loaded and the device ready; ``x`` has at least two
+    dimensions."""
+    result = _extension()[0].residual_layer_norm_if_supported(
+        x,
+        branch,
+        weight,
+        bias,
+        float(dropout_p),
+        float(eps),
+        bool(training),
+        _THREADS.get(x.shape[-1], 128),
+        *_LAUNCH_HINTS,
+        normalized_dtype,
+    )
+    return None if result is None else tuple(result)
+
+
 __all__ = [
     "NATIVE_HIDDEN_SIZES",
     "launch_threads",
@@ -101,4 +131,5 @@ __all__ = [
     "TARGET_ARCHITECTURE",
     "native_extension_status",
     "native_residual_layer_norm",
+    "native_residual_layer_norm_if_supported",
 ]

@@ -41,6 +41,7 @@ from ._normalization_native import (
     NATIVE_HIDDEN_SIZES_TEXT,
     TARGET_ARCHITECTURE,
     native_residual_layer_norm,
+    native_residual_layer_norm_if_supported,
 )
 from ._ops import residual_layer_norm_op
 from ._status import BackendStatus
@@ -265,6 +266,15 @@ def residual_layer_norm(
         return _traced(*args, implementation)
     if implementation in _STRICT_NATIVE:
         return _strict_native(*args)
+    # Inputs the fused kernels serve, on a device whose backend is known to be
+    # ready: one C++ check and call. The reasons below are only worked out
+    # when it declines.
+    if (implementation == "auto" and x.is_cuda and x.ndim >= 2
+            and x.get_device() in _READY_DEVICES):
+        result = native_residual_layer_norm_if_supported(
+            x, branch, weight, bias, dropout_p, eps, training, normalized_dtype)
+        if result is not None:
+            return result
 
     reason = _input_reason(x, branch, weight, bias, dropout_p, eps)
     if implementation == "triton":
@@ -281,6 +291,7 @@ def residual_layer_norm(
         if status.architecture == TARGET_ARCHITECTURE:
             raise RuntimeError(f"{_UNAVAILABLE}: {status.reason}")
         return _fall_back(status.reason, *args)
+    _READY_DEVICES.add(x.get_device())
     # The extension guards x's device itself (the reference wraps this call in
     # torch.cuda.device, normalization.py:289, which costs two device switches
     # per call here).

@@ -141,3 +141,68 @@ def test_forward_without_a_graph_equals_the_recorded_forward(mode):
     for actual, expected in zip(bare, recorded):
         assert actual.grad_fn is None and not actual.requires_grad
         assert_bitwise(host(actual), host(expected.detach()))
+
+
+def test_auto_fast_check_accepts_exactly_what_the_reasons_accept():
+    """implementation="auto" first asks one C++ check (`_C.fused_inputs_supported`)
+    and works out the reference's reason (`_input_reason`) only when the check
+    declines. The check must accept exactly the inputs with no reason and a
+    native hidden size: one case per reason, plus accepted ones. After the fast
+    path has served a call, a declined call still warns with its reason and
+    falls back."""
+    import warnings
+
+    from gfx1010_kernels.normalization import _NATIVE_SIZES, _input_reason
+
+    def inputs(rows=64, hidden=768, branch_dtype=torch.float16):
+        generator = torch.Generator(device="cuda").manual_seed(rows + hidden)
+        x = torch.randn(rows, hidden, device="cuda", generator=generator)
+        return dict(x=x, branch=torch.randn_like(x).to(branch_dtype),
+                    weight=torch.ones(hidden, device="cuda"),
+                    bias=torch.zeros(hidden, device="cuda"))
+
+    base = inputs()
+    transposed = torch.randn(768, 64, device="cuda").t()
+    cases = {
+        "valid f16": (base, 0.1, 1e-5),
+        "valid bf16": (inputs(branch_dtype=torch.bfloat16), 0.0, 1e-5),
+        "valid f32 1600": (inputs(7, 1600, torch.float32), 0.5, 1e-6),
+        "valid 3-d": ({**base, "x": base["x"].view(4, 16, 768),
+                       "branch": base["branch"].view(4, 16, 768)}, 0.1, 1e-5),
+        "x on cpu": ({**base, "x": base["x"].cpu()}, 0.1, 1e-5),
+        "bias on cpu": ({**base, "bias": base["bias"].cpu()}, 0.1, 1e-5),
+        "one dimension": ({**base, "x": base["x"][0], "branch": base["branch"][0]}, 0.1, 1e-5),
+        "shape mismatch": ({**base, "branch": base["branch"][:32]}, 0.1, 1e-5),
+        "hidden 160": (inputs(hidden=160), 0.1, 1e-5),
+        "hidden 96": (inputs(hidden=96), 0.1, 1e-5),
+        "hidden 8256": (inputs(2, 8256), 0.1, 1e-5),
+        "hidden 772": (inputs(hidden=772), 0.1, 1e-5),
+        "weight size": ({**base, "weight": base["weight"][:704]}, 0.1, 1e-5),
+        "x float16": ({**base, "x": base["x"].half()}, 0.1, 1e-5),
+        "x float64": ({**base, "x": base["x"].double()}, 0.1, 1e-5),
+        "branch int32": ({**base, "branch": base["branch"].int()}, 0.1, 1e-5),
+        "weight float16": ({**base, "weight": base["weight"].half()}, 0.1, 1e-5),
+        "x not contiguous": ({**base, "x": transposed}, 0.1, 1e-5),
+        "dropout 1": (base, 1.0, 1e-5),
+        "dropout negative": (base, -0.1, 1e-5),
+        "eps 0": (base, 0.1, 0.0),
+        "empty": (inputs(rows=0), 0.1, 1e-5),
+    }
+    for name, (tensors, dropout_p, eps) in cases.items():
+        args = (tensors["x"], tensors["branch"], tensors["weight"], tensors["bias"])
+        expected = (_input_reason(*args, dropout_p, eps) is None
+                    and args[0].shape[-1] in _NATIVE_SIZES)
+        assert _C.fused_inputs_supported(*args, dropout_p, eps) == expected, name
+        assert expected == name.startswith("valid"), name
+
+    served = residual_layer_norm(base["x"], base["branch"], base["weight"], base["bias"])
+    strict = residual_layer_norm(base["x"], base["branch"], base["weight"], base["bias"],
+                                 implementation="gfx950")
+    for actual, wanted in zip(served, strict):
+        assert_bitwise(host(actual), host(wanted))
+    declined = inputs(hidden=160)
+    with warnings.catch_warnings(record=True) as caught:
+        warnings.simplefilter("always")
+        residual_layer_norm(declined["x"], declined["branch"], declined["weight"],
+                            declined["bias"])
+    assert any("native hidden size must be one of" in str(w.message) for w in caught)
