@@ -45,6 +45,11 @@ def test_opcheck_forward_and_backward():
             torch.ops.gfx1010_kernels.rln_backward.default,
             (grads[0], grads[1], outputs[0], inputs[2], outputs[2], outputs[3], outputs[4],
              0.0, True, torch.float16))
+        # Without the weight/bias sums (a pass that needs neither gradient).
+        torch.library.opcheck(
+            torch.ops.gfx1010_kernels.rln_backward.default,
+            (grads[0], grads[1], outputs[0], inputs[2], outputs[2], outputs[3], outputs[4],
+             0.0, True, torch.float16, False))
 
 
 @pytest.mark.parametrize("implementation", ["gfx950", "auto"])
@@ -71,6 +76,34 @@ def test_compiled_step_matches_eager_bitwise(implementation, shape, dropout_p):
             results.append([host(t) for t in outputs] + [host(t.grad) for t in leaves])
     for eager, traced in zip(*results):
         assert_bitwise(traced, eager, "compiled vs eager")
+
+
+@pytest.mark.parametrize("backend", ["inductor", "aot_eager"])
+def test_compiled_step_with_frozen_parameters(backend):
+    """A compiled training step whose LayerNorm weight and bias are frozen:
+    the backward asks the op for no weight/bias sums, its input gradients
+    equal eager's bit for bit, and the frozen parameters get no gradient."""
+    shape = (4, 64, 768)
+    inputs = make_inputs(shape, torch.float16, seed=13)
+    grads = make_grads(shape, seed=14)
+
+    def step(x, branch, weight, bias):
+        return residual_layer_norm(x, branch, weight, bias, dropout_p=0.1,
+                                   implementation="gfx950")
+
+    compiled = torch.compile(step, backend=backend, fullgraph=True)
+    results = []
+    for function in (step, compiled):
+        x, branch = (t.detach().clone().requires_grad_(True) for t in inputs[:2])
+        weight, bias = (t.detach().clone() for t in inputs[2:])
+        torch.cuda.manual_seed(77)
+        outputs = function(x, branch, weight, bias)
+        torch.autograd.backward(outputs, grads)
+        torch.cuda.synchronize()
+        assert weight.grad is None and bias.grad is None
+        results.append([host(t) for t in outputs] + [host(x.grad), host(branch.grad)])
+    for eager, traced in zip(*results):
+        assert_bitwise(traced, eager, "compiled vs eager, frozen parameters")
 
 
 def test_compiled_auto_falls_back_for_non_native_hidden_size():
