@@ -510,7 +510,10 @@ def public_api_steps(torch, workload: Workload, stream, steps: int = 96) -> dict
     allocation per step; `host_us` is the CPU
     time to issue one eager forward and one eager step (perf_counter over
     `steps` calls, no synchronization inside: when it exceeds the GPU's time
-    the eager step is host-bound), and `engine_floor` that of
+    the eager step is host-bound), `forward_no_grad` that of one forward
+    under torch.no_grad() (an inference call, which records no graph; for the
+    fused path also `forward_no_grad_auto`, the same call with
+    implementation="auto"), and `engine_floor` that of
     torch.autograd.grad over one elementwise op (x * 2), PyTorch's own floor
     for a step with a CUDA backward; `graph_steps` replays HIP graphs holding 1,
     8 and 32 consecutive steps (the op draws a fresh dropout mask on every
@@ -579,11 +582,21 @@ def public_api_steps(torch, workload: Workload, stream, steps: int = 96) -> dict
                 (x, *_), grads = next_set()
                 return torch.autograd.grad((x * 2.0,), (x,), (grads[0],))
 
+            def forward_auto():
+                x, branch, weight_, bias_ = next_set()[0]
+                return residual_layer_norm(
+                    x, branch, weight_, bias_, dropout_p=workload.dropout_p, eps=EPS,
+                    training=workload.training)
+
             for _ in range(10):
                 step()
             entry = {"eager": timed(step, steps),
                      "host_us": {"forward": host_us(forward, steps), "step": host_us(step, steps),
                                  "engine_floor": host_us(engine_floor, steps)}}
+            with torch.no_grad():
+                entry["host_us"]["forward_no_grad"] = host_us(forward, steps)
+                if implementation == "gfx950":
+                    entry["host_us"]["forward_no_grad_auto"] = host_us(forward_auto, steps)
             graph_steps = {}
             for count in GRAPH_STEPS:
                 graph = torch.cuda.CUDAGraph()
