@@ -276,3 +276,43 @@ def test_backward_skips_the_parameter_sums_it_does_not_need(path):
     assert_bitwise(host(frozen[0].grad), host(full[0]), "frozen grad_x")
     assert_bitwise(host(frozen[1].grad), host(full[1]), "frozen grad_branch")
     assert frozen[2].grad is None and frozen[3].grad is None
+
+
+@pytest.mark.parametrize("deterministic", [False, True], ids=["atomic", "deterministic"])
+def test_training_step_allocates_only_its_outputs_and_saved_state(deterministic):
+    """Device memory of one training step through the public API: the forward
+    allocates `updated`, `normalized`, one row-statistics tensor (mean, rstd
+    and the dropout mask words, each 256-byte aligned) and the two
+    weight/bias sums; the backward adds grad_x, grad_branch and, in
+    deterministic mode, the per-block partials. Nothing else: no copy of an
+    input or of an upstream gradient (the caching allocator rounds each
+    allocation up to 512 bytes)."""
+    from gfx1010_kernels import _cabi
+
+    rows, hidden = 4096, 1024
+    inputs = make_inputs((rows, hidden), torch.float16, seed=91)
+    grads = make_grads((rows, hidden), seed=92)
+    leaves = [t.detach().clone().requires_grad_(True) for t in inputs]
+
+    def rounded(nbytes):
+        return (nbytes + 511) // 512 * 512
+
+    aligned_rows = (rows + 63) // 64 * 64
+    forward_bytes = (2 * rounded(rows * hidden * 4)
+                     + rounded(4 * (2 * aligned_rows + rows * hidden // 32))
+                     + 2 * rounded(hidden * 4))
+    workspace = _cabi.backward_workspace_bytes(rows, hidden, deterministic)
+    backward_bytes = (rounded(rows * hidden * 4) + rounded(rows * hidden * 2)
+                      + (rounded(workspace) if workspace else 0))
+
+    with deterministic_algorithms(deterministic):
+        torch.cuda.synchronize()
+        base = torch.cuda.memory_allocated()
+        outputs = residual_layer_norm(*leaves, dropout_p=0.1, implementation="gfx950")
+        assert torch.cuda.memory_allocated() - base == forward_bytes
+        torch.cuda.reset_peak_memory_stats()
+        gradients = torch.autograd.grad(outputs, leaves, grads)
+        torch.cuda.synchronize()
+        peak = torch.cuda.max_memory_allocated() - base
+    assert peak == forward_bytes + backward_bytes, (peak, forward_bytes, backward_bytes)
+    assert gradients[1].dtype == torch.float16
