@@ -316,3 +316,23 @@ def test_training_step_allocates_only_its_outputs_and_saved_state(deterministic)
         peak = torch.cuda.max_memory_allocated() - base
     assert peak == forward_bytes + backward_bytes, (peak, forward_bytes, backward_bytes)
     assert gradients[1].dtype == torch.float16
+
+
+def test_inference_call_keeps_only_its_outputs():
+    """Under torch.no_grad() a call keeps `updated` and `normalized` alone: no
+    saved state, no gradient sums (the row statistics it writes are freed
+    when it returns)."""
+    rows, hidden = 4096, 1024
+    inputs = [t.detach().clone().requires_grad_(True)
+              for t in make_inputs((rows, hidden), torch.float16, seed=93)]
+    torch.cuda.synchronize()
+    base = torch.cuda.memory_allocated()
+    with torch.no_grad():
+        updated, normalized = residual_layer_norm(*inputs, dropout_p=0.1,
+                                                  normalized_dtype=torch.bfloat16,
+                                                  implementation="gfx950")
+    torch.cuda.synchronize()
+    rounded = lambda nbytes: (nbytes + 511) // 512 * 512  # noqa: E731
+    assert torch.cuda.memory_allocated() - base == (rounded(rows * hidden * 4)
+                                                    + rounded(rows * hidden * 2))
+    assert normalized.dtype == torch.bfloat16 and updated.grad_fn is None
