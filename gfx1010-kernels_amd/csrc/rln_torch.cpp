@@ -643,7 +643,9 @@ bool fused_inputs_supported(const at::Tensor& x, const at::Tensor& branch,
           && bias.is_contiguous())) {
         return false;
     }
-    return dropout_p >= 0.0 && dropout_p < 1.0 && eps > 0.0 && x.numel() > 0;
+    // The Python comparisons exactly (`not 0 <= p < 1`, `eps <= 0`), NaN
+    // included: a NaN eps has no reason there, and the op itself rejects it.
+    return dropout_p >= 0.0 && dropout_p < 1.0 && !(eps <= 0.0) && x.numel() > 0;
 }
 
 // `residual_layer_norm` for inputs the fused kernels serve, else None (no

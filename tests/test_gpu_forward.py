@@ -186,6 +186,10 @@ def test_auto_fast_check_accepts_exactly_what_the_reasons_accept():
         "dropout 1": (base, 1.0, 1e-5),
         "dropout negative": (base, -0.1, 1e-5),
         "eps 0": (base, 0.1, 0.0),
+        "dropout nan": (base, float("nan"), 1e-5),
+        # No reason in Python (nan <= 0 is false): accepted, and the op itself
+        # rejects it ("eps must be positive"), as it did before the check.
+        "valid for the reasons, eps nan": (base, 0.1, float("nan")),
         "empty": (inputs(rows=0), 0.1, 1e-5),
     }
     for name, (tensors, dropout_p, eps) in cases.items():
@@ -194,6 +198,9 @@ def test_auto_fast_check_accepts_exactly_what_the_reasons_accept():
                     and args[0].shape[-1] in _NATIVE_SIZES)
         assert _C.fused_inputs_supported(*args, dropout_p, eps) == expected, name
         assert expected == name.startswith("valid"), name
+    with pytest.raises(RuntimeError, match="eps must be positive"):
+        residual_layer_norm(base["x"], base["branch"], base["weight"], base["bias"],
+                            eps=float("nan"))
 
     served = residual_layer_norm(base["x"], base["branch"], base["weight"], base["bias"])
     strict = residual_layer_norm(base["x"], base["branch"], base["weight"], base["bias"],
