@@ -153,3 +153,53 @@ def test_first_call_of_a_process_under_capture():
                             capture_output=True, text=True, timeout=240)
     assert result.returncode == 0, result.stdout + result.stderr
     assert "first call under capture: ok" in result.stdout
+
+
+@pytest.mark.parametrize("training,dropout_p", [(False, 0.0), (True, 0.1)],
+                         ids=["eval", "dropout"])
+def test_captured_inference_calls_replay(training, dropout_p):
+    """Public calls under torch.no_grad() (the forward-only path, no autograd
+    node) captured in a HIP graph, as a serving loop would: each replay over
+    new values copied into the static inputs equals, bit for bit, an eager
+    call on those values from the same generator state, with eager work
+    between replays; with dropout, each replay draws from a new offset of the
+    generator (a fresh mask), without dropout none is consumed."""
+    from gfx1010_kernels import residual_layer_norm
+
+    rows, hidden = 257, 1024
+    x, branch, weight, bias = make_inputs((rows, hidden), torch.float16, seed=31)
+    fresh = [make_inputs((rows, hidden), torch.float16, seed=40 + i)[:2] for i in range(3)]
+    generator = torch.cuda.default_generators[0]
+    torch.cuda.manual_seed(11)
+
+    def call(x_values, branch_values):
+        return residual_layer_norm(x_values, branch_values, weight, bias, dropout_p=dropout_p,
+                                   training=training, implementation="gfx950")
+
+    with torch.no_grad():
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            call(x, branch)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            captured = call(x, branch)
+        offsets = []
+        for x_values, branch_values in fresh:
+            x.copy_(x_values)
+            branch.copy_(branch_values)
+            offset = generator.get_offset()
+            offsets.append(offset)
+            graph.replay()
+            torch.cuda.synchronize()
+            replayed = [host(t).copy() for t in captured]
+            generator.set_offset(offset)
+            eager = call(x_values, branch_values)  # eager work between replays
+            torch.cuda.synchronize()
+            for actual, expected in zip(replayed, eager):
+                assert np.array_equal(actual.view(np.uint32), host(expected).view(np.uint32))
+    if dropout_p > 0.0:
+        assert offsets[0] < offsets[1] < offsets[2]
+    else:
+        assert offsets[0] == offsets[1] == offsets[2]
