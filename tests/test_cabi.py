@@ -181,6 +181,19 @@ def test_glue_module_imports_and_checks_device_first():
     assert _C.target_arch() == "gfx950"
 
 
+def test_glue_auto_check_declines_host_tensors_without_error():
+    """The auto path's C++ check answers False for host tensors (the
+    reference's first reason, "x must be a HIP tensor"), and the checked entry
+    point returns None instead of raising, so the Python path works out the
+    reason and falls back."""
+    from gfx1010_kernels import _C
+
+    x = torch.zeros(4, 768)
+    args = (x, x.half(), torch.ones(768), torch.zeros(768), 0.1, 1e-5)
+    assert _C.fused_inputs_supported(*args) is False
+    assert _C.residual_layer_norm_if_supported(*args, True, 128, 64, 64, 1, None) is None
+
+
 def test_noalloc_backward_refuses_partials_above_its_scratch_before_any_gpu_work():
     """rln_backward_noalloc checks its arguments and the size of the weight /
     bias partials on the host, before any HIP call: a shape whose
