@@ -26,10 +26,12 @@ Prints one JSON line:
                F.layer_norm, forward + autograd) on this host's cores
   step_us_spread  p20 / median / p80 of the step time over batches of 25
   copy_ceiling    a plain device copy's GB/s at ~100 MB per launch
-  ceiling_us   the streaming ceiling of this workload: one-pass non-temporal
-               kernels with the forward's and the backward's exact streams
-               (csrc/rln_ceiling.hip), timed like the op's kernels, and the
-               op's times as a fraction of them
+  ceiling_us   the measured streaming floor of this workload: the fastest of
+               benchmarks/rln_probe.hip's streaming kernels (block size,
+               bytes in flight per lane, look-ahead, 128-bit fp16, cache
+               policy, LDS staging, grid) with the forward's and the
+               backward's exact streams, timed like the op's kernels over
+               the same buffers, and the op's times as a fraction of them
   parity       the timed C-ABI step (set 0, its Philox offset, weight/bias
                sums accumulated from zero) checked before timing against the
                PyTorch decomposition in float64 on this GPU, with the kernel's
@@ -60,9 +62,10 @@ published measurement, run on this GPU: public-API forward and training-step
 speedups over the PyTorch decomposition at B = 1, H = 384, T = 128 .. 4096,
 beside the speedups the reference publishes for gfx1010. ``--config NAME``
 (repeatable) runs only the named sweep configurations and skips the C1 line,
-so that a profiler run sees one configuration's launches. ``--ceiling`` adds
-one line per configuration (C1 and the sweep's, or the ``--config`` ones)
-with the op's and the streaming-ceiling kernels' times side by side.
+so that a profiler run sees one configuration's launches. ``--ceiling`` prints
+every probe point of C1 (one ``probe_table`` line) and adds one line per
+other configuration with the probe's streams (or the ``--config`` ones) with
+the op's and the probe floor's times side by side.
 
 Algorithmic bytes per row (H = hidden, bb = branch bytes, mask H/8 bytes when
 dropping):
@@ -95,7 +98,7 @@ EPS = 1e-5
 TRAFFIC_FILE = REPO / "profiles" / "rln_backward_c1_traffic.json"
 CSRC = REPO / "gfx1010-kernels_amd" / "csrc"
 KERNEL_SOURCES = ("rln_device.h", "rln_api.hip", "rln_hidden.hip")
-CEILING_LIBRARY = REPO / "gfx1010-kernels_amd" / "gfx1010_kernels" / "librln_ceiling_gfx950.so"
+PROBE_LIBRARY = REPO / "benchmarks" / "librln_probe_gfx950.so"
 # Back-to-back launches timed for the roofline kernel and the ceiling kernels.
 ROOFLINE_LAUNCHES = 400
 
@@ -232,6 +235,9 @@ def parse_args():
                              "C=384, L=8), original vs fused normalization flow")
     parser.add_argument("--reference-table", action="store_true",
                         help="also print the reference's published speedup table, measured here")
+    parser.add_argument("--reference-matrix", action="store_true",
+                        help="also print the reference's end-to-end matrix (every native hidden "
+                             "size, forward and train, fused vs torch) at B=1, T=1024/2048/4096")
     parser.add_argument("--ceiling", action="store_true",
                         help="add op-vs-streaming-ceiling lines per configuration")
     parser.add_argument("--quick", action="store_true",
@@ -242,6 +248,16 @@ def parse_args():
     parser.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                         help="write profiles/rln_backward_c1_traffic.json from two rocprofv3 "
                              "--pmc output directories (no GPU needed)")
+    parser.add_argument("--ab", action="append", default=[], metavar="NAME=DEFINES",
+                        help="A/B run: also time a variant build of the library with the "
+                             "comma-separated compile-time switches (e.g. "
+                             "'nt=RLN_STORE_POLICY=2'), built into benchmarks/variants/ if "
+                             "missing, alternated round by round with the default build on C1 "
+                             "(or the --config workloads); repeatable")
+    parser.add_argument("--ab-rounds", type=int, default=5,
+                        help="rounds of an A/B run (each times every build once)")
+    parser.add_argument("--ab-build", action="store_true",
+                        help="rebuild the --ab variants even where a build exists")
     parser.add_argument("--config", action="append", default=[], metavar="NAME",
                         help="run only this sweep configuration (repeatable; e.g. 'C2 H=1024'), "
                              "without the C1 line: one kernel's launches per run, for counters")
@@ -321,6 +337,88 @@ def reference_table(torch, warmup: int = 100, reps: int = 1000,
                 "reference_speedup_gfx1010": published[index],
             }
         lines.append(line)
+    return lines
+
+
+# The reference's matrix script: every native hidden size at one (B, T), its
+# seed, branch dtype and dropout (benchmarks/benchmark_residual_layer_norm_matrix.py:
+# 13-14, :135-152 defaults B = 1, T = 1024, p = 0.15, fp16 branch, 50 warmup
+# and 500 timed calls).
+MATRIX_HIDDEN = (128, 256, 384, 512, 768, 1024)
+MATRIX_SEED = 29_072_026
+MATRIX_SEQUENCES = (1024, 2048, 4096)
+
+
+def reference_matrix(torch, batch: int = 1, sequences: tuple[int, ...] = MATRIX_SEQUENCES,
+                     dropout_p: float = 0.15, warmup: int = 50, reps: int = 500) -> list[dict]:
+    """The reference's end-to-end matrix on this GPU
+    (benchmarks/benchmark_residual_layer_norm_matrix.py:52-227): for every
+    hidden size, the public forward call and the forward + autograd.grad
+    "train" call over fresh leaves, implementation="gfx950" against
+    implementation="torch" on the same inputs (x, weight, bias fp32 and an
+    fp16 branch from torch.randn after seeding SEED + hidden; upstream
+    gradients randn_like), one CUDA-event pair around each call, median /
+    p20 / p80 (linear quantiles, as its quantile()) of `reps` calls after
+    `warmup`, and speedup = torch median / fused median. One line per
+    (T, hidden, mode)."""
+    from gfx1010_kernels import residual_layer_norm
+
+    def quantile(values, fraction):
+        ordered = sorted(values)
+        position = (len(ordered) - 1) * fraction
+        lower, upper = int(position // 1), -int(-position // 1)
+        weight = position - lower
+        return ordered[lower] * (1.0 - weight) + ordered[upper] * weight
+
+    def timed(call, seed):
+        torch.manual_seed(seed)
+        for _ in range(warmup):
+            call()
+        torch.cuda.synchronize()
+        torch.manual_seed(seed)
+        events = []
+        for _ in range(reps):
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record()
+            call()
+            end.record()
+            events.append((start, end))
+        torch.cuda.synchronize()
+        samples = [start.elapsed_time(end) for start, end in events]
+        return {"median_ms": round(quantile(samples, 0.5), 5),
+                "p20_ms": round(quantile(samples, 0.2), 5),
+                "p80_ms": round(quantile(samples, 0.8), 5)}
+
+    lines = []
+    for sequence in sequences:
+        for hidden in MATRIX_HIDDEN:
+            seed = MATRIX_SEED + hidden
+            torch.manual_seed(seed)
+            shape = (batch, sequence, hidden)
+            source = (torch.randn(shape, device="cuda"),
+                      torch.randn(shape, device="cuda", dtype=torch.float16),
+                      torch.randn(hidden, device="cuda"), torch.randn(hidden, device="cuda"))
+            grads = (torch.randn_like(source[0]), torch.randn_like(source[0]))
+            for mode in ("forward", "train"):
+                results = {}
+                for implementation in ("torch", "gfx950"):
+                    leaves = tuple(t.detach().clone().requires_grad_(True) for t in source)
+
+                    def call(leaves=leaves, implementation=implementation, mode=mode):
+                        outputs = residual_layer_norm(*leaves, dropout_p=dropout_p,
+                                                      training=True,
+                                                      implementation=implementation)
+                        if mode == "train":
+                            torch.autograd.grad(outputs, leaves, grads)
+
+                    results[implementation] = timed(call, seed + (mode == "train"))
+                lines.append({
+                    "kind": "reference_matrix", "B": batch, "T": sequence, "C": hidden,
+                    "mode": mode, "branch_dtype": "float16", "dropout_p": dropout_p,
+                    "warmup": warmup, "reps": reps, **results,
+                    "speedup": round(results["torch"]["median_ms"]
+                                     / results["gfx950"]["median_ms"], 3)})
     return lines
 
 
@@ -1095,60 +1193,162 @@ def parity_self_check(torch, runner: "Runner") -> dict:
     return errors
 
 
-def ceiling_library():
-    library = ctypes.CDLL(str(CEILING_LIBRARY))
-    pointer, size = ctypes.c_void_p, ctypes.c_int64
-    library.rln_ceiling_forward.argtypes = [pointer, pointer, ctypes.c_int, pointer, pointer,
-                                            ctypes.c_int, pointer, pointer, pointer, size, size,
-                                            pointer]
-    library.rln_ceiling_backward.argtypes = [pointer, pointer, ctypes.c_int, pointer, pointer,
-                                             pointer, pointer, pointer, pointer, ctypes.c_int,
-                                             size, size, pointer]
+def probe_library():
+    library = ctypes.CDLL(str(PROBE_LIBRARY))
+    library.rln_probe_variant_count.restype = ctypes.c_int
+    library.rln_probe_variant_name.restype = ctypes.c_char_p
+    library.rln_probe_variant_name.argtypes = [ctypes.c_int]
+    library.rln_probe_variant_kind.argtypes = [ctypes.c_int]
+    library.rln_probe_variant_threads.argtypes = [ctypes.c_int]
+    library.rln_probe_one_step_blocks.restype = ctypes.c_int64
+    library.rln_probe_one_step_blocks.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64]
+    library.rln_probe_launch.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
+                                         ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p]
+    library.rln_probe_atomic_combine.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
+                                                 ctypes.c_int, ctypes.c_int64, ctypes.c_int,
+                                                 ctypes.c_void_p]
+    library.rln_probe_empty_launches.argtypes = [ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                                 ctypes.c_void_p]
     return library
 
 
-def ceiling_times(torch, runner: "Runner", library, launches: int = ROOFLINE_LAUNCHES) -> dict:
-    """The streaming ceiling of the runner's workload: csrc/rln_ceiling.hip's
-    forward- and backward-shaped passes over the runner's own buffers (same
-    rotated sets), timed like the op's kernels; microseconds per launch."""
+# Copies of the weight/bias sums the atomic-combine probe spreads 256 blocks over.
+PROBE_ATOMIC_COPIES = (1, 2, 4, 8, 16, 64, 256)
+PROBE_EMPTY_BLOCKS = (1, 256, 768, 2048, 3072)
+
+
+def probe_fixed_costs(torch, runner: "Runner", library, hidden: int, repeats: int = 200) -> dict:
+    """Two fixed costs of a pass, each from `repeats` launches issued back to
+    back by a C loop (microseconds per launch): the weight/bias combine alone
+    (256 blocks of 512 threads adding 2 x hidden fp32 values each with
+    atomics, spread over 1..256 copies of the sums, consecutive blocks in
+    different copies or in the same one), and an empty kernel of 1..3072
+    blocks of 256 threads (a launch's own cost on the GPU)."""
+    handle = ctypes.c_void_p(runner.handle)
+    sums = torch.zeros(max(PROBE_ATOMIC_COPIES) * 2 * hidden, device="cuda")
+    atomic = {}
+    for ranges, label in ((0, "interleaved"), (1, "block ranges")):
+        atomic[label] = {}
+        for copies in PROBE_ATOMIC_COPIES:
+            def batch(_, copies=copies, ranges=ranges):
+                if library.rln_probe_atomic_combine(sums.data_ptr(), hidden, copies, ranges, 256,
+                                                    repeats, handle):
+                    raise RuntimeError("rln_probe_atomic_combine failed")
+            batch(0)
+            atomic[label][str(copies)] = round(runner.timed(batch, 1) * 1e3 / repeats, 3)
+    empty = {}
+    for blocks in PROBE_EMPTY_BLOCKS:
+        def batch(_, blocks=blocks):
+            if library.rln_probe_empty_launches(blocks, 256, repeats, handle):
+                raise RuntimeError("rln_probe_empty_launches failed")
+        batch(0)
+        empty[str(blocks)] = round(runner.timed(batch, 1) * 1e3 / repeats, 3)
+    return {"atomic_combine_us_by_copies": atomic, "empty_kernel_us_by_blocks": empty}
+
+
+# Persistent grids of the probe: waves per CU (each a whole number of blocks).
+PROBE_WAVES_PER_CU = (4, 8, 12, 16, 24, 32)
+# Probe points re-timed at the full launch count, per pass.
+PROBE_FINALISTS = 6
+
+
+def probe_applies(workload: Workload) -> bool:
+    """The probe moves an fp16 branch and fp32 normalized values (and their
+    gradients), with a mask: the headline configuration's streams."""
+    return (workload.branch == "f16" and workload.normalized == "f32" and workload.dropping
+            and workload.rows * workload.hidden * 4 <= (1 << 31))
+
+
+def probe_floor(torch, runner: "Runner", library, launches: int = ROOFLINE_LAUNCHES,
+                table: bool = False) -> dict:
+    """The measured streaming floor of the runner's workload: every variant of
+    benchmarks/rln_probe.hip (block size, units per lane, look-ahead, 128-bit
+    fp16, cache policy, LDS staging) on every grid (one step per thread, and
+    persistent grids of PROBE_WAVES_PER_CU waves per CU), over the runner's
+    own rotated sets. Each point is timed over launches / 4 back-to-back
+    launches; the PROBE_FINALISTS fastest per pass are timed again over
+    `launches`, twice, interleaved (the faster run counts); then the fastest
+    forward and backward are timed alternating, as the step runs them.
+    Microseconds per launch."""
     w = runner.w
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    arrays = []
+    for t in runner.sets:
+        tensors = (t["x"], t["branch"], t["updated"], t["normalized"], t["mask"], t["mean"],
+                   t["rstd"], t["grad_updated"], t["grad_normalized"], t["updated"], t["mask"],
+                   t["mean"], t["rstd"], t["grad_x"], t["grad_branch"])
+        arrays.append((ctypes.c_void_p * len(tensors))(*[x.data_ptr() for x in tensors]))
+    handle = ctypes.c_void_p(runner.handle)
+    rows, hidden = ctypes.c_int64(w.rows), ctypes.c_int64(w.hidden)
 
-    def forward(step):
-        t = runner.sets[step % len(runner.sets)]
-        status = library.rln_ceiling_forward(
-            t["x"].data_ptr(), t["branch"].data_ptr(), w.branch_bytes, t["updated"].data_ptr(),
-            t["normalized"].data_ptr(), w.normalized_bytes,
-            t["mask"].data_ptr() if w.dropping else None, t["mean"].data_ptr(),
-            t["rstd"].data_ptr(), w.rows, w.hidden, runner.handle)
-        if status:
-            raise RuntimeError(f"rln_ceiling_forward failed: {status}")
+    def launcher(index, blocks):
+        count = ctypes.c_int64(blocks)
 
-    def backward(step):
-        t = runner.sets[step % len(runner.sets)]
-        status = library.rln_ceiling_backward(
-            t["grad_updated"].data_ptr(), t["grad_normalized"].data_ptr(), w.normalized_bytes,
-            t["updated"].data_ptr(), t["mask"].data_ptr() if w.dropping else None,
-            t["mean"].data_ptr(), t["rstd"].data_ptr(), t["grad_x"].data_ptr(),
-            t["grad_branch"].data_ptr(), w.branch_bytes, w.rows, w.hidden, runner.handle)
-        if status:
-            raise RuntimeError(f"rln_ceiling_backward failed: {status}")
+        def launch(step):
+            if library.rln_probe_launch(index, arrays[step % len(arrays)], rows, hidden, count,
+                                        handle):
+                raise RuntimeError(f"rln_probe_launch({index}, {blocks}) failed")
+        return launch
 
-    for index in range(2 * len(runner.sets)):
+    points = {0: [], 1: []}
+    for index in range(library.rln_probe_variant_count()):
+        kind = library.rln_probe_variant_kind(index)
+        threads = library.rln_probe_variant_threads(index)
+        one_step = library.rln_probe_one_step_blocks(index, w.rows, w.hidden)
+        grids = {"one step per thread": one_step}
+        for waves in PROBE_WAVES_PER_CU:
+            if waves % (threads // 64) == 0:
+                blocks = waves * cus // (threads // 64)
+                if blocks < one_step:
+                    grids[f"{waves} waves/CU"] = blocks
+        if threads >= 512:
+            # One block on each of half the CUs: whether half the CUs can
+            # stream the pass as fast (half the blocks to combine).
+            grids["one block on half the CUs"] = cus // 2
+        if kind == 2:
+            continue
+        name = library.rln_probe_variant_name(index).decode()
+        for grid, blocks in grids.items():
+            launch = launcher(index, blocks)
+            for step in range(2 * len(arrays)):
+                launch(step)
+            us = runner.timed(launch, max(launches // 4, 1)) * 1e3
+            points[kind].append({"variant": name, "grid": grid, "blocks": blocks,
+                                 "index": index, "us": round(us, 3)})
+    best = {}
+    for kind, label in ((0, "fwd"), (1, "bwd")):
+        finalists = sorted(points[kind], key=lambda point: point["us"])[:PROBE_FINALISTS]
+        for point in finalists:
+            point["us_full"] = []
+        for _ in range(2):
+            for point in finalists:
+                point["us_full"].append(
+                    runner.timed(launcher(point["index"], point["blocks"]), launches) * 1e3)
+        for point in finalists:
+            point["us_full"] = round(min(point["us_full"]), 3)
+        best[label] = min(finalists, key=lambda point: point["us_full"])
+    forward = launcher(best["fwd"]["index"], best["fwd"]["blocks"])
+    backward = launcher(best["bwd"]["index"], best["bwd"]["blocks"])
+
+    def step(index):
         forward(index)
-        if w.backward:
-            backward(index)
-    result = {"fwd": round(runner.timed(forward, launches) * 1e3, 3)}
-    if w.backward:
-        result["bwd"] = round(runner.timed(backward, launches) * 1e3, 3)
+        backward(index)
 
-        def step(index):
-            forward(index)
-            backward(index)
-
-        result["step"] = round(runner.timed(step, launches) * 1e3, 3)
-    result["kind"] = ("one-pass non-temporal streaming kernels with the op's exact streams "
-                      f"(csrc/rln_ceiling.hip), {launches} launches back to back, "
-                      f"{len(runner.sets)} rotated sets")
+    result = {
+        "fwd": best["fwd"]["us_full"],
+        "fwd_probe": f'{best["fwd"]["variant"]}, {best["fwd"]["grid"]} ({best["fwd"]["blocks"]} blocks)',
+        "bwd": best["bwd"]["us_full"],
+        "bwd_probe": f'{best["bwd"]["variant"]}, {best["bwd"]["grid"]} ({best["bwd"]["blocks"]} blocks)',
+        "step": round(runner.timed(step, launches) * 1e3, 3),
+        "fixed_costs": probe_fixed_costs(torch, runner, library, w.hidden),
+        "points": len(points[0]) + len(points[1]),
+        "kind": ("fastest of the benchmarks/rln_probe.hip streaming variants with the op's "
+                 f"exact streams, {launches} launches back to back, {len(runner.sets)} rotated "
+                 "sets; step = the fastest forward and backward alternating"),
+    }
+    if table:
+        result["table"] = sorted(points[0] + points[1],
+                                 key=lambda point: (point["variant"][:3], point["us"]))
     return result
 
 
@@ -1315,6 +1515,10 @@ def main() -> int:
             print(f"[bench] calibration copy of {args.calibrate_copy_mib} MiB done", flush=True)
             del source, destination
 
+    if args.ab:
+        chosen = [workload for workload in sweep_workloads() if workload.name in args.config]
+        return run_ab(torch, _cabi, stream, args, chosen or [C1])
+
     if args.config:
         chosen = [workload for workload in sweep_workloads() if workload.name in args.config]
         if args.ceiling:
@@ -1334,7 +1538,8 @@ def main() -> int:
         # --quick (the profiling runs) launches the kernels only as the step
         # does, so per-kernel counter averages describe the step's launches.
         timing = runner.measure(args.warmup, args.steps, input_grads=not args.quick)
-        ceiling = None if args.quick else ceiling_times(torch, runner, ceiling_library())
+        ceiling = None if args.quick else probe_floor(torch, runner, probe_library(),
+                                                      table=args.ceiling)
         del runner
         print(f"[bench] C1: step {timing['step_ms'] * 1e3:.2f} us, forward "
               f"{timing['forward_ms'] * 1e3:.2f} us, backward {timing['backward_ms'] * 1e3:.2f} us, "
@@ -1346,7 +1551,11 @@ def main() -> int:
         print(json.dumps(result), flush=True)
         if args.sweep:
             run_sweep(torch, library, _cabi, stream, args, sweep_workloads())
+        if args.reference_matrix:
+            for line in reference_matrix(torch):
+                print(json.dumps(line), flush=True)
         return 0
+    probe_table = ceiling.pop("table", None)
     result["ceiling_us"] = {
         **ceiling,
         "op_fwd": round(timing["forward_ms"] * 1e3, 3),
@@ -1372,6 +1581,9 @@ def main() -> int:
         print(f"[bench] CPU baseline (~{args.cpu_seconds:.0f} s)", flush=True)
         result["cpu_baseline"] = cpu_baseline(torch, C1, args.cpu_seconds)
     print(json.dumps(result), flush=True)
+    if probe_table is not None:
+        print(json.dumps({"kind": "probe_table", "workload": C1.describe(),
+                          "points": probe_table}), flush=True)
 
     if args.prenorm:
         line = {"metric": "pre-norm stack fwd+bwd step time (ms)", "higher_is_better": False,
@@ -1387,18 +1599,25 @@ def main() -> int:
         for line in reference_table(torch):
             print(json.dumps(line), flush=True)
 
+    if args.reference_matrix:
+        for line in reference_matrix(torch):
+            print(json.dumps(line), flush=True)
+
     if args.sweep:
         run_sweep(torch, library, _cabi, stream, args, sweep_workloads())
     if args.ceiling:
-        run_ceilings(torch, library, _cabi, stream, args, [C1, *sweep_workloads()])
+        run_ceilings(torch, library, _cabi, stream, args, sweep_workloads())
     return 0
 
 
 def run_ceilings(torch, library, cabi, stream, args, workloads) -> None:
-    """One line per workload: the op's kernels and the streaming-ceiling
-    kernels over the same buffers, microseconds per launch."""
-    ceiling = ceiling_library()
+    """One line per workload whose streams the probe moves (fp16 branch,
+    fp32 normalized, dropping): the op's kernels and the probe's measured
+    streaming floor over the same buffers, microseconds per launch."""
+    probe = probe_library()
     for workload in workloads:
+        if not probe_applies(workload):
+            continue
         torch.cuda.empty_cache()
         large = workload.rows * workload.hidden >= (1 << 26)
         launches = 40 if large else ROOFLINE_LAUNCHES
@@ -1406,7 +1625,7 @@ def run_ceilings(torch, library, cabi, stream, args, workloads) -> None:
             runner = Runner(torch, library, cabi, workload, 2 if large else args.sets, stream)
             timing = runner.measure(min(args.warmup, 10), max(args.steps // 10, 20) if large
                                     else args.steps, launches)
-            limit = ceiling_times(torch, runner, ceiling, launches)
+            limit = probe_floor(torch, runner, probe, launches)
             del runner
         line = {"kind": "ceiling", "workload": workload.describe(),
                 "op_us": {"fwd": round(timing["forward_ms"] * 1e3, 3)}, "ceiling_us": limit}
@@ -1417,6 +1636,79 @@ def run_ceilings(torch, library, cabi, stream, args, workloads) -> None:
             if key in line["op_us"]:
                 line[f"op_over_ceiling_{key}"] = round(line["op_us"][key] / limit[key], 4)
         print(json.dumps(line), flush=True)
+
+
+def parse_ab(specs) -> list[tuple[str, tuple[str, ...]]]:
+    variants = []
+    for spec in specs:
+        name, _, defines = spec.partition("=")
+        if not name or name == "default":
+            raise SystemExit(f"bench.py: --ab {spec!r}: give the variant a name other than "
+                             "'default'")
+        variants.append((name, tuple(define for define in defines.split(",") if define)))
+    return variants
+
+
+def run_ab(torch, cabi, stream, args, workloads) -> int:
+    """Times the default build and each --ab variant build of the library on
+    the same inputs (one Runner per build, same seeds), round by round, so
+    that every build is timed on the same box in alternation. Prints one
+    line per workload with the per-round kernel times of every build and
+    their medians (microseconds); each build's timed path passes the parity
+    self-check first."""
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location(
+        "rln_build", REPO / "gfx1010-kernels_amd" / "build.py")
+    build = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(build)
+    builds = [("default", (), cabi.library())]
+    for name, defines in parse_ab(args.ab):
+        path = build.variant_path(name)
+        if args.ab_build or not path.exists():
+            print(f"[bench] building variant {name}: {', '.join(defines)}", flush=True)
+            build.build_variant(name, defines)
+        builds.append((name, defines, cabi.load(path)))
+    for workload in workloads:
+        torch.cuda.empty_cache()
+        large = workload.rows * workload.hidden >= (1 << 26)
+        sets = 2 if large else args.sets
+        launches = 40 if large else ROOFLINE_LAUNCHES
+        steps = max(args.steps // 10, 20) if large else args.steps
+        rounds = {name: [] for name, _, _ in builds}
+        with torch.cuda.stream(stream):
+            runners = []
+            for name, _, library in builds:
+                runner = Runner(torch, library, cabi, workload, sets, stream)
+                parity = parity_self_check(torch, runner)
+                if not parity["pass"]:
+                    print(f"bench.py: build {name} misses the parity bars on {workload.name}: "
+                          f"{parity}", file=sys.stderr)
+                    return 1
+                runners.append((name, runner))
+            for index in range(args.ab_rounds):
+                for name, runner in runners:
+                    timing = runner.measure(min(args.warmup, 10), steps, launches,
+                                            input_grads=workload.backward)
+                    rounds[name].append({key[:-3]: round(value * 1e3, 3)
+                                         for key, value in timing.items()
+                                         if key.endswith("_ms") and isinstance(value, float)})
+                print(f"[bench] A/B {workload.name} round {index + 1}/{args.ab_rounds}: "
+                      + ", ".join(f"{name} step {rounds[name][-1]['step']:.2f} us"
+                                  for name, _ in runners), flush=True)
+            del runners
+        line = {"kind": "ab", "workload": workload.describe(), "rounds": args.ab_rounds,
+                "builds": {}}
+        for name, defines, _ in builds:
+            keys = rounds[name][0].keys()
+            line["builds"][name] = {
+                "defines": list(defines),
+                "median_us": {key: round(statistics.median(r[key] for r in rounds[name]), 3)
+                              for key in keys},
+                "rounds_us": rounds[name],
+            }
+        print(json.dumps(line), flush=True)
+    return 0
 
 
 def run_sweep(torch, library, cabi, stream, args, workloads) -> None:

@@ -6,8 +6,9 @@ Produces, inside ``gfx1010_kernels/``:
   ``include/rln.h`` (hipcc, device code for gfx950 only);
 * ``_C<EXT_SUFFIX>`` - the PyTorch glue module (g++, host code only), linked
   against ``librln_gfx950.so`` with an ``$ORIGIN`` run path;
-* ``librln_ceiling_gfx950.so`` - the streaming-ceiling kernels bench.py times
-  beside the operator (``csrc/rln_ceiling.hip``; not part of the operator).
+and, outside the package, ``benchmarks/librln_probe_gfx950.so`` - the
+streaming-probe kernels bench.py times beside the operator
+(``benchmarks/rln_probe.hip``; not part of the operator).
 
 Run ``python gfx1010-kernels_amd/build.py`` or call :func:`build`.
 """
@@ -31,7 +32,8 @@ ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 ARCH = "gfx950"
 LIBRARY = PACKAGE / f"librln_{ARCH}.so"
 GLUE = PACKAGE / f"_C{sysconfig.get_config_var('EXT_SUFFIX')}"
-CEILING = PACKAGE / f"librln_ceiling_{ARCH}.so"
+PROBE_SOURCE = REPO / "benchmarks" / "rln_probe.hip"
+PROBE = REPO / "benchmarks" / f"librln_probe_{ARCH}.so"
 
 # Device-code flags. Packed fp32 instructions are disabled (the compiler may
 # otherwise form v_pk_{add,mul,fma}_f32 from float code); FP contraction is
@@ -85,18 +87,22 @@ def _compile_object(source: Path, output: Path, defines: list[str]) -> Path:
     return output
 
 
-def build_library(jobs: int | None = None) -> Path:
-    """Compile the gfx950 kernels and C ABI into librln_gfx950.so."""
-    BUILD_DIR.mkdir(parents=True, exist_ok=True)
-    units = [(CSRC / "rln_api.hip", BUILD_DIR / "rln_api.o", [])]
+def build_library(jobs: int | None = None, defines: tuple[str, ...] = (),
+                  output: Path = LIBRARY, build_dir: Path = BUILD_DIR) -> Path:
+    """Compile the gfx950 kernels and C ABI into librln_gfx950.so (or, with
+    extra -D `defines`, a variant build at `output`)."""
+    build_dir.mkdir(parents=True, exist_ok=True)
+    extra = [f"-D{define}" for define in defines]
+    units = [(CSRC / "rln_api.hip", build_dir / "rln_api.o", extra)]
     units += [
-        (CSRC / "rln_hidden.hip", BUILD_DIR / f"rln_hidden_{hidden}.o",
-         [f"-DRLN_HIDDEN={hidden}", f"-DRLN_PASSES={1 | (hidden in FIXED_BACKWARD) << 1}"])
+        (CSRC / "rln_hidden.hip", build_dir / f"rln_hidden_{hidden}.o",
+         [*extra, f"-DRLN_HIDDEN={hidden}",
+          f"-DRLN_PASSES={1 | (hidden in FIXED_BACKWARD) << 1}"])
         for hidden in HIDDEN_SIZES
     ]
     units += [
-        (CSRC / "rln_hidden.hip", BUILD_DIR / f"rln_wide_{v}x{p}.o",
-         [f"-DRLN_WIDE_V={v}", f"-DRLN_WIDE_P={p}",
+        (CSRC / "rln_hidden.hip", build_dir / f"rln_wide_{v}x{p}.o",
+         [*extra, f"-DRLN_WIDE_V={v}", f"-DRLN_WIDE_P={p}",
           f"-DRLN_PASSES={((v, p) in WIDE_FORWARD) | ((v, p) in WIDE_BACKWARD) << 1}"])
         for v, p in sorted(set(WIDE_FORWARD) | set(WIDE_BACKWARD))
     ]
@@ -104,22 +110,39 @@ def build_library(jobs: int | None = None) -> Path:
     with ThreadPoolExecutor(max_workers=workers) as pool:
         objects = list(pool.map(lambda unit: _compile_object(*unit), units))
     hipcc = str(ROCM / "bin" / "hipcc")
-    temporary = LIBRARY.with_name(LIBRARY.name + ".tmp")
+    output.parent.mkdir(parents=True, exist_ok=True)
+    temporary = output.with_name(output.name + ".tmp")
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects),
-          f"-Wl,-soname,{LIBRARY.name}", "-Wl,-z,defs", "-o", str(temporary)])
-    os.replace(temporary, LIBRARY)
-    return LIBRARY
+          f"-Wl,-soname,{output.name}", "-Wl,-z,defs", "-o", str(temporary)])
+    os.replace(temporary, output)
+    return output
 
 
-def build_ceiling() -> Path:
-    """Compile the benchmark's streaming-ceiling kernels into their own library."""
-    BUILD_DIR.mkdir(parents=True, exist_ok=True)
+VARIANTS = REPO / "benchmarks" / "variants"
+
+
+def variant_path(name: str) -> Path:
+    return VARIANTS / f"librln_{ARCH}_{name}.so"
+
+
+def build_variant(name: str, defines: tuple[str, ...], jobs: int | None = None) -> Path:
+    """A variant build of the library with compile-time switches (the RLN_*
+    macros of rln_device.h) for the benchmark's A/B runs (bench.py --ab),
+    at benchmarks/variants/librln_gfx950_<name>.so."""
+    if not name.replace("_", "").replace("-", "").isalnum():
+        raise ValueError(f"variant name {name!r}: letters, digits, '-' and '_' only")
+    return build_library(jobs, defines, variant_path(name), BUILD_DIR / "variants" / name)
+
+
+def build_probe() -> Path:
+    """Compile the benchmark's streaming-probe kernels into their own library,
+    beside their source (not in the package)."""
     hipcc = str(ROCM / "bin" / "hipcc")
-    temporary = CEILING.with_name(CEILING.name + ".tmp")
-    _run([hipcc, *HIP_FLAGS, "-shared", str(CSRC / "rln_ceiling.hip"),
-          f"-Wl,-soname,{CEILING.name}", "-Wl,-z,defs", "-o", str(temporary)])
-    os.replace(temporary, CEILING)
-    return CEILING
+    temporary = PROBE.with_name(PROBE.name + ".tmp")
+    _run([hipcc, *HIP_FLAGS, "-shared", str(PROBE_SOURCE), f"-Wl,-soname,{PROBE.name}",
+          "-Wl,-z,defs", "-o", str(temporary)])
+    os.replace(temporary, PROBE)
+    return PROBE
 
 
 def _torch_paths() -> tuple[list[str], Path, bool]:
@@ -179,7 +202,7 @@ def build() -> tuple[Path, Path]:
     PACKAGE.mkdir(parents=True, exist_ok=True)
     library = build_library()
     glue = build_glue()
-    build_ceiling()
+    build_probe()
     return library, glue
 
 

@@ -180,6 +180,29 @@ int check_common(int64_t rows, int64_t hidden, int branch_dtype) {
     return RLN_OK;
 }
 
+// A non-default stream must belong to the calling thread's current device:
+// the launch shapes (the forward's CU count) and rln_backward_noalloc's
+// scratch are those of the current device, and the pointers are on it.
+int check_stream(void* stream) {
+    if (stream == nullptr) {
+        return RLN_OK;
+    }
+    int current = -1;
+    hipDevice_t owner = -1;
+    const hipError_t got_current = hipGetDevice(&current);
+    const hipError_t got_owner = hipStreamGetDevice(static_cast<hipStream_t>(stream), &owner);
+    if (got_current != hipSuccess || got_owner != hipSuccess) {
+        static_cast<void>(hipGetLastError());  // clear the failed call's error
+        return fail(RLN_ERR_INVALID, "stream: cannot tell its device (%s)",
+                    hipGetErrorString(got_current != hipSuccess ? got_current : got_owner));
+    }
+    if (owner != current) {
+        return fail(RLN_ERR_INVALID,
+                    "stream belongs to device %d but the current device is %d", owner, current);
+    }
+    return RLN_OK;
+}
+
 // The dropout layout `threads` selects: 0 for this library's; 128, 192 or
 // 256 for the reference's stream of a launch with that many threads per row
 // (reference csrc/residual_layer_norm_kernel.hip:68-72 accepts the same three
@@ -240,6 +263,10 @@ int rln_forward(
     void* stream) {
     rln::t_last_error.clear();
     int status = check_common(rows, hidden, branch_dtype);
+    if (status != RLN_OK) {
+        return status;
+    }
+    status = check_stream(stream);
     if (status != RLN_OK) {
         return status;
     }
@@ -523,6 +550,9 @@ int rln_backward(
     if (status != RLN_OK) {
         return status;
     }
+    if (check_stream(stream) != RLN_OK) {
+        return RLN_ERR_INVALID;
+    }
     return backward_launches(grad_updated, grad_normalized, grad_normalized_dtype, updated, weight,
                              mean, rstd, dropout_mask, grad_x, grad_branch, branch_dtype,
                              grad_weight, grad_bias, rows, hidden, dropout_p, training,
@@ -557,6 +587,9 @@ int rln_backward_noalloc(
                                       grad_bias, dropout_mask, rows, hidden, dropout_p, training);
     if (status != RLN_OK) {
         return status;
+    }
+    if (check_stream(stream) != RLN_OK) {
+        return RLN_ERR_INVALID;
     }
     const bool parameters = grad_weight != nullptr && grad_normalized != nullptr;
     const size_t needed = parameters ? rln_backward_workspace_bytes(rows, hidden, deterministic) : 0;

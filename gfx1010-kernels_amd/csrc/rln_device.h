@@ -87,8 +87,31 @@
 #ifndef RLN_FWD_PERSISTENT_ELEMENTS_8
 #define RLN_FWD_PERSISTENT_ELEMENTS_8 (1ll << 27)
 #endif
+// Small forward launches of rows owned by one whole wave (768 and 1024
+// columns) run at most this many blocks per CU (forward_blocks).
+#ifndef RLN_FWD_WAVE_ROW_BLOCKS_PER_CU
+#define RLN_FWD_WAVE_ROW_BLOCKS_PER_CU 3
+#endif
 #ifndef RLN_BWD_MAX_BLOCKS
 #define RLN_BWD_MAX_BLOCKS 256
+#endif
+// 1: the look-ahead backward keeps two rows in flight for one-wave rows of up
+// to three slots (kTwoAhead); 0: one row, as every other shape.
+#ifndef RLN_BWD_TWO_AHEAD
+#define RLN_BWD_TWO_AHEAD 1
+#endif
+// 1: the look-ahead forward keeps two rows in flight for one-part rows of up
+// to three slots; 0: one row.
+#ifndef RLN_FWD_TWO_AHEAD
+#define RLN_FWD_TWO_AHEAD 0
+#endif
+// 1: the atomic-mode backward adds its last rows' weight/bias contributions
+// as soon as their loads arrive, combines the block's sums in LDS with LDS
+// atomics (no block barrier) and has the block's last wave issue the global
+// atomics, which then drain while the last rows' gradients are computed and
+// stored; 0: the fixed-order block combine after the last row.
+#ifndef RLN_BWD_EARLY_PARAMETERS
+#define RLN_BWD_EARLY_PARAMETERS 1
 #endif
 #ifndef RLN_BWD_THREADS
 #define RLN_BWD_THREADS 512
@@ -107,8 +130,26 @@
 #ifndef RLN_NT_LOADS
 #define RLN_NT_LOADS 1
 #endif
-#ifndef RLN_NT_STORES
-#define RLN_NT_STORES 1
+// Cache policy of the row outputs' stores (every output the kernels write per
+// row: updated, normalized, the mask, mean and rstd, grad_x, grad_branch),
+// as the cache-policy bits of a gfx950 buffer store: sc0 = 1, nt = 2,
+// sc1 = 16. The default, sc0 | sc1, writes through the caches at system
+// scope, so that no dirty line is left in L2 for the end-of-kernel release to
+// write back. Measured on MI355X with the streaming probe at C1 ([8192, 768],
+// benchmarks/rln_probe.hip, fastest grid per policy): forward-shaped pass
+// 15.2 us with sc0 | sc1 against 15.8 us plain and 18.8 us non-temporal;
+// backward-shaped 19.0 us against 19.5 us and 20.2 us; nt | sc1 and
+// sc0 | sc1 | nt are slower still (20.2-23 us).
+#ifndef RLN_STORE_POLICY
+#define RLN_STORE_POLICY 17
+#endif
+// The same for the dropout mask (a row's words are 32-byte pieces per slot)
+// and for the row statistics (mean, rstd: one word per row each).
+#ifndef RLN_MASK_STORE_POLICY
+#define RLN_MASK_STORE_POLICY RLN_STORE_POLICY
+#endif
+#ifndef RLN_STATS_STORE_POLICY
+#define RLN_STATS_STORE_POLICY RLN_STORE_POLICY
 #endif
 
 namespace rln {
@@ -470,8 +511,9 @@ int64_t forward_blocks(int64_t rows, int64_t hidden, int cus, int resident) {
     } else {
         blocks = launch_blocks(rows, info_of<S>(), S::kForwardThreads, kForwardMaxBlocks,
                                RLN_FWD_GROUPS_PER_WAVE);
-        if (cus > 0 && S::kHidden > 0 && S::kLanes == kWaveSize && blocks > 3 * cus) {
-            blocks = 3 * cus;
+        constexpr int64_t kPerCu = RLN_FWD_WAVE_ROW_BLOCKS_PER_CU;
+        if (cus > 0 && S::kHidden > 0 && S::kLanes == kWaveSize && blocks > kPerCu * cus) {
+            blocks = kPerCu * cus;
         }
         // No part-full second round: between one and two rounds of resident
         // blocks, one round.
@@ -595,9 +637,9 @@ struct PhiloxArgs {
 };
 
 // ----------------------------------------------------------------------------
-// Global memory access. Aligned = one 128-bit access (64-bit for 4 x fp16);
-// otherwise element accesses with the same values. Streaming accesses carry
-// the non-temporal hint.
+// Global memory loads. Aligned = one 128-bit access (64-bit for 4 x fp16);
+// otherwise element accesses with the same values. Row loads carry the
+// non-temporal hint (RLN_NT_LOADS); stores are the row outputs below.
 
 template <typename T>
 __device__ __forceinline__ T stream_load(const T* pointer) {
@@ -605,15 +647,6 @@ __device__ __forceinline__ T stream_load(const T* pointer) {
     return __builtin_nontemporal_load(pointer);
 #else
     return *pointer;
-#endif
-}
-
-template <typename T>
-__device__ __forceinline__ void stream_store(T value, T* pointer) {
-#if RLN_NT_STORES
-    __builtin_nontemporal_store(value, pointer);
-#else
-    *pointer = value;
 #endif
 }
 
@@ -627,19 +660,63 @@ __device__ __forceinline__ f32x4 load4(const float* __restrict__ pointer) {
     }
 }
 
+// ----------------------------------------------------------------------------
+// Row outputs. Every per-row output goes out through buffer stores with the
+// cache policy RLN_STORE_POLICY (a global store cannot carry its sc bits from
+// HIP source). A wave's stores of one row step go through one descriptor per
+// output over exactly the rows the wave writes in that step: its base and
+// extent are wave-uniform (scalar registers), every lane stores at a byte
+// offset into it, and the hardware's range check drops any store outside
+// the wave's rows.
+
+using rsrc_t = __amdgpu_buffer_rsrc_t;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// The descriptor's fourth word for a raw (untyped, unswizzled) buffer.
+constexpr int kRawBufferWord3 = 0x00020000;
+
+// `value` of the wave's first active lane, in scalar registers.
+__device__ __forceinline__ int64_t wave_uniform(int64_t value) {
+    const uint64_t bits = static_cast<uint64_t>(value);
+    const uint32_t low = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(bits));
+    const uint32_t high = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(bits >> 32));
+    return static_cast<int64_t>((static_cast<uint64_t>(high) << 32) | low);
+}
+
+// A descriptor over `count` elements of `tensor` from element `first`
+// (wave-uniform arguments; count * sizeof(T) < 2^31).
+template <typename T>
+__device__ __forceinline__ rsrc_t output_range(T* tensor, int64_t first, int64_t count) {
+    return __builtin_amdgcn_make_buffer_rsrc(
+        static_cast<void*>(tensor + first), 0,
+        static_cast<int>(count * static_cast<int64_t>(sizeof(T))), kRawBufferWord3);
+}
+
+template <int Policy = RLN_STORE_POLICY>
+__device__ __forceinline__ void output_b32(rsrc_t r, uint32_t offset, uint32_t value) {
+    __builtin_amdgcn_raw_buffer_store_b32(value, r, offset, 0, Policy);
+}
+
+// Four fp32 values at byte `offset`: one 128-bit store, or four element
+// stores with the same values when the tensor is not 16-byte aligned.
 template <bool Aligned>
-__device__ __forceinline__ void store4(float* __restrict__ pointer, f32x4 value) {
+__device__ __forceinline__ void output4(rsrc_t r, uint32_t offset, f32x4 value) {
     if constexpr (Aligned) {
-        stream_store(value, reinterpret_cast<f32x4*>(pointer));
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, value), r, offset, 0,
+                                               RLN_STORE_POLICY);
     } else {
-        stream_store(value.x, pointer);
-        stream_store(value.y, pointer + 1);
-        stream_store(value.z, pointer + 2);
-        stream_store(value.w, pointer + 3);
+        // Element by element through a scalar copy: clang's __builtin_bit_cast
+        // of a vector element expression (value.y) reads element 0.
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float element = value[e];
+            output_b32(r, offset + 4 * e, __builtin_bit_cast(uint32_t, element));
+        }
     }
 }
 
-// Parameters (weight, bias): ordinary cached loads, every wave reads them.
+// Parameters (weight, bias): ordinary cached loads, every wave reads them.// Parameters (weight, bias): ordinary cached loads, every wave reads them.
 template <bool Aligned>
 __device__ __forceinline__ f32x4 load_parameter4(const float* __restrict__ pointer) {
     if constexpr (Aligned) {
@@ -687,18 +764,26 @@ __device__ __forceinline__ f32x4 widen4(typename Vector4<T>::type raw) {
     return __builtin_convertvector(raw, f32x4);
 }
 
-// Stores four fp32 values as type T; narrowing rounds to nearest even.
+// Stores four fp32 values as type T at byte `offset` (the offset of the
+// first element); narrowing rounds to nearest even.
 template <typename T, bool Aligned>
-__device__ __forceinline__ void store_convert4(T* __restrict__ pointer, f32x4 value) {
-    const typename Vector4<T>::type packed =
-        __builtin_convertvector(value, typename Vector4<T>::type);
-    if constexpr (Aligned) {
-        stream_store(packed, reinterpret_cast<typename Vector4<T>::type*>(pointer));
+__device__ __forceinline__ void output_convert4(rsrc_t r, uint32_t offset, f32x4 value) {
+    if constexpr (std::is_same_v<T, float>) {
+        output4<Aligned>(r, offset, value);
     } else {
-        stream_store(static_cast<T>(packed.x), pointer);
-        stream_store(static_cast<T>(packed.y), pointer + 1);
-        stream_store(static_cast<T>(packed.z), pointer + 2);
-        stream_store(static_cast<T>(packed.w), pointer + 3);
+        const typename Vector4<T>::type packed =
+            __builtin_convertvector(value, typename Vector4<T>::type);
+        if constexpr (Aligned) {
+            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, packed), r, offset, 0,
+                                                  RLN_STORE_POLICY);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                __builtin_amdgcn_raw_buffer_store_b16(
+                    __builtin_bit_cast(uint16_t, static_cast<T>(packed[e])), r,
+                    offset + 2 * e, 0, RLN_STORE_POLICY);
+            }
+        }
     }
 }
 
@@ -771,6 +856,18 @@ __device__ __forceinline__ float team_sum(float value, float (*exchange)[S::kPar
     }
 }
 
+// Orders the LDS accesses of the wave's lanes before this point ahead of
+// those after it, as a memory handoff between lanes of one wave: the release
+// and acquire fences at wavefront scope stop the compiler from moving memory
+// accesses across (a bare wave barrier only constrains instruction
+// scheduling), and a wave's LDS operations complete in issue order, so no
+// instruction is needed for the hardware.
+__device__ __forceinline__ void wave_handoff() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // Keep bits of the reference's own dropout stream for one row of a fixed
 // shape (reference csrc/residual_layer_norm_kernel.hip:449-511). The
 // reference launches `threads` threads per row; thread t of row r seeds
@@ -788,9 +885,10 @@ __device__ __forceinline__ float team_sum(float value, float (*exchange)[S::kPar
 // wave). Each lane then reads the 4 bits of each of its slots and returns
 // them packed, slot v in bits 4v .. 4v + 3. `stage` is the row's H / 16
 // pieces, used by this wave only: LDS accesses of one wave complete in
-// order, so no block barrier is needed; two wave barriers (compiler
-// ordering fences) keep the cross-lane handoff from being reordered: the
-// writes after the previous row's reads, the reads after the writes.
+// order, so no block barrier is needed; two wave-level handoffs
+// (wave_handoff: wavefront-scope release and acquire fences around a wave
+// barrier) order the cross-lane exchange for the compiler: the writes after
+// the previous row's reads, the reads after the writes.
 // Requires offset % 4 == 0 and at most 8
 // items (the reference's two hiprand4 calls), checked on the host.
 template <typename S>
@@ -808,10 +906,8 @@ __device__ __forceinline__ uint32_t reference_keep_bits(
     // the row), so their draws are skipped.
     const int k_end = per_item < kChunks ? per_item : kChunks;
     // The previous row's reads of `stage` (other lanes of this wave) come
-    // before this row's writes: a wave barrier keeps the compiler from
-    // moving LDS accesses across it, and one wave's LDS operations complete
-    // in issue order.
-    __builtin_amdgcn_wave_barrier();
+    // before this row's writes.
+    wave_handoff();
     for (int k = 0; k < k_end; ++k) {
         const uint64_t subsequence = static_cast<uint64_t>(row) * threads + k * L + lane;
         for (int n = 0; n < calls; ++n) {
@@ -837,7 +933,7 @@ __device__ __forceinline__ uint32_t reference_keep_bits(
         }
     }
     // The staging writes of lanes < L / 16 come before every lane's reads.
-    __builtin_amdgcn_wave_barrier();
+    wave_handoff();
     uint32_t keep = 0;
 #pragma unroll
     for (int v = 0; v < S::kV; ++v) {
@@ -1007,7 +1103,18 @@ void rln_forward_kernel(
 
     auto process_row = [&](const ForwardRow<V, B>& r, int64_t row, uint32_t reference_bits) {
         const bool valid = row < rows;
-        const int64_t base = row * hidden;
+        // The wave's rows of this step (consecutive; wave-uniform first row
+        // and count) and this lane's row among them; the outputs' stores go
+        // through descriptors over exactly those rows.
+        const int64_t wave_row = wave_uniform(row - (S::kParts == 1 ? team.offset : 0));
+        const int64_t left = rows - wave_row;
+        const int64_t wave_rows =
+            left <= 0 ? 0 : left < S::kRowsPerWave ? left : S::kRowsPerWave;
+        const uint32_t row_in_wave = static_cast<uint32_t>(row - wave_row);
+        const uint32_t element = row_in_wave * static_cast<uint32_t>(hidden);
+        const rsrc_t updated_out = output_range(updated, wave_row * hidden, wave_rows * hidden);
+        const rsrc_t normalized_out =
+            output_range(normalized, wave_row * hidden, wave_rows * hidden);
         f32x4 u[V];
         uint32_t keep_bits[V];
 #pragma unroll
@@ -1047,7 +1154,7 @@ void rln_forward_kernel(
             }
             u[v] = r.x[v] + bv;
             if (valid && slots.active(v)) {
-                store4<Aligned>(updated + base + slots.column(v), u[v]);
+                output4<Aligned>(updated_out, (element + slots.column(v)) * 4, u[v]);
             }
             if (!slots.active(v)) {
                 u[v] = zero4();
@@ -1055,13 +1162,18 @@ void rln_forward_kernel(
         }
 
         if (dropout) {
+            const int64_t words = hidden / 32;
+            const rsrc_t mask_out = output_range(mask, wave_row * words, wave_rows * words);
 #pragma unroll
             for (int v = 0; v < V; ++v) {
                 // A word's 32 columns belong to 8 lanes of one slot, all
                 // active or all idle (hidden is a multiple of 32).
                 const uint32_t word = or8(keep_bits[v] << (4 * (l & 7)));
                 if (valid && slots.active(v) && (l & 7) == 0) {
-                    stream_store(word, mask + row * (hidden / 32) + slots.vector(v) / 8);
+                    output_b32<RLN_MASK_STORE_POLICY>(mask_out,
+                               (row_in_wave * static_cast<uint32_t>(words) + slots.vector(v) / 8)
+                                   * 4,
+                               word);
                 }
             }
         }
@@ -1086,8 +1198,12 @@ void rln_forward_kernel(
 
         if (valid) {
             if (l == 0 && team.part == 0) {
-                mean_out[row] = mean;
-                rstd_out[row] = rstd;
+                output_b32<RLN_STATS_STORE_POLICY>(output_range(mean_out, wave_row, wave_rows),
+                                                   row_in_wave * 4,
+                                                   __builtin_bit_cast(uint32_t, mean));
+                output_b32<RLN_STATS_STORE_POLICY>(output_range(rstd_out, wave_row, wave_rows),
+                                                   row_in_wave * 4,
+                                                   __builtin_bit_cast(uint32_t, rstd));
             }
 #pragma unroll
             for (int v = 0; v < V; ++v) {
@@ -1097,7 +1213,8 @@ void rln_forward_kernel(
                     __builtin_fmaf(u[v].z * rstd, w[v].z, b[v].z),
                     __builtin_fmaf(u[v].w * rstd, w[v].w, b[v].w)};
                 if (slots.active(v)) {
-                    store_convert4<N, Aligned>(normalized + base + slots.column(v), y);
+                    output_convert4<N, Aligned>(normalized_out,
+                                                (element + slots.column(v)) * sizeof(N), y);
                 }
             }
         }
@@ -1125,6 +1242,25 @@ void rln_forward_kernel(
             process_row(current, first + team.offset, keep);
             keep = reference_keep(first + stride + team.offset);
             load_row(current, first + stride + team.offset, true);
+        }
+    } else if constexpr (RLN_FWD_TWO_AHEAD && S::kParts == 1 && V <= 3) {
+        ForwardRow<V, B> second;
+        if (first + stride < rows) {
+            load_row(second, first + stride + team.offset, false);
+        }
+        for (; first + 2 * stride < rows; first += stride) {
+            ForwardRow<V, B> third;
+            load_row(third, first + 2 * stride + team.offset, false);
+            process_row(current, first + team.offset, keep);
+            keep = reference_keep(first + stride + team.offset);
+            current = second;
+            second = third;
+        }
+        if (first + stride < rows) {
+            process_row(current, first + team.offset, keep);
+            keep = reference_keep(first + stride + team.offset);
+            current = second;
+            first += stride;
         }
     } else {
         for (; first + stride < rows; first += stride) {
@@ -1185,7 +1321,7 @@ void rln_backward_kernel(
     constexpr int P = S::kParts;
     using T = Teams<S, S::kBackwardBlockThreads>;
     constexpr int kWaves = T::kWaves;
-    constexpr bool kTwoAhead = P == 1 && V <= 3;
+    constexpr bool kTwoAhead = RLN_BWD_TWO_AHEAD && P == 1 && V <= 3;
     const int64_t hidden = shape.hidden();
     const float inv_hidden = shape.inv_hidden();
     const int lane = threadIdx.x & (kWaveSize - 1);
@@ -1248,8 +1384,9 @@ void rln_backward_kernel(
         }
     };
 
-    // Input gradients of one row and its contribution to the parameter sums.
-    auto process_row = [&](const BackwardRow<V, GY>& r, int64_t row) {
+    // Input gradients of one row and, with `accumulate`, its contribution to
+    // the parameter sums.
+    auto process_row = [&](const BackwardRow<V, GY>& r, int64_t row, bool accumulate) {
         f32x4 w[V];
 #pragma unroll
         for (int v = 0; v < V; ++v) {
@@ -1260,7 +1397,18 @@ void rln_backward_kernel(
             }
         }
         const bool valid = row < rows;
-        const int64_t base = row * hidden;
+        // The wave's rows of this step and this lane's row among them (as in
+        // the forward); the input gradients go out through descriptors over
+        // exactly those rows.
+        const int64_t wave_row = wave_uniform(row - (P == 1 ? team.offset : 0));
+        const int64_t left = rows - wave_row;
+        const int64_t wave_rows =
+            left <= 0 ? 0 : left < S::kRowsPerWave ? left : S::kRowsPerWave;
+        const uint32_t element =
+            static_cast<uint32_t>(row - wave_row) * static_cast<uint32_t>(hidden);
+        const rsrc_t grad_x_out = output_range(grad_x, wave_row * hidden, wave_rows * hidden);
+        const rsrc_t grad_branch_out =
+            output_range(grad_branch, wave_row * hidden, wave_rows * hidden);
         f32x4 xhat[V];
         f32x4 gy[V];
         float sum_q = 0.0f;
@@ -1298,7 +1446,7 @@ void rln_backward_kernel(
                     const f32x4 q = gy[v] * w[v];
                     g = g + r.rstd * ((q - mean_q) - xhat[v] * mean_qx);
                 }
-                store4<Aligned>(grad_x + base + column, g);
+                output4<Aligned>(grad_x_out, (element + column) * 4, g);
                 if (dropout) {
                     const uint32_t bits = r.mask_word[v] >> (4 * (l & 7));
                     g.x = g.x * (static_cast<float>(bits & 1u) * scale);
@@ -1306,11 +1454,11 @@ void rln_backward_kernel(
                     g.z = g.z * (static_cast<float>((bits >> 2) & 1u) * scale);
                     g.w = g.w * (static_cast<float>((bits >> 3) & 1u) * scale);
                 }
-                store_convert4<B, Aligned>(grad_branch + base + column, g);
+                output_convert4<B, Aligned>(grad_branch_out, (element + column) * sizeof(B), g);
             }
         }
 
-        if (parameters) {
+        if (parameters && accumulate) {
 #pragma unroll
             for (int v = 0; v < V; ++v) {
                 acc_w[v].x = __builtin_fmaf(gy[v].x, xhat[v].x, acc_w[v].x);
@@ -1318,6 +1466,77 @@ void rln_backward_kernel(
                 acc_w[v].z = __builtin_fmaf(gy[v].z, xhat[v].z, acc_w[v].z);
                 acc_w[v].w = __builtin_fmaf(gy[v].w, xhat[v].w, acc_w[v].w);
                 acc_b[v] = acc_b[v] + gy[v];
+            }
+        }
+    };
+
+    // A row's contribution to the parameter sums alone, with the arithmetic
+    // process_row uses (the lane's sums come out bitwise the same).
+    auto accumulate_row = [&](const BackwardRow<V, GY>& r, int64_t row) {
+        if (!(has_gy && row < rows)) {
+            return;
+        }
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+            if (!slots.active(v)) {
+                continue;
+            }
+            const f32x4 gy = widen4<GY>(r.gy[v]);
+            const f32x4 xhat = (r.u[v] - r.mean) * r.rstd;
+            acc_w[v].x = __builtin_fmaf(gy.x, xhat.x, acc_w[v].x);
+            acc_w[v].y = __builtin_fmaf(gy.y, xhat.y, acc_w[v].y);
+            acc_w[v].z = __builtin_fmaf(gy.z, xhat.z, acc_w[v].z);
+            acc_w[v].w = __builtin_fmaf(gy.w, xhat.w, acc_w[v].w);
+            acc_b[v] = acc_b[v] + gy;
+        }
+    };
+
+    // The block's parameter sums: staged per wave for the fixed-order combine,
+    // or (early mode) added up in LDS as [2, hidden] floats in the same space.
+    __shared__ f32x4 staging[V][kWaves][kWaveSize][2];
+    __shared__ int arrivals;
+    static_assert(sizeof(staging) >= 2 * sizeof(float) * V * P * L * 4, "LDS sums fit");
+    float* const block_sums = reinterpret_cast<float*>(&staging[0][0][0][0]);
+    const bool early = RLN_BWD_EARLY_PARAMETERS && parameters && !(flags & kPartials);
+    if (early) {
+        for (int i = threadIdx.x; i < 2 * hidden; i += S::kBackwardBlockThreads) {
+            block_sums[i] = 0.0f;
+        }
+        if (threadIdx.x == 0) {
+            arrivals = 0;
+        }
+        __syncthreads();
+    }
+
+    // Early mode: adds this wave's sums into the block's LDS sums (LDS
+    // atomics), then counts the wave in; the block's last wave to arrive
+    // adds the block's sums into grad_weight / grad_bias with fp32 atomics.
+    // Every wave of the block calls it once, rows or not.
+    auto deposit_parameters = [&]() {
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+            if (!slots.active(v)) {
+                continue;
+            }
+            const int column = slots.column(v);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                atomicAdd(block_sums + column + e, acc_w[v][e]);
+                atomicAdd(block_sums + hidden + column + e, acc_b[v][e]);
+            }
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        int arrived = 0;
+        if (lane == 0) {
+            arrived = atomicAdd(&arrivals, 1);
+        }
+        arrived = __builtin_amdgcn_readfirstlane(arrived);
+        if (arrived == kWaves - 1) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+            for (int i = lane; i < 2 * hidden; i += kWaveSize) {
+                const bool bias_sum = i >= hidden;
+                unsafeAtomicAdd((bias_sum ? grad_bias : grad_weight) + (i - (bias_sum ? hidden : 0)),
+                                block_sums[i]);
             }
         }
     };
@@ -1333,14 +1552,20 @@ void rln_backward_kernel(
     // rows. `first` is uniform over a team, so a multi-wave team meets its
     // barriers together; a team without rows still takes part in the block's
     // combine below.
+    // In early mode the rows still held when a team's walk ends (its last
+    // row, or last two with two rows ahead) add their contributions first,
+    // the wave deposits its sums, and only then are those rows' gradients
+    // computed and stored, so that the block's global atomics drain under
+    // that work instead of after it.
     const int64_t stride = team.stride;
     int64_t first = team.first;
     if (first < rows) {
         BackwardRow<V, GY> current;
+        bool deposited = false;
         load_row(current, first + team.offset, false);
         if (paced) {
             for (; first + stride < rows; first += stride) {
-                process_row(current, first + team.offset);
+                process_row(current, first + team.offset, true);
                 load_row(current, first + stride + team.offset, true);
             }
         } else if constexpr (kTwoAhead) {
@@ -1351,12 +1576,18 @@ void rln_backward_kernel(
             for (; first + 2 * stride < rows; first += stride) {
                 BackwardRow<V, GY> third;
                 load_row(third, first + 2 * stride + team.offset, false);
-                process_row(current, first + team.offset);
+                process_row(current, first + team.offset, true);
                 current = second;
                 second = third;
             }
             if (first + stride < rows) {
-                process_row(current, first + team.offset);
+                if (early) {
+                    accumulate_row(current, first + team.offset);
+                    accumulate_row(second, first + stride + team.offset);
+                    deposit_parameters();
+                    deposited = true;
+                }
+                process_row(current, first + team.offset, !early);
                 current = second;
                 first += stride;
             }
@@ -1364,14 +1595,20 @@ void rln_backward_kernel(
             for (; first + stride < rows; first += stride) {
                 BackwardRow<V, GY> next;
                 load_row(next, first + stride + team.offset, false);
-                process_row(current, first + team.offset);
+                process_row(current, first + team.offset, true);
                 current = next;
             }
         }
-        process_row(current, first + team.offset);
+        if (early && !deposited) {
+            accumulate_row(current, first + team.offset);
+            deposit_parameters();
+        }
+        process_row(current, first + team.offset, !early);
+    } else if (early) {
+        deposit_parameters();
     }
 
-    if (!parameters) {
+    if (!parameters || early) {
         return;
     }
 
@@ -1379,7 +1616,6 @@ void rln_backward_kernel(
     // (part, lane) pair; for each, the block adds groups 0..kGroups-1 and,
     // within a wave, row slots 0..kRowsPerWave-1. All slots are staged at
     // once (16 KiB of LDS per slot), so one barrier serves the whole combine.
-    __shared__ f32x4 staging[V][kWaves][kWaveSize][2];
     const bool write_partials = flags & kPartials;
 #pragma unroll
     for (int v = 0; v < V; ++v) {

@@ -78,19 +78,23 @@ SIGNATURES = {
 }
 
 
-@lru_cache(maxsize=1)
-def library() -> ctypes.CDLL:
-    """Load librln_gfx950.so and declare every C ABI signature."""
-    if not LIBRARY_PATH.exists():
-        raise OSError(
-            f"{LIBRARY_PATH} is missing; build it with gfx1010-kernels_amd/build.py"
-        )
-    handle = ctypes.CDLL(str(LIBRARY_PATH))
+def load(path: Path) -> ctypes.CDLL:
+    """Load a build of the C ABI at `path` and declare every signature (the
+    benchmark's A/B runs load variant builds of the library this way)."""
+    if not Path(path).exists():
+        raise OSError(f"{path} is missing; build it with gfx1010-kernels_amd/build.py")
+    handle = ctypes.CDLL(str(path))
     for name, (restype, argtypes) in SIGNATURES.items():
         function = getattr(handle, name)
         function.restype = restype
         function.argtypes = argtypes
     return handle
+
+
+@lru_cache(maxsize=1)
+def library() -> ctypes.CDLL:
+    """Load librln_gfx950.so and declare every C ABI signature."""
+    return load(LIBRARY_PATH)
 
 
 def last_error() -> str:

@@ -23,8 +23,10 @@
  *  - The dropout mask is `rows * hidden / 32` uint32 words: keep(r, c) is
  *    bit (c % 32) of word r * hidden / 32 + c / 32 - the reference's layout
  *    (csrc/residual_layer_norm_kernel.hip:500-511, :162-164).
- *  - `stream` is a hipStream_t (NULL = the legacy default stream). Work is
- *    enqueued asynchronously; nothing synchronizes the host.
+ *  - `stream` is a hipStream_t (NULL = the legacy default stream) of the
+ *    current device; a stream of another device is rejected with
+ *    RLN_ERR_INVALID. Work is enqueued asynchronously; nothing synchronizes
+ *    the host.
  *  - No entry point allocates device memory; rln_backward_noalloc also takes
  *    no workspace (it keeps a static per-device scratch instead).
  *  - Return value: RLN_OK, or an RLN_ERR_* code with a message available

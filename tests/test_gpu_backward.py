@@ -209,6 +209,39 @@ def test_atomic_mode_is_close_to_deterministic_mode():
     assert np.isfinite(host(fixed[2])).all()
 
 
+# Row counts around the team walks' edges, per row shape: teams without rows,
+# with one, two and three rows (the two-rows-ahead walk ends on one or two
+# held rows), paced launches, two and four rows per wave, multi-wave rows.
+EARLY_COMBINE_SHAPES = [(1, 768), (5, 768), (2048, 768), (4096, 768), (6144, 768),
+                        (16384, 768), (3, 128), (1000, 256), (300, 1024), (77, 2048),
+                        (33, 5952), (5000, 512)]
+
+
+@pytest.mark.parametrize("rows,hidden", EARLY_COMBINE_SHAPES,
+                         ids=[f"{r}x{h}" for r, h in EARLY_COMBINE_SHAPES])
+def test_atomic_weight_bias_sums_match_the_fixed_order_sums(rows, hidden):
+    """The atomic backward adds each block's sums in LDS and its last wave adds
+    them into grad_weight / grad_bias, starting with the last rows'
+    contributions before those rows' gradients are stored: the input
+    gradients equal the deterministic backward's bit for bit, the weight/bias
+    sums are within 1e-5 of its fixed-order sums (relative to their largest
+    value), for row counts at every edge of the team walks."""
+    print(f"[backward] atomic vs fixed-order sums {rows}x{hidden}", flush=True)
+    inputs = make_inputs((rows, hidden), torch.float16, seed=rows + hidden)
+    grad_updated, grad_normalized = make_grads((rows, hidden), seed=7 + rows)
+    torch.cuda.manual_seed(3)
+    outputs = _C.residual_layer_norm_forward(*inputs, 0.1, 1e-5, True, 128)
+    with deterministic_algorithms(False):
+        atomic = raw_backward(grad_updated, grad_normalized, outputs, inputs[2], 0.1, True)
+    with deterministic_algorithms(True):
+        fixed = raw_backward(grad_updated, grad_normalized, outputs, inputs[2], 0.1, True)
+    assert_bitwise(host(atomic[0]), host(fixed[0]), "grad_x")
+    assert_bitwise(host(atomic[1]), host(fixed[1]), "grad_branch")
+    for a, b, name in zip(atomic[2:], fixed[2:], ("grad_weight", "grad_bias")):
+        scale = float(b.abs().max())
+        assert float((a - b).abs().max()) <= 1e-5 * scale, name
+
+
 @pytest.mark.parametrize("deterministic", [False, True], ids=["atomic", "deterministic"])
 def test_repeated_backward_of_one_forward(deterministic):
     """The first backward of a call accumulates into sums its forward zeroed;
