@@ -96,22 +96,36 @@
 #define RLN_BWD_MAX_BLOCKS 256
 #endif
 // 1: the look-ahead backward keeps two rows in flight for one-wave rows of up
-// to three slots (kTwoAhead); 0: one row, as every other shape.
+// to three slots (kTwoAhead); 0 (default): one row, as every other shape.
+// Measured on MI355X at C1 (bench.py --ab, alternated, register rings):
+// backward 22.4 us with one row ahead against 22.9 us with two (input
+// gradients alone 19.0 against 20.2 us).
 #ifndef RLN_BWD_TWO_AHEAD
-#define RLN_BWD_TWO_AHEAD 1
+#define RLN_BWD_TWO_AHEAD 0
 #endif
-// 1: the look-ahead forward keeps two rows in flight for one-part rows of up
-// to three slots; 0: one row.
+// 1 (default): the look-ahead backward walks its rows in a ring of register
+// buffers; 0: one-ahead walks that copy the next row between registers (the
+// copy waits for that row's loads, and with them every older access, before
+// the following row's loads issue).
+#ifndef RLN_BWD_RING
+#define RLN_BWD_RING 1
+#endif
+// 1 (default): the look-ahead forward keeps two rows in flight for one-part
+// rows of up to three slots; 0: one row. Measured on MI355X at C1 (bench.py
+// --ab, alternated, register rings): forward 15.0 us against 17.1 us.
 #ifndef RLN_FWD_TWO_AHEAD
-#define RLN_FWD_TWO_AHEAD 0
+#define RLN_FWD_TWO_AHEAD 1
 #endif
 // 1: the atomic-mode backward adds its last rows' weight/bias contributions
 // as soon as their loads arrive, combines the block's sums in LDS with LDS
 // atomics (no block barrier) and has the block's last wave issue the global
-// atomics, which then drain while the last rows' gradients are computed and
-// stored; 0: the fixed-order block combine after the last row.
+// atomics, to drain while the last rows' gradients are computed and stored;
+// 0 (default): the fixed-order block combine after the last row. Measured on
+// MI355X at C1 (bench.py --ab, alternated): backward 34.4 us early against
+// 22.9 us after the last row - global atomics issued while the other blocks
+// still stream stall the memory channels that hold the sums' lines.
 #ifndef RLN_BWD_EARLY_PARAMETERS
-#define RLN_BWD_EARLY_PARAMETERS 1
+#define RLN_BWD_EARLY_PARAMETERS 0
 #endif
 #ifndef RLN_BWD_THREADS
 #define RLN_BWD_THREADS 512
@@ -126,6 +140,9 @@
 #endif
 #ifndef RLN_PACED_MIN_HIDDEN
 #define RLN_PACED_MIN_HIDDEN 256
+#endif
+#ifndef RLN_REFERENCE_DRAWS_UNROLLED
+#define RLN_REFERENCE_DRAWS_UNROLLED 1
 #endif
 #ifndef RLN_NT_LOADS
 #define RLN_NT_LOADS 1
@@ -891,22 +908,86 @@ __device__ __forceinline__ void wave_handoff() {
 // the previous row's reads, the reads after the writes.
 // Requires offset % 4 == 0 and at most 8
 // items (the reference's two hiprand4 calls), checked on the host.
-template <typename S>
-__device__ __forceinline__ uint32_t reference_keep_bits(
-    uint16_t* stage, int64_t row, int lane, int group, int threads, uint64_t position,
-    uint32_t key0, uint32_t key1, uint32_t threshold) {
+template <typename S, int Threads>
+__device__ __forceinline__ uint32_t reference_keep_bits_of(
+    uint16_t* stage, int64_t row, int lane, int group, uint64_t position, uint32_t key0,
+    uint32_t key1, uint32_t threshold) {
     constexpr int L = S::kLanes;
     constexpr int kChunks = S::kHidden / L;
     static_assert(S::kParts == 1 && S::kHidden > 0 && L % 16 == 0 && S::kV <= 8,
                   "fixed one-part rows of at most 8 slots");
+    static_assert(Threads % L == 0, "stand-in lanes divide the threads");
+    constexpr int kPerItem = Threads / L;
+    constexpr int kItems = (S::kHidden + Threads - 1) / Threads;
+    constexpr int kCalls = (kItems + 3) / 4;
+    static_assert(kItems <= 8, "at most the reference's two hiprand4 calls");
+    // Threads k * L + l with k >= H / L own no column (item 0 is already past
+    // the row), so their draws are skipped.
+    constexpr int kEnd = kPerItem < kChunks ? kPerItem : kChunks;
+    // Every Philox block of the row first - independent chains of quarter-rate
+    // multiplies the compiler interleaves - then the ballots.
+    uint4 random[kEnd][kCalls];
+#pragma unroll
+    for (int k = 0; k < kEnd; ++k) {
+        const uint64_t subsequence = static_cast<uint64_t>(row) * Threads + k * L + lane;
+#pragma unroll
+        for (int n = 0; n < kCalls; ++n) {
+            const uint64_t low = position + n;
+            const uint64_t high = subsequence + (low < position ? 1 : 0);
+            random[k][n] = philox4x32_10(
+                make_uint4(static_cast<uint32_t>(low), static_cast<uint32_t>(low >> 32),
+                           static_cast<uint32_t>(high), static_cast<uint32_t>(high >> 32)),
+                key0, key1);
+        }
+    }
+    // The previous row's reads of `stage` (other lanes of this wave) come
+    // before this row's writes.
+    wave_handoff();
+#pragma unroll
+    for (int k = 0; k < kEnd; ++k) {
+#pragma unroll
+        for (int n = 0; n < kCalls; ++n) {
+            const uint32_t draws[4] = {random[k][n].x, random[k][n].y, random[k][n].z,
+                                       random[k][n].w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                constexpr int kUnused = -1;
+                const int item = 4 * n + e;
+                const int chunk = item < kItems ? item * kPerItem + k : kUnused;
+                if (chunk != kUnused && chunk < kChunks) {
+                    const uint64_t ballot = __ballot(draws[e] >= threshold);
+                    if (lane < L / 16) {
+                        stage[chunk * (L / 16) + lane] =
+                            static_cast<uint16_t>(ballot >> (group * L + 16 * lane));
+                    }
+                }
+            }
+        }
+    }
+    // The staging writes of lanes < L / 16 come before every lane's reads.
+    wave_handoff();
+    uint32_t keep = 0;
+#pragma unroll
+    for (int v = 0; v < S::kV; ++v) {
+        const int vector = v * L + lane;
+        keep |= ((static_cast<uint32_t>(stage[vector / 4]) >> (4 * (vector % 4))) & 0xFu)
+            << (4 * v);
+    }
+    return keep;
+}
+
+// The same draws with run-time loop bounds (one Philox chain after another,
+// each followed by its ballots): RLN_REFERENCE_DRAWS_UNROLLED=0.
+template <typename S>
+__device__ __forceinline__ uint32_t reference_keep_bits_looped(
+    uint16_t* stage, int64_t row, int lane, int group, int threads, uint64_t position,
+    uint32_t key0, uint32_t key1, uint32_t threshold) {
+    constexpr int L = S::kLanes;
+    constexpr int kChunks = S::kHidden / L;
     const int per_item = threads / L;
     const int items = (S::kHidden + threads - 1) / threads;
     const int calls = (items + 3) / 4;
-    // Threads k * L + l with k >= H / L own no column (item 0 is already past
-    // the row), so their draws are skipped.
     const int k_end = per_item < kChunks ? per_item : kChunks;
-    // The previous row's reads of `stage` (other lanes of this wave) come
-    // before this row's writes.
     wave_handoff();
     for (int k = 0; k < k_end; ++k) {
         const uint64_t subsequence = static_cast<uint64_t>(row) * threads + k * L + lane;
@@ -932,7 +1013,6 @@ __device__ __forceinline__ uint32_t reference_keep_bits(
             }
         }
     }
-    // The staging writes of lanes < L / 16 come before every lane's reads.
     wave_handoff();
     uint32_t keep = 0;
 #pragma unroll
@@ -942,6 +1022,31 @@ __device__ __forceinline__ uint32_t reference_keep_bits(
             << (4 * v);
     }
     return keep;
+}
+
+// The reference stream's keep bits for a launch of `threads` (128, 192 or
+// 256) threads per row: one unrolled instance per width, chosen by a
+// wave-uniform switch (RLN_REFERENCE_DRAWS_UNROLLED, default 1), or the
+// looped draws.
+template <typename S>
+__device__ __forceinline__ uint32_t reference_keep_bits(
+    uint16_t* stage, int64_t row, int lane, int group, int threads, uint64_t position,
+    uint32_t key0, uint32_t key1, uint32_t threshold) {
+    if constexpr (!RLN_REFERENCE_DRAWS_UNROLLED) {
+        return reference_keep_bits_looped<S>(stage, row, lane, group, threads, position, key0,
+                                             key1, threshold);
+    }
+    switch (threads) {
+        case 128:
+            return reference_keep_bits_of<S, 128>(stage, row, lane, group, position, key0, key1,
+                                                   threshold);
+        case 192:
+            return reference_keep_bits_of<S, 192>(stage, row, lane, group, position, key0, key1,
+                                                   threshold);
+        default:
+            return reference_keep_bits_of<S, 256>(stage, row, lane, group, position, key0, key1,
+                                                   threshold);
+    }
 }
 
 // Rows are walked by teams: a wave (one or two rows at a time) when a row
@@ -980,7 +1085,14 @@ struct Teams {
     }
 };
 
-template <typename S, typename B, typename N, bool Aligned>
+// `Ring`: the kernel instance walks its rows with look-ahead in a ring of
+// register buffers (two rows ahead for one-part rows of up to three slots):
+// launches whose teams walk several rows. The other instance - paced walks
+// and one-ahead walks that copy rows between registers - serves the large
+// launches whose teams take one or two row steps, where the ring's registers
+// would only lower occupancy (measured: [262144, 128] forward 117 us with
+// the ring's 171+ VGPRs against 80 us).
+template <typename S, typename B, typename N, bool Aligned, bool Ring>
 __global__ __launch_bounds__(S::kForwardThreads)
 void rln_forward_kernel(
     const float* __restrict__ x,
@@ -1220,58 +1332,99 @@ void rln_forward_kernel(
         }
     };
 
-    // Two schedules. Look-ahead (small launches): the next row's loads are
-    // in flight while the current row is computed and stored. Paced (large
-    // launches): a row is loaded after the previous one is stored, one
-    // 4-column slice at a time, each waited for (with every earlier store of
-    // the wave), which keeps fewer reads and writes interleaved per wave and
-    // streams large tensors faster. The last row of a team is peeled off, so
-    // no load reaches past the team's rows. `first` is uniform over a team,
-    // so a multi-wave team meets its barriers together.
+    // Two schedules. Look-ahead (small launches): the next row's loads (the
+    // next two rows' for one-part rows of up to three slots) are in flight
+    // while the current row is computed and stored. Paced (large launches):
+    // a row is loaded after the previous one is stored, one 4-column slice
+    // at a time, each waited for (with every earlier store of the wave),
+    // which keeps fewer reads and writes interleaved per wave and streams
+    // large tensors faster. The team's rows are first + i * stride, i <
+    // count (uniform over a team, so a multi-wave team meets its barriers
+    // together); no load reaches past them. The look-ahead walks keep their
+    // rows in a ring of two or three register buffers whose roles rotate by
+    // unrolling: a row copied between registers would wait for its loads,
+    // and with them for every older access, before the next loads issue.
     const int64_t stride = team.stride;
-    int64_t first = team.first;
+    const int64_t first = team.first;
     if (first >= rows) {
         return;
     }
-    ForwardRow<V, B> current;
-    load_row(current, first + team.offset, false);
+    const int64_t count = (rows - first + stride - 1) / stride;
+    auto row_of = [&](int64_t i) { return first + i * stride + team.offset; };
+    ForwardRow<V, B> ra;
+    load_row(ra, row_of(0), false);
     read_philox_state();
-    uint32_t keep = reference_keep(first + team.offset);
-    if (paced) {
-        for (; first + stride < rows; first += stride) {
-            process_row(current, first + team.offset, keep);
-            keep = reference_keep(first + stride + team.offset);
-            load_row(current, first + stride + team.offset, true);
+    uint32_t keep_a = reference_keep(row_of(0));
+    if constexpr (!Ring) {
+        if (paced) {
+            for (int64_t i = 0; i + 1 < count; ++i) {
+                process_row(ra, row_of(i), keep_a);
+                keep_a = reference_keep(row_of(i + 1));
+                load_row(ra, row_of(i + 1), true);
+            }
+        } else {
+            for (int64_t i = 0; i + 1 < count; ++i) {
+                ForwardRow<V, B> next;
+                load_row(next, row_of(i + 1), false);
+                process_row(ra, row_of(i), keep_a);
+                keep_a = reference_keep(row_of(i + 1));
+                ra = next;
+            }
         }
+        process_row(ra, row_of(count - 1), keep_a);
     } else if constexpr (RLN_FWD_TWO_AHEAD && S::kParts == 1 && V <= 3) {
-        ForwardRow<V, B> second;
-        if (first + stride < rows) {
-            load_row(second, first + stride + team.offset, false);
+        ForwardRow<V, B> rb;
+        ForwardRow<V, B> rc;
+        uint32_t keep_b = 0;
+        uint32_t keep_c = 0;
+        if (count > 1) {
+            load_row(rb, row_of(1), false);
         }
-        for (; first + 2 * stride < rows; first += stride) {
-            ForwardRow<V, B> third;
-            load_row(third, first + 2 * stride + team.offset, false);
-            process_row(current, first + team.offset, keep);
-            keep = reference_keep(first + stride + team.offset);
-            current = second;
-            second = third;
+        int64_t i = 0;
+        for (; i + 3 <= count; i += 3) {
+            load_row(rc, row_of(i + 2), false);
+            process_row(ra, row_of(i), keep_a);
+            keep_b = reference_keep(row_of(i + 1));
+            if (i + 3 < count) {
+                load_row(ra, row_of(i + 3), false);
+            }
+            process_row(rb, row_of(i + 1), keep_b);
+            keep_c = reference_keep(row_of(i + 2));
+            if (i + 4 < count) {
+                load_row(rb, row_of(i + 4), false);
+            }
+            process_row(rc, row_of(i + 2), keep_c);
+            if (i + 3 < count) {
+                keep_a = reference_keep(row_of(i + 3));
+            }
         }
-        if (first + stride < rows) {
-            process_row(current, first + team.offset, keep);
-            keep = reference_keep(first + stride + team.offset);
-            current = second;
-            first += stride;
+        if (i < count) {
+            process_row(ra, row_of(i), keep_a);
+            if (i + 1 < count) {
+                keep_b = reference_keep(row_of(i + 1));
+                process_row(rb, row_of(i + 1), keep_b);
+            }
         }
     } else {
-        for (; first + stride < rows; first += stride) {
-            ForwardRow<V, B> next;
-            load_row(next, first + stride + team.offset, false);
-            process_row(current, first + team.offset, keep);
-            keep = reference_keep(first + stride + team.offset);
-            current = next;
+        ForwardRow<V, B> rb;
+        uint32_t keep_b = 0;
+        int64_t i = 0;
+        for (; i + 2 <= count; i += 2) {
+            load_row(rb, row_of(i + 1), false);
+            process_row(ra, row_of(i), keep_a);
+            keep_b = reference_keep(row_of(i + 1));
+            if (i + 2 < count) {
+                load_row(ra, row_of(i + 2), false);
+            }
+            process_row(rb, row_of(i + 1), keep_b);
+            if (i + 2 < count) {
+                keep_a = reference_keep(row_of(i + 2));
+            }
+        }
+        if (i < count) {
+            process_row(ra, row_of(i), keep_a);
         }
     }
-    process_row(current, first + team.offset, keep);
 }
 
 // ----------------------------------------------------------------------------
@@ -1552,58 +1705,95 @@ void rln_backward_kernel(
     // rows. `first` is uniform over a team, so a multi-wave team meets its
     // barriers together; a team without rows still takes part in the block's
     // combine below.
+    // The team's rows are first + i * stride, i < count (this lane's row is
+    // offset by team.offset). Look-ahead walks keep their rows in a ring of
+    // two (one row ahead) or three (two rows ahead) register buffers whose
+    // roles rotate by unrolling, so no row is ever copied between registers:
+    // a copy would wait for the copied row's loads (and with them for every
+    // older access, stores included) before the next row's loads are issued.
     // In early mode the rows still held when a team's walk ends (its last
-    // row, or last two with two rows ahead) add their contributions first,
-    // the wave deposits its sums, and only then are those rows' gradients
-    // computed and stored, so that the block's global atomics drain under
-    // that work instead of after it.
+    // one or two) add their contributions first, the wave deposits its sums,
+    // and only then are those rows' gradients computed and stored, so that
+    // the block's global atomics drain under that work instead of after it.
     const int64_t stride = team.stride;
-    int64_t first = team.first;
-    if (first < rows) {
-        BackwardRow<V, GY> current;
-        bool deposited = false;
-        load_row(current, first + team.offset, false);
-        if (paced) {
-            for (; first + stride < rows; first += stride) {
-                process_row(current, first + team.offset, true);
-                load_row(current, first + stride + team.offset, true);
+    const int64_t first = team.first;
+    const int64_t count = first < rows ? (rows - first + stride - 1) / stride : 0;
+    auto row_of = [&](int64_t i) { return first + i * stride + team.offset; };
+    // Finishes the walk on the held rows `a` (row i) and, when present, `b`
+    // (row i + 1).
+    auto finish = [&](const BackwardRow<V, GY>& a, const BackwardRow<V, GY>& b, int64_t i) {
+        const bool second = i + 1 < count;
+        if (early) {
+            accumulate_row(a, row_of(i));
+            if (second) {
+                accumulate_row(b, row_of(i + 1));
             }
-        } else if constexpr (kTwoAhead) {
-            BackwardRow<V, GY> second;
-            if (first + stride < rows) {
-                load_row(second, first + stride + team.offset, false);
-            }
-            for (; first + 2 * stride < rows; first += stride) {
-                BackwardRow<V, GY> third;
-                load_row(third, first + 2 * stride + team.offset, false);
-                process_row(current, first + team.offset, true);
-                current = second;
-                second = third;
-            }
-            if (first + stride < rows) {
-                if (early) {
-                    accumulate_row(current, first + team.offset);
-                    accumulate_row(second, first + stride + team.offset);
-                    deposit_parameters();
-                    deposited = true;
-                }
-                process_row(current, first + team.offset, !early);
-                current = second;
-                first += stride;
-            }
-        } else {
-            for (; first + stride < rows; first += stride) {
-                BackwardRow<V, GY> next;
-                load_row(next, first + stride + team.offset, false);
-                process_row(current, first + team.offset, true);
-                current = next;
-            }
-        }
-        if (early && !deposited) {
-            accumulate_row(current, first + team.offset);
             deposit_parameters();
         }
-        process_row(current, first + team.offset, !early);
+        process_row(a, row_of(i), !early);
+        if (second) {
+            process_row(b, row_of(i + 1), !early);
+        }
+    };
+    if (count > 0) {
+        BackwardRow<V, GY> ra;
+        BackwardRow<V, GY> rb;
+        load_row(ra, row_of(0), false);
+        if (paced) {
+            int64_t i = 0;
+            for (; i + 1 < count; ++i) {
+                process_row(ra, row_of(i), true);
+                load_row(ra, row_of(i + 1), true);
+            }
+            finish(ra, rb, i);
+        } else if constexpr (!RLN_BWD_RING) {
+            int64_t i = 0;
+            for (; i + 1 < count; ++i) {
+                BackwardRow<V, GY> next;
+                load_row(next, row_of(i + 1), false);
+                process_row(ra, row_of(i), true);
+                ra = next;
+            }
+            finish(ra, rb, i);
+        } else if constexpr (kTwoAhead) {
+            BackwardRow<V, GY> rc;
+            if (count > 1) {
+                load_row(rb, row_of(1), false);
+            }
+            int64_t i = 0;
+            for (; i + 3 <= count; i += 3) {
+                load_row(rc, row_of(i + 2), false);
+                process_row(ra, row_of(i), true);
+                if (i + 3 < count) {
+                    load_row(ra, row_of(i + 3), false);
+                }
+                process_row(rb, row_of(i + 1), true);
+                if (i + 4 < count) {
+                    load_row(rb, row_of(i + 4), false);
+                }
+                process_row(rc, row_of(i + 2), true);
+            }
+            if (i < count) {
+                finish(ra, rb, i);
+            } else if (early) {
+                deposit_parameters();
+            }
+        } else {
+            int64_t i = 0;
+            for (; i + 2 <= count; i += 2) {
+                load_row(rb, row_of(i + 1), false);
+                process_row(ra, row_of(i), true);
+                if (i + 2 < count) {
+                    load_row(ra, row_of(i + 2), false);
+                }
+                process_row(rb, row_of(i + 1), true);
+            }
+            if (i < count) {
+                finish(ra, rb, i);
+            } else if (early) {
+                deposit_parameters();
+            }
+        }
     } else if (early) {
         deposit_parameters();
     }
@@ -1715,12 +1905,13 @@ int check_shape(const S& shape, Pass pass, int64_t rows) {
 
 // Blocks of one forward kernel instance a CU holds at once (registers and
 // LDS permitting), asked of the runtime once per instance; 0 if it cannot say.
-template <typename S, typename B, typename N, bool Aligned>
+template <typename S, typename B, typename N, bool Aligned, bool Ring>
 int forward_resident_blocks() {
     static const int resident = [] {
         int blocks = 0;
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &blocks, reinterpret_cast<const void*>(&rln_forward_kernel<S, B, N, Aligned>),
+                &blocks,
+                reinterpret_cast<const void*>(&rln_forward_kernel<S, B, N, Aligned, Ring>),
                 S::kForwardThreads, 0) != hipSuccess) {
             static_cast<void>(hipGetLastError());  // clear the failed call's error
             return 0;
@@ -1730,11 +1921,32 @@ int forward_resident_blocks() {
     return resident;
 }
 
-template <typename S, typename B, typename N, bool Aligned>
-int launch_forward(const ForwardArgs& a, S shape) {
+// Whether a forward launch runs the ring-walk kernel instance: launches that
+// are not paced and whose grid gives teams several rows - the small-launch
+// grid, the one-round grid of four-slot rows and the persistent grid of
+// multi-wave rows (forward_blocks).
+template <typename S>
+bool forward_ring(int64_t rows, int64_t hidden) {
+    if (forward_paced(rows, hidden)) {
+        return false;
+    }
+    const int64_t elements = rows * hidden;
+    if (S::kParts > 1) {
+        return elements < (S::kParts < 8 ? kForwardPersistentElements
+                                         : kForwardPersistentElements8);
+    }
+    if (S::kHidden > 0 && S::kV == 4 && elements < kForwardPersistentElements) {
+        return true;
+    }
+    return elements < kForwardLargeElements;
+}
+
+template <typename S, typename B, typename N, bool Aligned, bool Ring>
+int launch_forward_walk(const ForwardArgs& a, S shape) {
     const dim3 grid(static_cast<unsigned>(forward_blocks<S>(
-        a.rows, shape.hidden(), a.compute_units, forward_resident_blocks<S, B, N, Aligned>())));
-    rln_forward_kernel<S, B, N, Aligned><<<grid, S::kForwardThreads, 0, a.stream>>>(
+        a.rows, shape.hidden(), a.compute_units,
+        forward_resident_blocks<S, B, N, Aligned, Ring>())));
+    rln_forward_kernel<S, B, N, Aligned, Ring><<<grid, S::kForwardThreads, 0, a.stream>>>(
         a.x,
         static_cast<const B*>(a.branch),
         a.weight,
@@ -1755,6 +1967,13 @@ int launch_forward(const ForwardArgs& a, S shape) {
         a.philox,
         forward_paced(a.rows, shape.hidden()));
     return check_launch("rln_forward_kernel");
+}
+
+template <typename S, typename B, typename N, bool Aligned>
+int launch_forward(const ForwardArgs& a, S shape) {
+    return forward_ring<S>(a.rows, shape.hidden())
+        ? launch_forward_walk<S, B, N, Aligned, true>(a, shape)
+        : launch_forward_walk<S, B, N, Aligned, false>(a, shape);
 }
 
 template <typename S, typename B, typename GY, bool Aligned>

@@ -155,3 +155,30 @@ def test_paced_element_access_matches_aligned(deterministic):
         assert_bitwise(host(shifted["parameters"]), host(aligned["parameters"]), "parameters")
     else:
         check_parameter_sums(shifted, aligned_case[5], rows)
+
+
+# Row counts around whole multiples of the teams the look-ahead walks use
+# (the backward's 2048 one-wave teams at 768 columns, 4096 rows per step at
+# 384; the forward's device-dependent grid on 256 CUs: 3072 teams at 768):
+# every team then walks 1 to 5 rows, so the register rings of the look-ahead
+# walks end on each of their buffers with one or two rows left.
+RING_CASES = [(768, rows) for rows in (2047, 2049, 3071, 3073, 4095, 4097, 6143, 6145,
+                                        8193, 9215, 9217, 10241)] + \
+             [(384, rows) for rows in (4095, 4097, 8193, 12287, 12289, 16385, 20479)]
+
+
+@pytest.mark.parametrize("hidden,rows", RING_CASES, ids=[f"{h}x{r}" for h, r in RING_CASES])
+def test_look_ahead_rows_equal_paced_rows_at_every_ring_position(hidden, rows):
+    """Every row output of a look-ahead launch equals, bit for bit, the same row
+    of a paced launch over more rows (fp16 branch, p = 0.1), for row counts
+    that end the look-ahead walks on every buffer of their rings."""
+    paced_rows = PACED_ELEMENTS // hidden + 37
+    print(f"[schedules] ring H={hidden} rows={rows} (paced reference {paced_rows})", flush=True)
+    case = make_case(paced_rows, hidden, torch.float16)
+    paced = run(case, paced_rows, torch.float32, 0.1, deterministic=True)
+    look_ahead = run(case, rows, torch.float32, 0.1, deterministic=True)
+    for name in ROW_OUTPUTS:
+        assert_same_bits(paced[name][:rows], look_ahead[name], name)
+    words = look_ahead["mask"].numel()
+    assert_same_bits(paced["mask"][:words], look_ahead["mask"], "mask")
+    check_parameter_sums(look_ahead, case[5], rows)
