@@ -251,7 +251,7 @@ def parse_args():
     parser.add_argument("--ab", action="append", default=[], metavar="NAME=DEFINES",
                         help="A/B run: also time a variant build of the library with the "
                              "comma-separated compile-time switches (e.g. "
-                             "'nt=RLN_STORE_POLICY=2'), built into benchmarks/variants/ if "
+                             "'nt=RLN_SMALL_STORE_POLICY=2'), built into benchmarks/variants/ if "
                              "missing, alternated round by round with the default build on C1 "
                              "(or the --config workloads); repeatable")
     parser.add_argument("--ab-rounds", type=int, default=5,
@@ -1209,6 +1209,8 @@ def probe_library():
                                                  ctypes.c_void_p]
     library.rln_probe_empty_launches.argtypes = [ctypes.c_int64, ctypes.c_int, ctypes.c_int,
                                                  ctypes.c_void_p]
+    library.rln_probe_atomic_policy.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
+                                                ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
     return library
 
 
@@ -1236,6 +1238,19 @@ def probe_fixed_costs(torch, runner: "Runner", library, hidden: int, repeats: in
                     raise RuntimeError("rln_probe_atomic_combine failed")
             batch(0)
             atomic[label][str(copies)] = round(runner.timed(batch, 1) * 1e3 / repeats, 3)
+    policies = {}
+    for policy, label in ((0, "plain"), (2, "nt"), (16, "sc1"), (18, "nt sc1")):
+        one = torch.zeros(2 * hidden, device="cuda")
+
+        def batch(_, policy=policy, one=one):
+            if library.rln_probe_atomic_policy(one.data_ptr(), hidden, policy, 256, repeats,
+                                               handle):
+                raise RuntimeError("rln_probe_atomic_policy failed")
+        us = runner.timed(batch, 1) * 1e3 / repeats
+        # Every float received exactly 256 * repeats additions of 1.0.
+        exact = bool(torch.all(one == float(256 * repeats)).item())
+        policies[label] = {"us": round(us, 3), "sums_exact": exact}
+    atomic["one copy, buffer atomics by cache policy"] = policies
     empty = {}
     for blocks in PROBE_EMPTY_BLOCKS:
         def batch(_, blocks=blocks):

@@ -366,6 +366,20 @@ __global__ __launch_bounds__(512) void probe_atomic_combine(float* sums, int hid
     }
 }
 
+// The same combine through buffer atomics carrying the cache-policy bits
+// `Aux` (sc0 = 1 asks for the pre-op value, nt = 2, sc1 = 16), into one copy.
+template <int Aux>
+__global__ __launch_bounds__(512) void probe_atomic_policy(float* sums, int hidden) {
+    const rsrc_t r = make_rsrc(sums, 2 * hidden * 4);
+    for (int entry = threadIdx.x; entry < 2 * hidden; entry += 512) {
+        const int owner = entry / 8;
+        const int which = (entry / 4) & 1;
+        const int column = owner * 4 + (entry & 3);
+        __builtin_amdgcn_raw_ptr_buffer_atomic_fadd_f32(1.0f, r, (which * hidden + column) * 4, 0,
+                                                    Aux);
+    }
+}
+
 // A kernel of `blocks` blocks doing nothing, for the per-launch cost.
 __global__ void probe_nothing(int) {}
 
@@ -496,6 +510,30 @@ int rln_probe_atomic_combine(float* sums, int64_t hidden, int copies, int ranges
         probe_atomic_combine<<<dim3(static_cast<unsigned>(blocks)), dim3(512), 0,
                                static_cast<hipStream_t>(stream)>>>(
             sums, static_cast<int>(hidden), copies, ranges);
+    }
+    return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+// `repeats` launches of the buffer-atomic combine with cache policy `policy`
+// (0, nt = 2, sc1 = 16, nt | sc1 = 18) over `sums` ([2, hidden] floats, one
+// copy) with `blocks` blocks; every launch adds exactly 1.0 per block to each
+// float, so the caller can check the sums after the last launch.
+int rln_probe_atomic_policy(float* sums, int64_t hidden, int policy, int64_t blocks,
+                            int repeats, void* stream) {
+    if (sums == nullptr || hidden <= 0 || hidden > 8192 || hidden % 32 != 0 || blocks <= 0
+        || blocks > 65536 || repeats <= 0) {
+        return 1;
+    }
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    for (int i = 0; i < repeats; ++i) {
+        const dim3 grid(static_cast<unsigned>(blocks));
+        switch (policy) {
+            case 0: probe_atomic_policy<0><<<grid, 512, 0, s>>>(sums, static_cast<int>(hidden)); break;
+            case 2: probe_atomic_policy<2><<<grid, 512, 0, s>>>(sums, static_cast<int>(hidden)); break;
+            case 16: probe_atomic_policy<16><<<grid, 512, 0, s>>>(sums, static_cast<int>(hidden)); break;
+            case 18: probe_atomic_policy<18><<<grid, 512, 0, s>>>(sums, static_cast<int>(hidden)); break;
+            default: return 1;
+        }
     }
     return hipGetLastError() == hipSuccess ? 0 : 3;
 }

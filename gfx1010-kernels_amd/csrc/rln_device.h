@@ -95,18 +95,24 @@
 #ifndef RLN_BWD_MAX_BLOCKS
 #define RLN_BWD_MAX_BLOCKS 256
 #endif
-// 1: the look-ahead backward keeps two rows in flight for one-wave rows of up
-// to three slots (kTwoAhead); 0 (default): one row, as every other shape.
-// Measured on MI355X at C1 (bench.py --ab, alternated, register rings):
-// backward 22.4 us with one row ahead against 22.9 us with two (input
-// gradients alone 19.0 against 20.2 us).
-#ifndef RLN_BWD_TWO_AHEAD
-#define RLN_BWD_TWO_AHEAD 0
+// The look-ahead backward keeps two rows in flight for one-part rows of at
+// most this many slots per lane (kTwoAhead), one row for every other shape.
+// Default 1: one-slot rows (128 and 256 columns) are short, so one row ahead
+// keeps too few bytes in flight ([262144, 128] backward 108.6 us against
+// 97.4 with two ahead); at C1 (three slots) one row ahead measured 22.4 us
+// against 22.9 us with two (input gradients alone 19.0 against 20.2 us;
+// bench.py --ab, alternated, register rings).
+#ifndef RLN_BWD_TWO_AHEAD_MAX_SLOTS
+#define RLN_BWD_TWO_AHEAD_MAX_SLOTS 1
 #endif
-// 1 (default): the look-ahead backward walks its rows in a ring of register
-// buffers; 0: one-ahead walks that copy the next row between registers (the
-// copy waits for that row's loads, and with them every older access, before
-// the following row's loads issue).
+// 1 (default): the look-ahead backward walks one-part rows in a ring of
+// register buffers; 0, and rows of several waves: one-ahead walks that copy
+// the next row between registers (the copy waits for that row's loads, and
+// with them every older access, before the following row's loads issue).
+// Measured on MI355X (bench.py --ab, alternated): the ring at C1 backward
+// 22.5 against 23.2 us, [262144, 768] 611 against 628 us; the copy walk for
+// rows of several waves: [8192, 1600] 43.3 against 49.9 us, [104857, 1280]
+// 410 against 462 us, C3 200 against 210 us.
 #ifndef RLN_BWD_RING
 #define RLN_BWD_RING 1
 #endif
@@ -141,32 +147,46 @@
 #ifndef RLN_PACED_MIN_HIDDEN
 #define RLN_PACED_MIN_HIDDEN 256
 #endif
+// The reference dropout stream's draws of a row: 1 (default) unrolled for the
+// launch width the public API uses at the row's size (128 threads up to 768
+// columns, 192 at 1024: the reference's table) and looped for the other
+// widths - except the forward of 768 columns with a 2-byte branch and fp32
+// output, which unrolls every width; 2 unrolled for every width; 0 looped
+// for every width. Unrolled, a row's Philox chains interleave (C1 forward
+// 16.9 against 17.4 us; [262144, 128] 80 against 93 us). Unrolling every
+// width takes the forward's ring instance past 168 VGPRs (two waves per SIMD
+// instead of three) at every size and type except 768 and 1024 columns with
+// a 2-byte branch and fp32 output (165), and where it crosses, it is slower
+// ([12291, 384] fp32 branch forward 16.1 against 14.2 us); at 768 it is
+// faster (C1 forward 15.2 against 15.9 us, step 39.9 against 40.8 us;
+// bench.py --ab, alternated).
 #ifndef RLN_REFERENCE_DRAWS_UNROLLED
 #define RLN_REFERENCE_DRAWS_UNROLLED 1
 #endif
 #ifndef RLN_NT_LOADS
 #define RLN_NT_LOADS 1
 #endif
-// Cache policy of the row outputs' stores (every output the kernels write per
-// row: updated, normalized, the mask, mean and rstd, grad_x, grad_branch),
-// as the cache-policy bits of a gfx950 buffer store: sc0 = 1, nt = 2,
-// sc1 = 16. The default, sc0 | sc1, writes through the caches at system
-// scope, so that no dirty line is left in L2 for the end-of-kernel release to
-// write back. Measured on MI355X with the streaming probe at C1 ([8192, 768],
-// benchmarks/rln_probe.hip, fastest grid per policy): forward-shaped pass
-// 15.2 us with sc0 | sc1 against 15.8 us plain and 18.8 us non-temporal;
-// backward-shaped 19.0 us against 19.5 us and 20.2 us; nt | sc1 and
-// sc0 | sc1 | nt are slower still (20.2-23 us).
-#ifndef RLN_STORE_POLICY
-#define RLN_STORE_POLICY 17
+// Cache policies of the row outputs' stores (every output the kernels write
+// per row: updated, normalized, the mask, mean and rstd, grad_x,
+// grad_branch), as the cache-policy bits of a gfx950 buffer store: sc0 = 1,
+// nt = 2, sc1 = 16. Launches over fewer than RLN_WRITE_THROUGH_ELEMENTS
+// elements write through the caches at system scope (sc0 | sc1), so that no
+// dirty line is left in L2 for the end-of-kernel release to write back;
+// larger launches store non-temporally. Measured on MI355X (bench.py --ab,
+// alternated): C1 [8192, 768] step 39.1 us write-through against 40.3 us
+// non-temporal (forward 14.8 against 17.0 us); at 2^26+ elements
+// non-temporal wins by 1-7 % (C3 358.7 against 371.6 us, [262144, 384]
+// 541 against 555 us), and so at [8192, 1600] (83.3 against 85.7 us). The
+// streaming probe at C1 (benchmarks/rln_probe.hip): forward-shaped pass 15.2
+// us write-through against 15.8 us plain and 18.8 us non-temporal.
+#ifndef RLN_SMALL_STORE_POLICY
+#define RLN_SMALL_STORE_POLICY 17
 #endif
-// The same for the dropout mask (a row's words are 32-byte pieces per slot)
-// and for the row statistics (mean, rstd: one word per row each).
-#ifndef RLN_MASK_STORE_POLICY
-#define RLN_MASK_STORE_POLICY RLN_STORE_POLICY
+#ifndef RLN_LARGE_STORE_POLICY
+#define RLN_LARGE_STORE_POLICY 2
 #endif
-#ifndef RLN_STATS_STORE_POLICY
-#define RLN_STATS_STORE_POLICY RLN_STORE_POLICY
+#ifndef RLN_WRITE_THROUGH_ELEMENTS
+#define RLN_WRITE_THROUGH_ELEMENTS (1ll << 23)
 #endif
 
 namespace rln {
@@ -679,12 +699,14 @@ __device__ __forceinline__ f32x4 load4(const float* __restrict__ pointer) {
 
 // ----------------------------------------------------------------------------
 // Row outputs. Every per-row output goes out through buffer stores with the
-// cache policy RLN_STORE_POLICY (a global store cannot carry its sc bits from
-// HIP source). A wave's stores of one row step go through one descriptor per
-// output over exactly the rows the wave writes in that step: its base and
-// extent are wave-uniform (scalar registers), every lane stores at a byte
-// offset into it, and the hardware's range check drops any store outside
-// the wave's rows.
+// launch's cache policy (a global store cannot carry its sc bits from HIP
+// source): write-through, or non-temporal (`wt` false), a wave-uniform kernel
+// argument, so each store site is a scalar branch between the two
+// instructions. A wave's stores of one row step go through one descriptor
+// per output over exactly the rows the wave writes in that step: its base
+// and extent are wave-uniform (scalar registers), every lane stores at a
+// byte offset into it, and the hardware's range check drops any store
+// outside the wave's rows.
 
 using rsrc_t = __amdgpu_buffer_rsrc_t;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -692,6 +714,7 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // The descriptor's fourth word for a raw (untyped, unswizzled) buffer.
 constexpr int kRawBufferWord3 = 0x00020000;
+constexpr int64_t kWriteThroughElements = RLN_WRITE_THROUGH_ELEMENTS;
 
 // `value` of the wave's first active lane, in scalar registers.
 __device__ __forceinline__ int64_t wave_uniform(int64_t value) {
@@ -710,25 +733,51 @@ __device__ __forceinline__ rsrc_t output_range(T* tensor, int64_t first, int64_t
         static_cast<int>(count * static_cast<int64_t>(sizeof(T))), kRawBufferWord3);
 }
 
-template <int Policy = RLN_STORE_POLICY>
-__device__ __forceinline__ void output_b32(rsrc_t r, uint32_t offset, uint32_t value) {
-    __builtin_amdgcn_raw_buffer_store_b32(value, r, offset, 0, Policy);
+__device__ __forceinline__ void output_b32(rsrc_t r, uint32_t offset, uint32_t value, bool wt) {
+    if (wt) {
+        __builtin_amdgcn_raw_buffer_store_b32(value, r, offset, 0, RLN_SMALL_STORE_POLICY);
+    } else {
+        __builtin_amdgcn_raw_buffer_store_b32(value, r, offset, 0, RLN_LARGE_STORE_POLICY);
+    }
+}
+
+__device__ __forceinline__ void output_b128(rsrc_t r, uint32_t offset, u32x4 value, bool wt) {
+    if (wt) {
+        __builtin_amdgcn_raw_buffer_store_b128(value, r, offset, 0, RLN_SMALL_STORE_POLICY);
+    } else {
+        __builtin_amdgcn_raw_buffer_store_b128(value, r, offset, 0, RLN_LARGE_STORE_POLICY);
+    }
+}
+
+__device__ __forceinline__ void output_b64(rsrc_t r, uint32_t offset, u32x2 value, bool wt) {
+    if (wt) {
+        __builtin_amdgcn_raw_buffer_store_b64(value, r, offset, 0, RLN_SMALL_STORE_POLICY);
+    } else {
+        __builtin_amdgcn_raw_buffer_store_b64(value, r, offset, 0, RLN_LARGE_STORE_POLICY);
+    }
+}
+
+__device__ __forceinline__ void output_b16(rsrc_t r, uint32_t offset, uint16_t value, bool wt) {
+    if (wt) {
+        __builtin_amdgcn_raw_buffer_store_b16(value, r, offset, 0, RLN_SMALL_STORE_POLICY);
+    } else {
+        __builtin_amdgcn_raw_buffer_store_b16(value, r, offset, 0, RLN_LARGE_STORE_POLICY);
+    }
 }
 
 // Four fp32 values at byte `offset`: one 128-bit store, or four element
 // stores with the same values when the tensor is not 16-byte aligned.
 template <bool Aligned>
-__device__ __forceinline__ void output4(rsrc_t r, uint32_t offset, f32x4 value) {
+__device__ __forceinline__ void output4(rsrc_t r, uint32_t offset, f32x4 value, bool wt) {
     if constexpr (Aligned) {
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, value), r, offset, 0,
-                                               RLN_STORE_POLICY);
+        output_b128(r, offset, __builtin_bit_cast(u32x4, value), wt);
     } else {
         // Element by element through a scalar copy: clang's __builtin_bit_cast
         // of a vector element expression (value.y) reads element 0.
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const float element = value[e];
-            output_b32(r, offset + 4 * e, __builtin_bit_cast(uint32_t, element));
+            output_b32(r, offset + 4 * e, __builtin_bit_cast(uint32_t, element), wt);
         }
     }
 }
@@ -784,21 +833,20 @@ __device__ __forceinline__ f32x4 widen4(typename Vector4<T>::type raw) {
 // Stores four fp32 values as type T at byte `offset` (the offset of the
 // first element); narrowing rounds to nearest even.
 template <typename T, bool Aligned>
-__device__ __forceinline__ void output_convert4(rsrc_t r, uint32_t offset, f32x4 value) {
+__device__ __forceinline__ void output_convert4(rsrc_t r, uint32_t offset, f32x4 value,
+                                                bool wt) {
     if constexpr (std::is_same_v<T, float>) {
-        output4<Aligned>(r, offset, value);
+        output4<Aligned>(r, offset, value, wt);
     } else {
         const typename Vector4<T>::type packed =
             __builtin_convertvector(value, typename Vector4<T>::type);
         if constexpr (Aligned) {
-            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, packed), r, offset, 0,
-                                                  RLN_STORE_POLICY);
+            output_b64(r, offset, __builtin_bit_cast(u32x2, packed), wt);
         } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                __builtin_amdgcn_raw_buffer_store_b16(
-                    __builtin_bit_cast(uint16_t, static_cast<T>(packed[e])), r,
-                    offset + 2 * e, 0, RLN_STORE_POLICY);
+                output_b16(r, offset + 2 * e, __builtin_bit_cast(uint16_t, static_cast<T>(packed[e])),
+                           wt);
             }
         }
     }
@@ -1025,14 +1073,21 @@ __device__ __forceinline__ uint32_t reference_keep_bits_looped(
 }
 
 // The reference stream's keep bits for a launch of `threads` (128, 192 or
-// 256) threads per row: one unrolled instance per width, chosen by a
-// wave-uniform switch (RLN_REFERENCE_DRAWS_UNROLLED, default 1), or the
-// looped draws.
-template <typename S>
+// 256) threads per row: unrolled for the widths RLN_REFERENCE_DRAWS_UNROLLED
+// selects (a wave-uniform switch), else the looped draws.
+template <typename S, bool AllWidths = false>
 __device__ __forceinline__ uint32_t reference_keep_bits(
     uint16_t* stage, int64_t row, int lane, int group, int threads, uint64_t position,
     uint32_t key0, uint32_t key1, uint32_t threshold) {
-    if constexpr (!RLN_REFERENCE_DRAWS_UNROLLED) {
+    constexpr int kApiThreads = S::kHidden == 1024 ? 192 : 128;
+    if constexpr (RLN_REFERENCE_DRAWS_UNROLLED == 0) {
+        return reference_keep_bits_looped<S>(stage, row, lane, group, threads, position, key0,
+                                             key1, threshold);
+    } else if constexpr (RLN_REFERENCE_DRAWS_UNROLLED == 1 && !AllWidths) {
+        if (threads == kApiThreads) {
+            return reference_keep_bits_of<S, kApiThreads>(stage, row, lane, group, position, key0,
+                                                          key1, threshold);
+        }
         return reference_keep_bits_looped<S>(stage, row, lane, group, threads, position, key0,
                                              key1, threshold);
     }
@@ -1113,9 +1168,11 @@ void rln_forward_kernel(
     float scale,
     uint32_t threshold,
     PhiloxArgs philox,
-    int paced) {
+    int paced,
+    int write_through) {
     constexpr int V = S::kV;
     using T = Teams<S, S::kForwardThreads>;
+    const bool wt = write_through != 0;
     const int64_t hidden = shape.hidden();
     const float inv_hidden = shape.inv_hidden();
     const T team;
@@ -1205,9 +1262,11 @@ void rln_forward_kernel(
         if constexpr (kReferenceStream) {
             if (reference_stream) {
                 const int wave = threadIdx.x / kWaveSize;
-                return reference_keep_bits<S>(stage[wave * S::kRowsPerWave + team.offset], row,
-                                              l, team.offset, philox.threads, position, key0,
-                                              key1, threshold);
+                constexpr bool kAllWidths =
+                    S::kHidden == 768 && sizeof(B) == 2 && std::is_same_v<N, float>;
+                return reference_keep_bits<S, kAllWidths>(
+                    stage[wave * S::kRowsPerWave + team.offset], row, l, team.offset,
+                    philox.threads, position, key0, key1, threshold);
             }
         }
         return 0u;
@@ -1266,7 +1325,7 @@ void rln_forward_kernel(
             }
             u[v] = r.x[v] + bv;
             if (valid && slots.active(v)) {
-                output4<Aligned>(updated_out, (element + slots.column(v)) * 4, u[v]);
+                output4<Aligned>(updated_out, (element + slots.column(v)) * 4, u[v], wt);
             }
             if (!slots.active(v)) {
                 u[v] = zero4();
@@ -1282,10 +1341,10 @@ void rln_forward_kernel(
                 // active or all idle (hidden is a multiple of 32).
                 const uint32_t word = or8(keep_bits[v] << (4 * (l & 7)));
                 if (valid && slots.active(v) && (l & 7) == 0) {
-                    output_b32<RLN_MASK_STORE_POLICY>(mask_out,
+                    output_b32(mask_out,
                                (row_in_wave * static_cast<uint32_t>(words) + slots.vector(v) / 8)
                                    * 4,
-                               word);
+                               word, wt);
                 }
             }
         }
@@ -1310,12 +1369,10 @@ void rln_forward_kernel(
 
         if (valid) {
             if (l == 0 && team.part == 0) {
-                output_b32<RLN_STATS_STORE_POLICY>(output_range(mean_out, wave_row, wave_rows),
-                                                   row_in_wave * 4,
-                                                   __builtin_bit_cast(uint32_t, mean));
-                output_b32<RLN_STATS_STORE_POLICY>(output_range(rstd_out, wave_row, wave_rows),
-                                                   row_in_wave * 4,
-                                                   __builtin_bit_cast(uint32_t, rstd));
+                output_b32(output_range(mean_out, wave_row, wave_rows), row_in_wave * 4,
+                           __builtin_bit_cast(uint32_t, mean), wt);
+                output_b32(output_range(rstd_out, wave_row, wave_rows), row_in_wave * 4,
+                           __builtin_bit_cast(uint32_t, rstd), wt);
             }
 #pragma unroll
             for (int v = 0; v < V; ++v) {
@@ -1326,7 +1383,7 @@ void rln_forward_kernel(
                     __builtin_fmaf(u[v].w * rstd, w[v].w, b[v].w)};
                 if (slots.active(v)) {
                     output_convert4<N, Aligned>(normalized_out,
-                                                (element + slots.column(v)) * sizeof(N), y);
+                                                (element + slots.column(v)) * sizeof(N), y, wt);
                 }
             }
         }
@@ -1468,13 +1525,15 @@ void rln_backward_kernel(
     S shape,
     int flags,
     float scale,
-    int paced) {
+    int paced,
+    int write_through) {
     constexpr int L = S::kLanes;
+    const bool wt = write_through != 0;
     constexpr int V = S::kV;
     constexpr int P = S::kParts;
     using T = Teams<S, S::kBackwardBlockThreads>;
     constexpr int kWaves = T::kWaves;
-    constexpr bool kTwoAhead = RLN_BWD_TWO_AHEAD && P == 1 && V <= 3;
+    constexpr bool kTwoAhead = P == 1 && V <= RLN_BWD_TWO_AHEAD_MAX_SLOTS;
     const int64_t hidden = shape.hidden();
     const float inv_hidden = shape.inv_hidden();
     const int lane = threadIdx.x & (kWaveSize - 1);
@@ -1599,7 +1658,7 @@ void rln_backward_kernel(
                     const f32x4 q = gy[v] * w[v];
                     g = g + r.rstd * ((q - mean_q) - xhat[v] * mean_qx);
                 }
-                output4<Aligned>(grad_x_out, (element + column) * 4, g);
+                output4<Aligned>(grad_x_out, (element + column) * 4, g, wt);
                 if (dropout) {
                     const uint32_t bits = r.mask_word[v] >> (4 * (l & 7));
                     g.x = g.x * (static_cast<float>(bits & 1u) * scale);
@@ -1607,7 +1666,8 @@ void rln_backward_kernel(
                     g.z = g.z * (static_cast<float>((bits >> 2) & 1u) * scale);
                     g.w = g.w * (static_cast<float>((bits >> 3) & 1u) * scale);
                 }
-                output_convert4<B, Aligned>(grad_branch_out, (element + column) * sizeof(B), g);
+                output_convert4<B, Aligned>(grad_branch_out, (element + column) * sizeof(B), g,
+                                            wt);
             }
         }
 
@@ -1746,7 +1806,7 @@ void rln_backward_kernel(
                 load_row(ra, row_of(i + 1), true);
             }
             finish(ra, rb, i);
-        } else if constexpr (!RLN_BWD_RING) {
+        } else if constexpr (!RLN_BWD_RING || P > 1) {
             int64_t i = 0;
             for (; i + 1 < count; ++i) {
                 BackwardRow<V, GY> next;
@@ -1965,7 +2025,8 @@ int launch_forward_walk(const ForwardArgs& a, S shape) {
         a.scale,
         a.threshold,
         a.philox,
-        forward_paced(a.rows, shape.hidden()));
+        forward_paced(a.rows, shape.hidden()),
+        a.rows * shape.hidden() < kWriteThroughElements ? 1 : 0);
     return check_launch("rln_forward_kernel");
 }
 
@@ -1996,7 +2057,8 @@ int launch_backward(const BackwardArgs& a, S shape) {
         shape,
         a.flags,
         a.scale,
-        backward_paced(a.rows, shape.hidden()));
+        backward_paced(a.rows, shape.hidden()),
+        a.rows * shape.hidden() < kWriteThroughElements ? 1 : 0);
     return check_launch("rln_backward_kernel");
 }
 
