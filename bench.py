@@ -1015,14 +1015,15 @@ def mangled_kernel_name(name: str) -> str:
     __bf16 arguments mangled, so counter csv rows are matched on this too."""
     import re
 
-    match = re.fullmatch(r"rln::(\w+)<rln::(\w+)<(\d+), (\d+)>, ([\w ]+), ([\w ]+), (true|false)>",
-                         name)
+    match = re.fullmatch(r"rln::(\w+)<rln::(\w+)<(\d+), (\d+)>, ([\w ]+), ([\w ]+), "
+                         r"(true|false)(?:, (true|false))?>", name)
     if match is None:
         raise ValueError(f"not a kernel_name() instance: {name}")
-    kernel, shape, first, second, branch, normalized, aligned = match.groups()
+    kernel, shape, first, second, branch, normalized, aligned, ring = match.groups()
     types = {"float": "f", "_Float16": "DF16_", "__bf16": "DF16b"}
+    flags = f"Lb{int(aligned == 'true')}E" + (f"Lb{int(ring == 'true')}E" if ring else "")
     return (f"_ZN3rln{len(kernel)}{kernel}INS_{len(shape)}{shape}ILi{first}ELi{second}EEE"
-            f"{types[branch]}{types[normalized]}Lb{int(aligned == 'true')}EEE")
+            f"{types[branch]}{types[normalized]}{flags}EE")
 
 
 def _counter_values(directory: str) -> tuple[str, dict[str, list[float]]]:
@@ -1417,8 +1418,27 @@ def kernel_name(kernel: str, workload: Workload) -> str:
         vectors = -(-hidden // (256 * parts))
         shape = f"rln::WideShape<{vectors}, {parts}>"
     types = {"f32": "float", "f16": "_Float16", "bf16": "__bf16"}
+    ring = ", true" if forward_ring(workload.rows, hidden) else ", false"
     return (f"rln::{kernel}<{shape}, {types[workload.branch]}, "
-            f"{types[workload.normalized]}, true>")
+            f"{types[workload.normalized]}, true{ring if forward else ''}>")
+
+
+def forward_ring(rows: int, hidden: int) -> bool:
+    """Whether the forward runs its ring-walk instance (rln_device.h
+    forward_ring and forward_paced): launches that are not paced and whose
+    grid gives teams several rows."""
+    elements = rows * hidden
+    parts = wide_parts(hidden, "rln_forward_kernel")
+    vectors = -(-hidden // (256 * parts))
+    specialized_four_slots = hidden in (512, 1024)
+    if hidden >= 256 and elements >= 1 << 23:
+        if parts == 1 or (elements >= 1 << 26 and not (parts == 8 and vectors == 4)):
+            return False
+    if parts > 1:
+        return elements < (1 << 24 if parts < 8 else 1 << 27)
+    if specialized_four_slots and elements < 1 << 24:
+        return True
+    return elements < 1 << 23
 
 
 def result_line(torch, workload: Workload, timing: dict, steps: int, warmup: int,
