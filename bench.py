@@ -1201,6 +1201,7 @@ def probe_library():
     library.rln_probe_variant_name.argtypes = [ctypes.c_int]
     library.rln_probe_variant_kind.argtypes = [ctypes.c_int]
     library.rln_probe_variant_threads.argtypes = [ctypes.c_int]
+    library.rln_probe_variant_config.argtypes = [ctypes.c_int]
     library.rln_probe_one_step_blocks.restype = ctypes.c_int64
     library.rln_probe_one_step_blocks.argtypes = [ctypes.c_int, ctypes.c_int64, ctypes.c_int64]
     library.rln_probe_launch.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_int64,
@@ -1268,10 +1269,22 @@ PROBE_WAVES_PER_CU = (4, 8, 12, 16, 24, 32)
 PROBE_FINALISTS = 6
 
 
+# Stream configurations benchmarks/rln_probe.hip instantiates (its Cfg bits).
+PROBE_CONFIGS = (0, 1, 2, 5)
+
+
+def probe_config(workload: Workload) -> int:
+    """The probe's stream configuration of a workload: bit 0 an fp32 branch
+    (else 16-bit), bit 1 a 16-bit normalized output and upstream gradient
+    (else fp32), bit 2 no mask (not dropping)."""
+    return ((workload.branch_bytes == 4) | (workload.normalized_bytes == 2) << 1
+            | (not workload.dropping) << 2)
+
+
 def probe_applies(workload: Workload) -> bool:
-    """The probe moves an fp16 branch and fp32 normalized values (and their
-    gradients), with a mask: the headline configuration's streams."""
-    return (workload.branch == "f16" and workload.normalized == "f32" and workload.dropping
+    """Whether the probe moves this workload's streams: a configuration it
+    instantiates, over at most 2^31 bytes per fp32 tensor."""
+    return (probe_config(workload) in PROBE_CONFIGS
             and workload.rows * workload.hidden * 4 <= (1 << 31))
 
 
@@ -1287,13 +1300,15 @@ def probe_floor(torch, runner: "Runner", library, launches: int = ROOFLINE_LAUNC
     forward and backward are timed alternating, as the step runs them.
     Microseconds per launch."""
     w = runner.w
+    config = probe_config(w)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     arrays = []
     for t in runner.sets:
-        tensors = (t["x"], t["branch"], t["updated"], t["normalized"], t["mask"], t["mean"],
-                   t["rstd"], t["grad_updated"], t["grad_normalized"], t["updated"], t["mask"],
-                   t["mean"], t["rstd"], t["grad_x"], t["grad_branch"])
-        arrays.append((ctypes.c_void_p * len(tensors))(*[x.data_ptr() for x in tensors]))
+        names = ("x", "branch", "updated", "normalized", "mask", "mean", "rstd", "grad_updated",
+                 "grad_normalized", "updated", "mask", "mean", "rstd", "grad_x", "grad_branch")
+        # NULL for what the workload lacks (a forward-only one's gradients).
+        arrays.append((ctypes.c_void_p * len(names))(
+            *[t[name].data_ptr() if name in t else None for name in names]))
     handle = ctypes.c_void_p(runner.handle)
     rows, hidden = ctypes.c_int64(w.rows), ctypes.c_int64(w.hidden)
 
@@ -1309,6 +1324,8 @@ def probe_floor(torch, runner: "Runner", library, launches: int = ROOFLINE_LAUNC
     points = {0: [], 1: []}
     for index in range(library.rln_probe_variant_count()):
         kind = library.rln_probe_variant_kind(index)
+        if library.rln_probe_variant_config(index) != config or (kind == 1 and not w.backward):
+            continue
         threads = library.rln_probe_variant_threads(index)
         one_step = library.rln_probe_one_step_blocks(index, w.rows, w.hidden)
         grids = {"one step per thread": one_step}
@@ -1333,6 +1350,8 @@ def probe_floor(torch, runner: "Runner", library, launches: int = ROOFLINE_LAUNC
                                  "index": index, "us": round(us, 3)})
     best = {}
     for kind, label in ((0, "fwd"), (1, "bwd")):
+        if not points[kind]:
+            continue
         finalists = sorted(points[kind], key=lambda point: point["us"])[:PROBE_FINALISTS]
         for point in finalists:
             point["us_full"] = []
@@ -1343,25 +1362,26 @@ def probe_floor(torch, runner: "Runner", library, launches: int = ROOFLINE_LAUNC
         for point in finalists:
             point["us_full"] = round(min(point["us_full"]), 3)
         best[label] = min(finalists, key=lambda point: point["us_full"])
-    forward = launcher(best["fwd"]["index"], best["fwd"]["blocks"])
-    backward = launcher(best["bwd"]["index"], best["bwd"]["blocks"])
+    result = {}
+    for label, point in best.items():
+        result[label] = point["us_full"]
+        result[f"{label}_probe"] = f'{point["variant"]}, {point["grid"]} ({point["blocks"]} blocks)'
+    if "bwd" in best:
+        forward = launcher(best["fwd"]["index"], best["fwd"]["blocks"])
+        backward = launcher(best["bwd"]["index"], best["bwd"]["blocks"])
 
-    def step(index):
-        forward(index)
-        backward(index)
+        def step(index):
+            forward(index)
+            backward(index)
 
-    result = {
-        "fwd": best["fwd"]["us_full"],
-        "fwd_probe": f'{best["fwd"]["variant"]}, {best["fwd"]["grid"]} ({best["fwd"]["blocks"]} blocks)',
-        "bwd": best["bwd"]["us_full"],
-        "bwd_probe": f'{best["bwd"]["variant"]}, {best["bwd"]["grid"]} ({best["bwd"]["blocks"]} blocks)',
-        "step": round(runner.timed(step, launches) * 1e3, 3),
+        result["step"] = round(runner.timed(step, launches) * 1e3, 3)
+    result.update({
         "fixed_costs": probe_fixed_costs(torch, runner, library, w.hidden),
         "points": len(points[0]) + len(points[1]),
         "kind": ("fastest of the benchmarks/rln_probe.hip streaming variants with the op's "
                  f"exact streams, {launches} launches back to back, {len(runner.sets)} rotated "
                  "sets; step = the fastest forward and backward alternating"),
-    }
+    })
     if table:
         result["table"] = sorted(points[0] + points[1],
                                  key=lambda point: (point["variant"][:3], point["us"]))
@@ -1646,9 +1666,9 @@ def main() -> int:
 
 
 def run_ceilings(torch, library, cabi, stream, args, workloads) -> None:
-    """One line per workload whose streams the probe moves (fp16 branch,
-    fp32 normalized, dropping): the op's kernels and the probe's measured
-    streaming floor over the same buffers, microseconds per launch."""
+    """One line per workload whose streams the probe moves (probe_applies):
+    the op's kernels and the probe's measured streaming floor over the same
+    buffers, microseconds per launch."""
     probe = probe_library()
     for workload in workloads:
         if not probe_applies(workload):

@@ -1,15 +1,18 @@
 // Streaming probe for the benchmark (benchmarks/librln_probe_gfx950.so,
 // loaded by bench.py only; the operator never calls it). Each kernel moves
 // exactly the bytes of one pass of the fused residual LayerNorm over
-// [rows, hidden] with an fp16 branch and fp32 everything else (the headline
-// configuration's streams), with no row reductions and no dropout draws:
+// [rows, hidden], with no row reductions and no dropout draws:
 //
-//   forward:  reads x (fp32), branch (fp16); writes updated (fp32),
-//             normalized (fp32), one mask word per 32 columns, mean and
-//             rstd per row;
-//   backward: reads grad_updated (fp32), grad_normalized (fp32), updated
-//             (fp32), the mask word of each 32 columns, mean and rstd per
-//             row; writes grad_x (fp32), grad_branch (fp16).
+//   forward:  reads x (fp32), branch; writes updated (fp32), normalized,
+//             one mask word per 32 columns, mean and rstd per row;
+//   backward: reads grad_updated (fp32), grad_normalized, updated (fp32),
+//             the mask word of each 32 columns, mean and rstd per row;
+//             writes grad_x (fp32), grad_branch.
+//
+// The stream configuration is a template argument (Cfg bits): the branch and
+// grad_branch 16-bit (the headline configuration, Cfg 0) or fp32 (bit 0);
+// normalized and grad_normalized fp32 or 16-bit (bit 1); the mask written
+// and read (training with dropout) or absent (bit 2).
 //
 // The variants span the launch and access choices a streaming kernel has on
 // MI355X, so that the fastest of them is a measured floor for the bytes of
@@ -131,6 +134,16 @@ struct Geometry {
     uint32_t rows;
 };
 
+// The streams of stream configuration Cfg.
+template <int Cfg>
+struct Streams {
+    static constexpr bool kBranch32 = (Cfg & 1) != 0;  // branch, grad_branch fp32
+    static constexpr bool kNorm16 = (Cfg & 2) != 0;    // normalized, grad_normalized 16-bit
+    static constexpr bool kMask = (Cfg & 4) == 0;      // mask written / read
+    static constexpr uint32_t kBranchBytes = kBranch32 ? 16 : 8;  // per four-column unit
+    static constexpr uint32_t kNormBytes = kNorm16 ? 8 : 16;
+};
+
 // Unit index of slot k of this lane in the step starting at `base`.
 template <int T, int U, bool Wide>
 __device__ __forceinline__ uint32_t unit_of(uint32_t base, int k) {
@@ -141,19 +154,22 @@ __device__ __forceinline__ uint32_t unit_of(uint32_t base, int k) {
     }
 }
 
-template <int T, int U, int LoadAux, int StoreAux, bool Ahead, bool Wide>
+template <int T, int U, int LoadAux, int StoreAux, bool Ahead, bool Wide, int Cfg>
 __global__ __launch_bounds__(T) void probe_forward(ProbeBuffers b, Geometry g) {
+    using C = Streams<Cfg>;
     static_assert(!Wide || U % 2 == 0, "wide fp16 takes unit pairs");
+    static_assert(!Wide || !C::kBranch32, "wide applies to a 16-bit branch");
     const rsrc_t rx = make_rsrc(b.x, g.units * 16);
-    const rsrc_t rb = make_rsrc(b.branch, g.units * 8);
+    const rsrc_t rb = make_rsrc(b.branch, g.units * C::kBranchBytes);
     const rsrc_t ru = make_rsrc(b.updated_out, g.units * 16);
-    const rsrc_t rn = make_rsrc(b.normalized, g.units * 16);
-    const rsrc_t rm = make_rsrc(b.mask_out, g.units / 2);
+    const rsrc_t rn = make_rsrc(b.normalized, g.units * C::kNormBytes);
+    const rsrc_t rm = make_rsrc(b.mask_out, C::kMask ? g.units / 2 : 0);
     const rsrc_t rmean = make_rsrc(b.mean_out, g.rows * 4);
     const rsrc_t rrstd = make_rsrc(b.rstd_out, g.rows * 4);
     struct Regs {
         f32x4 x[U];
-        u32x2 br[Wide ? 1 : U];
+        u32x2 br[Wide || C::kBranch32 ? 1 : U];
+        u32x4 br32[C::kBranch32 ? U : 1];
         u32x4 wide[Wide ? U / 2 : 1];
     };
     auto load = [&](Regs& r, uint32_t base) {
@@ -161,7 +177,9 @@ __global__ __launch_bounds__(T) void probe_forward(ProbeBuffers b, Geometry g) {
         for (int k = 0; k < U; ++k) {
             const uint32_t j = unit_of<T, U, Wide>(base, k);
             r.x[k] = load128<LoadAux>(rx, j * 16);
-            if constexpr (Wide) {
+            if constexpr (C::kBranch32) {
+                r.br32[k] = load128u<LoadAux>(rb, j * 16);
+            } else if constexpr (Wide) {
                 if ((k & 1) == 0) {
                     r.wide[k / 2] = load128u<LoadAux>(rb, j * 8);
                 }
@@ -174,20 +192,26 @@ __global__ __launch_bounds__(T) void probe_forward(ProbeBuffers b, Geometry g) {
 #pragma unroll
         for (int k = 0; k < U; ++k) {
             const uint32_t j = unit_of<T, U, Wide>(base, k);
-            u32x2 raw;
-            if constexpr (Wide) {
+            f32x4 branch;
+            if constexpr (C::kBranch32) {
+                branch = __builtin_bit_cast(f32x4, r.br32[k]);
+            } else if constexpr (Wide) {
                 const u32x4 pair = r.wide[k / 2];
-                raw = (k & 1) ? u32x2{pair.z, pair.w} : u32x2{pair.x, pair.y};
+                branch = widen((k & 1) ? u32x2{pair.z, pair.w} : u32x2{pair.x, pair.y});
             } else {
-                raw = r.br[k];
+                branch = widen(r.br[k]);
             }
-            const f32x4 u = r.x[k] + widen(raw);
+            const f32x4 u = r.x[k] + branch;
             store128<StoreAux>(ru, j * 16, u);
-            store128<StoreAux>(rn, j * 16, u * 0.5f);
+            if constexpr (C::kNorm16) {
+                store64<StoreAux>(rn, j * 8, narrow(u * 0.5f));
+            } else {
+                store128<StoreAux>(rn, j * 16, u * 0.5f);
+            }
             // (Scalar copies: clang's __builtin_bit_cast of a vector element
             // expression reads element 0.)
             const float u0 = u.x, u1 = u.y, u2 = u.z;
-            if ((j & 7) == 0) {
+            if (C::kMask && (j & 7) == 0) {
                 store32<StoreAux>(rm, (j / 8) * 4, __builtin_bit_cast(uint32_t, u0));
             }
             if (j % g.row_units == 0) {
@@ -218,18 +242,21 @@ __global__ __launch_bounds__(T) void probe_forward(ProbeBuffers b, Geometry g) {
     process(current, base);
 }
 
-template <int T, int U, int LoadAux, int StoreAux, bool Ahead, bool Wide>
+template <int T, int U, int LoadAux, int StoreAux, bool Ahead, bool Wide, int Cfg>
 __global__ __launch_bounds__(T) void probe_backward(ProbeBuffers b, Geometry g) {
+    using C = Streams<Cfg>;
     static_assert(!Wide || U % 2 == 0, "wide fp16 takes unit pairs");
+    static_assert(!Wide || !C::kBranch32, "wide applies to a 16-bit branch");
     constexpr bool kViaLds = (LoadAux & kLds) != 0;
+    static_assert(!kViaLds || !C::kNorm16, "the LDS path stages three fp32 streams");
     const rsrc_t rgu = make_rsrc(b.grad_updated, g.units * 16);
-    const rsrc_t rgy = make_rsrc(b.grad_normalized, g.units * 16);
+    const rsrc_t rgy = make_rsrc(b.grad_normalized, g.units * C::kNormBytes);
     const rsrc_t ru = make_rsrc(b.updated, g.units * 16);
-    const rsrc_t rm = make_rsrc(b.mask, g.units / 2);
+    const rsrc_t rm = make_rsrc(b.mask, C::kMask ? g.units / 2 : 0);
     const rsrc_t rmean = make_rsrc(b.mean, g.rows * 4);
     const rsrc_t rrstd = make_rsrc(b.rstd, g.rows * 4);
     const rsrc_t rgx = make_rsrc(b.grad_x, g.units * 16);
-    const rsrc_t rgb = make_rsrc(b.grad_branch, g.units * 8);
+    const rsrc_t rgb = make_rsrc(b.grad_branch, g.units * C::kBranchBytes);
     // LDS staging for the direct-to-LDS variant: per wave, two buffers of
     // three streams x U units x 64 lanes x 16 B.
     constexpr int kWaves = T / 64;
@@ -239,7 +266,8 @@ __global__ __launch_bounds__(T) void probe_backward(ProbeBuffers b, Geometry g) 
 
     struct Regs {
         f32x4 gu[kViaLds ? 1 : U];
-        f32x4 gy[kViaLds ? 1 : U];
+        f32x4 gy[kViaLds || C::kNorm16 ? 1 : U];
+        u32x2 gy16[C::kNorm16 ? U : 1];
         f32x4 u[kViaLds ? 1 : U];
         uint32_t word[U];
         float mean[U];
@@ -262,10 +290,14 @@ __global__ __launch_bounds__(T) void probe_backward(ProbeBuffers b, Geometry g) 
                     LoadAux & 0xFF);
             } else {
                 r.gu[k] = load128<LoadAux>(rgu, j * 16);
-                r.gy[k] = load128<LoadAux>(rgy, j * 16);
+                if constexpr (C::kNorm16) {
+                    r.gy16[k] = load64<LoadAux>(rgy, j * 8);
+                } else {
+                    r.gy[k] = load128<LoadAux>(rgy, j * 16);
+                }
                 r.u[k] = load128<LoadAux>(ru, j * 16);
             }
-            r.word[k] = load32<0>(rm, (j / 8) * 4);
+            r.word[k] = C::kMask ? load32<0>(rm, (j / 8) * 4) : 1u;
             const uint32_t row = j / g.row_units;
             r.mean[k] = __builtin_bit_cast(float, load32<0>(rmean, row * 4));
             r.rstd[k] = __builtin_bit_cast(float, load32<0>(rrstd, row * 4));
@@ -282,7 +314,11 @@ __global__ __launch_bounds__(T) void probe_backward(ProbeBuffers b, Geometry g) 
                 u = stage[wave][buffer][3 * k + 2][lane];
             } else {
                 gu = r.gu[k];
-                gy = r.gy[k];
+                if constexpr (C::kNorm16) {
+                    gy = widen(r.gy16[k]);
+                } else {
+                    gy = r.gy[k];
+                }
                 u = r.u[k];
             }
             grad[k] = (gu + gy * (u - r.mean[k] * r.rstd[k]))
@@ -292,7 +328,9 @@ __global__ __launch_bounds__(T) void probe_backward(ProbeBuffers b, Geometry g) 
         for (int k = 0; k < U; ++k) {
             const uint32_t j = unit_of<T, U, Wide>(base, k);
             store128<StoreAux>(rgx, j * 16, grad[k]);
-            if constexpr (Wide) {
+            if constexpr (C::kBranch32) {
+                store128<StoreAux>(rgb, j * 16, grad[k]);
+            } else if constexpr (Wide) {
                 if ((k & 1) == 0) {
                     const u32x2 lo = narrow(grad[k]);
                     const u32x2 hi = narrow(grad[k + 1]);
@@ -323,8 +361,9 @@ __global__ __launch_bounds__(T) void probe_backward(ProbeBuffers b, Geometry g) 
             Regs next;
             load(next, base + stride, buffer ^ 1);
             if constexpr (kViaLds) {
-                // The next step's 6U loads may stay in flight.
-                wait_vm(std::integral_constant<int, 6 * U>{});
+                // The next step's loads (six per unit, five without the
+                // mask) may stay in flight.
+                wait_vm(std::integral_constant<int, (C::kMask ? 6 : 5) * U>{});
             }
             process(current, base, buffer);
             current = next;
@@ -391,14 +430,38 @@ struct Variant {
     int threads;
     int units_per_lane;
     void (*kernel)(ProbeBuffers, Geometry);
+    int config;  // the Cfg bits of its streams
 };
 
 #define PROBE_F(T, U, L, S, A, W)                                                      \
     {"fwd t" #T " u" #U " ld" #L " st" #S " ahead" #A " wide" #W, kForward, T, U,      \
-     &probe_forward<T, U, L, S, A, W>},
+     &probe_forward<T, U, L, S, A, W, 0>, 0},
 #define PROBE_B(T, U, L, S, A, W)                                                      \
     {"bwd t" #T " u" #U " ld" #L " st" #S " ahead" #A " wide" #W, kBackward, T, U,     \
-     &probe_backward<T, U, L, S, A, W>},
+     &probe_backward<T, U, L, S, A, W, 0>, 0},
+// Variants of the other stream configurations: the name carries the
+// configuration ("b32": fp32 branch, "n16": 16-bit normalized, "nomask").
+#define PROBE_FC(T, U, L, S, A, W, C, SUFFIX)                                          \
+    {"fwd t" #T " u" #U " ld" #L " st" #S " ahead" #A " wide" #W SUFFIX, kForward, T, U, \
+     &probe_forward<T, U, L, S, A, W, C>, C},
+#define PROBE_BC(T, U, L, S, A, W, C, SUFFIX)                                          \
+    {"bwd t" #T " u" #U " ld" #L " st" #S " ahead" #A " wide" #W SUFFIX, kBackward, T, U, \
+     &probe_backward<T, U, L, S, A, W, C>, C},
+// Per other stream configuration: one to four units, with and without
+// look-ahead, at 256, 512 and 1024 threads, sc0 | sc1 stores; two shapes
+// with non-temporal stores.
+#define PROBE_CONFIG_SHAPES_T(X, T, C, SUFFIX)                                         \
+    X(T, 1, 2, 17, 0, 0, C, SUFFIX) X(T, 1, 2, 17, 1, 0, C, SUFFIX)                    \
+    X(T, 2, 2, 17, 0, 0, C, SUFFIX) X(T, 2, 2, 17, 1, 0, C, SUFFIX)                    \
+    X(T, 4, 2, 17, 0, 0, C, SUFFIX) X(T, 4, 2, 17, 1, 0, C, SUFFIX)
+#define PROBE_CONFIG_SHAPES(X, C, SUFFIX)                                              \
+    PROBE_CONFIG_SHAPES_T(X, 256, C, SUFFIX) PROBE_CONFIG_SHAPES_T(X, 512, C, SUFFIX)  \
+    PROBE_CONFIG_SHAPES_T(X, 1024, C, SUFFIX)                                          \
+    X(256, 2, 2, 2, 1, 0, C, SUFFIX) X(256, 1, 2, 2, 0, 0, C, SUFFIX)
+// The backward's LDS-staged loads where grad_normalized is fp32.
+#define PROBE_CONFIG_LDS(C, SUFFIX)                                                    \
+    PROBE_BC(256, 1, 258, 17, 0, 0, C, SUFFIX) PROBE_BC(256, 1, 258, 17, 1, 0, C, SUFFIX) \
+    PROBE_BC(512, 1, 258, 17, 0, 0, C, SUFFIX)
 // Shapes with non-temporal loads and sc0 | sc1 stores (the operator's policy).
 #define PROBE_SHAPES(X, T)                                                             \
     X(T, 1, 2, 17, 0, 0) X(T, 1, 2, 17, 1, 0) X(T, 2, 2, 17, 0, 0) X(T, 2, 2, 17, 1, 0)    \
@@ -413,7 +476,7 @@ struct Variant {
     X(256, 2, 0, 18, 1, 0) X(256, 2, 16, 17, 1, 0)
 
 const Variant kVariants[] = {
-    {"empty t256", kEmpty, 256, 1, &probe_empty},
+    {"empty t256", kEmpty, 256, 1, &probe_empty, 0},
     PROBE_SHAPES(PROBE_F, 256) PROBE_SHAPES(PROBE_F, 512) PROBE_SHAPES(PROBE_F, 1024)
     PROBE_POLICIES(PROBE_F)
     PROBE_SHAPES(PROBE_B, 256) PROBE_SHAPES(PROBE_B, 512) PROBE_SHAPES(PROBE_B, 1024)
@@ -422,6 +485,14 @@ const Variant kVariants[] = {
     PROBE_B(256, 1, 258, 17, 0, 0) PROBE_B(256, 1, 258, 17, 1, 0)
     PROBE_B(256, 2, 258, 17, 0, 0) PROBE_B(256, 2, 258, 17, 1, 0)
     PROBE_B(512, 1, 258, 17, 0, 0) PROBE_B(512, 1, 258, 17, 1, 0)
+    // fp32 branch with a mask (the C4 tail at p > 0), fp32 branch without a
+    // mask (C0, the C4 tail at p = 0), 16-bit normalized with a mask (the
+    // bf16-out configurations).
+    PROBE_CONFIG_SHAPES(PROBE_FC, 1, " b32") PROBE_CONFIG_SHAPES(PROBE_BC, 1, " b32")
+    PROBE_CONFIG_LDS(1, " b32")
+    PROBE_CONFIG_SHAPES(PROBE_FC, 5, " b32 nomask") PROBE_CONFIG_SHAPES(PROBE_BC, 5, " b32 nomask")
+    PROBE_CONFIG_LDS(5, " b32 nomask")
+    PROBE_CONFIG_SHAPES(PROBE_FC, 2, " n16") PROBE_CONFIG_SHAPES(PROBE_BC, 2, " n16")
 };
 
 constexpr int kVariantCount = sizeof(kVariants) / sizeof(kVariants[0]);
@@ -444,6 +515,12 @@ int rln_probe_variant_kind(int index) {
 int rln_probe_variant_threads(int index) {
     return index >= 0 && index < kVariantCount ? kVariants[index].threads : -1;
 }
+// Stream configuration of variant `index` (bit 0: fp32 branch and
+// grad_branch, else 16-bit; bit 1: 16-bit normalized and grad_normalized,
+// else fp32; bit 2: no mask); -1 out of range.
+int rln_probe_variant_config(int index) {
+    return index >= 0 && index < kVariantCount ? kVariants[index].config : -1;
+}
 
 // Blocks that give every thread one step of variant `index` over
 // [rows, hidden]; 0 for bad arguments.
@@ -462,15 +539,30 @@ int64_t rln_probe_one_step_blocks(int index, int64_t rows, int64_t hidden) {
 // backward's streams, in the order x, branch, updated (forward output),
 // normalized, mask (forward output), mean (forward output), rstd (forward
 // output), grad_updated, grad_normalized, updated, mask, mean, rstd,
-// grad_x, grad_branch; a pass reads and writes only its own. Returns 0, 1
-// for bad arguments (the tensor over 2^31 bytes included) or 3 for a
-// launch error.
+// grad_x, grad_branch; a pass reads and writes only its own (the other
+// pass's, and the masks of a configuration without one, may be NULL).
+// Returns 0, 1 for bad arguments (the tensor over 2^31 bytes and a NULL
+// buffer the pass uses included) or 3 for a launch error.
 int rln_probe_launch(int index, const void* const* buffers, int64_t rows, int64_t hidden,
                      int64_t blocks, void* stream) {
     if (index < 0 || index >= kVariantCount || buffers == nullptr || rows <= 0 || hidden <= 0
         || hidden % 32 != 0 || rows * hidden * 4 > (int64_t{1} << 31) || blocks <= 0
         || blocks > (int64_t{1} << 20)) {
         return 1;
+    }
+    const bool masked = (kVariants[index].config & 4) == 0;
+    if (kVariants[index].kind == kForward) {
+        for (int i = 0; i < 7; ++i) {
+            if (buffers[i] == nullptr && (i != 4 || masked)) {
+                return 1;
+            }
+        }
+    } else if (kVariants[index].kind == kBackward) {
+        for (int i = 7; i < 15; ++i) {
+            if (buffers[i] == nullptr && (i != 10 || masked)) {
+                return 1;
+            }
+        }
     }
     ProbeBuffers b;
     b.x = static_cast<const float*>(buffers[0]);

@@ -76,7 +76,7 @@
 #define RLN_FWD_LARGE_ELEMENTS (1ll << 23)
 #endif
 #ifndef RLN_FWD_LARGE_MAX_BLOCKS
-#define RLN_FWD_LARGE_MAX_BLOCKS 24576
+#define RLN_FWD_LARGE_MAX_BLOCKS 65536
 #endif
 // Forward launches of multi-wave rows below these sizes (elements; the first
 // for rows of two or four waves, the second for eight) run a persistent grid
@@ -187,6 +187,12 @@
 #endif
 #ifndef RLN_WRITE_THROUGH_ELEMENTS
 #define RLN_WRITE_THROUGH_ELEMENTS (1ll << 23)
+#endif
+#ifndef RLN_FWD_WRITE_THROUGH_ELEMENTS
+#define RLN_FWD_WRITE_THROUGH_ELEMENTS RLN_WRITE_THROUGH_ELEMENTS
+#endif
+#ifndef RLN_BWD_WRITE_THROUGH_ELEMENTS
+#define RLN_BWD_WRITE_THROUGH_ELEMENTS RLN_WRITE_THROUGH_ELEMENTS
 #endif
 
 namespace rln {
@@ -467,10 +473,16 @@ inline int backward_paced(int64_t rows, int64_t hidden) {
 // one round was 7 % slower, and [8192, 768] at four blocks per CU runs its
 // forward 0.4 us faster but the forward + backward step 0.3 us slower.
 // Large launches (2^23 elements and up) instead run one row step per
-// team (two for eight-wave rows), up to 24576 blocks, again a whole number per
+// team (two for eight-wave rows), up to 65536 blocks, again a whole number per
 // CU: the hardware keeps as many of them resident as registers allow and
 // starts the next as one ends, which streams faster than fewer teams walking
-// many rows. Measured at 262144 rows (forward, us, the small-launch grid
+// many rows. A cap of 65536 instead of 24576 blocks, so that 262144 rows of
+// one wave take one step each: forward 660 -> 614 us at [262144, 1024], 499
+// -> 487 at [262144, 768] (bf16 out 396 -> 385), 324 -> 307 at [209715,
+// 640], 324 -> 311 at [104857, 1280], 330 -> 320 at [83886, 1600]; the same
+// at [262144, 384] and at rows of 2048 and 4096 columns (bench.py --ab
+// fwd64k=RLN_FWD_LARGE_MAX_BLOCKS=65536, three alternated rounds). Measured
+// at 262144 rows (forward, us, the small-launch grid
 // against one step per team, alternated in one run where marked *): H = 128
 // 99 -> 92, 256 179 -> 159, 384 258 -> 238, 512 352 -> 317, 768 541-550 ->
 // 491-495 *, 1024 681-758 -> 652-653 *; [65536, 1024] 166-169 -> 159 *,
@@ -714,7 +726,8 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // The descriptor's fourth word for a raw (untyped, unswizzled) buffer.
 constexpr int kRawBufferWord3 = 0x00020000;
-constexpr int64_t kWriteThroughElements = RLN_WRITE_THROUGH_ELEMENTS;
+constexpr int64_t kForwardWriteThroughElements = RLN_FWD_WRITE_THROUGH_ELEMENTS;
+constexpr int64_t kBackwardWriteThroughElements = RLN_BWD_WRITE_THROUGH_ELEMENTS;
 
 // `value` of the wave's first active lane, in scalar registers.
 __device__ __forceinline__ int64_t wave_uniform(int64_t value) {
@@ -2026,7 +2039,7 @@ int launch_forward_walk(const ForwardArgs& a, S shape) {
         a.threshold,
         a.philox,
         forward_paced(a.rows, shape.hidden()),
-        a.rows * shape.hidden() < kWriteThroughElements ? 1 : 0);
+        a.rows * shape.hidden() < kForwardWriteThroughElements ? 1 : 0);
     return check_launch("rln_forward_kernel");
 }
 
@@ -2058,7 +2071,7 @@ int launch_backward(const BackwardArgs& a, S shape) {
         a.flags,
         a.scale,
         backward_paced(a.rows, shape.hidden()),
-        a.rows * shape.hidden() < kWriteThroughElements ? 1 : 0);
+        a.rows * shape.hidden() < kBackwardWriteThroughElements ? 1 : 0);
     return check_launch("rln_backward_kernel");
 }
 

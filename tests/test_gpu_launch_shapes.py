@@ -2,7 +2,7 @@
 
 Forward launches of one-wave rows below 2^23 elements run 2-5 blocks per CU
 whose teams walk several rows (2^24 for the four-slot rows of 512 and 1024
-columns); above, one row step per team on up to 24576 blocks, rounded down to
+columns); above, one row step per team on up to 65536 blocks, rounded down to
 a whole number of blocks per CU, so that some teams take one step more.
 Multi-wave rows run a persistent grid of eight waves
 per CU (one block per row step when there are fewer) below 2^24 elements, or
