@@ -1213,11 +1213,16 @@ def probe_library():
                                                  ctypes.c_void_p]
     library.rln_probe_atomic_policy.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
                                                 ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
+    library.rln_probe_atomic_fold.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                              ctypes.c_int64, ctypes.c_int, ctypes.c_int64,
+                                              ctypes.c_int, ctypes.c_void_p]
     return library
 
 
 # Copies of the weight/bias sums the atomic-combine probe spreads 256 blocks over.
 PROBE_ATOMIC_COPIES = (1, 2, 4, 8, 16, 64, 256)
+# Copies of the in-launch fold combine.
+PROBE_FOLD_COPIES = (1, 2, 4, 8, 16)
 PROBE_EMPTY_BLOCKS = (1, 256, 768, 2048, 3072)
 
 
@@ -1226,8 +1231,10 @@ def probe_fixed_costs(torch, runner: "Runner", library, hidden: int, repeats: in
     back by a C loop (microseconds per launch): the weight/bias combine alone
     (256 blocks of 512 threads adding 2 x hidden fp32 values each with
     atomics, spread over 1..256 copies of the sums, consecutive blocks in
-    different copies or in the same one), and an empty kernel of 1..3072
-    blocks of 256 threads (a launch's own cost on the GPU)."""
+    different copies or in the same one; by the atomics' cache policy; and
+    folded inside the launch - copies, agent-scope release fences, a ticket,
+    the last block swapping the copies into the output), and an empty kernel
+    of 1..3072 blocks of 256 threads (a launch's own cost on the GPU)."""
     handle = ctypes.c_void_p(runner.handle)
     sums = torch.zeros(max(PROBE_ATOMIC_COPIES) * 2 * hidden, device="cuda")
     atomic = {}
@@ -1253,6 +1260,26 @@ def probe_fixed_costs(torch, runner: "Runner", library, hidden: int, repeats: in
         exact = bool(torch.all(one == float(256 * repeats)).item())
         policies[label] = {"us": round(us, 3), "sums_exact": exact}
     atomic["one copy, buffer atomics by cache policy"] = policies
+    # The fold inside one launch: adds into copies, release fence, ticket; the
+    # last block swaps the copies for zeros and adds their total into the
+    # output. After the launches every output value must be 256 * repeats and
+    # every copy zero.
+    fold = {}
+    for copies in PROBE_FOLD_COPIES:
+        copy_sums = torch.zeros(copies * 2 * hidden, device="cuda")
+        out = torch.zeros(2 * hidden, device="cuda")
+        counter = torch.zeros(1, device="cuda", dtype=torch.int32)
+
+        def batch(_, copies=copies, copy_sums=copy_sums, out=out, counter=counter):
+            if library.rln_probe_atomic_fold(copy_sums.data_ptr(), out.data_ptr(),
+                                             counter.data_ptr(), hidden, copies, 256, repeats,
+                                             handle):
+                raise RuntimeError("rln_probe_atomic_fold failed")
+        us = runner.timed(batch, 1) * 1e3 / repeats
+        exact = bool(torch.all(out == float(256 * repeats)).item()
+                     and torch.all(copy_sums == 0).item() and int(counter.item()) == 0)
+        fold[str(copies)] = {"us": round(us, 3), "sums_exact": exact}
+    atomic["fold in the launch, by copies"] = fold
     empty = {}
     for blocks in PROBE_EMPTY_BLOCKS:
         def batch(_, blocks=blocks):

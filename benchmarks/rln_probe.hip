@@ -419,6 +419,61 @@ __global__ __launch_bounds__(512) void probe_atomic_policy(float* sums, int hidd
     }
 }
 
+// The combine as a fold inside one launch: each 512-thread block adds its
+// 2 x hidden values (1.0 each) with fp32 atomics into copy blockIdx % copies
+// of `sums` ([copies, 2, hidden]), makes them visible at agent scope
+// (release fence by every wave, then a block barrier) and takes a ticket
+// from `counter`; the block that takes the last ticket (acquire fence) swaps
+// every copy's values for zeros, adds their total into `out` ([2, hidden])
+// and resets the counter, so that `sums` and `counter` are zero again for
+// the next launch. After n launches of g blocks, out holds g * n per value.
+constexpr int kFoldCopies = 16;
+
+__global__ __launch_bounds__(512) void probe_atomic_fold(float* sums, float* out,
+                                                         uint32_t* counter, int hidden,
+                                                         int copies) {
+    const int copy = static_cast<int>(blockIdx.x % copies);
+    float* target = sums + static_cast<int64_t>(copy) * 2 * hidden;
+    for (int entry = threadIdx.x; entry < 2 * hidden; entry += 512) {
+        const int owner = entry / 8;
+        const int which = (entry / 4) & 1;
+        const int column = owner * 4 + (entry & 3);
+        unsafeAtomicAdd(target + which * hidden + column, 1.0f);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __shared__ uint32_t ticket;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        ticket = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (ticket != gridDim.x - 1) {
+        return;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    // Every swap of a column is issued before any is waited for (at most
+    // kFoldCopies copies).
+    for (int i = threadIdx.x; i < 2 * hidden; i += 512) {
+        float values[kFoldCopies];
+#pragma unroll
+        for (int k = 0; k < kFoldCopies; ++k) {
+            values[k] = k < copies
+                ? __hip_atomic_exchange(sums + static_cast<int64_t>(k) * 2 * hidden + i, 0.0f,
+                                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                : 0.0f;
+        }
+        float total = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kFoldCopies; ++k) {
+            total += values[k];
+        }
+        unsafeAtomicAdd(out + i, total);
+    }
+    if (threadIdx.x == 0) {
+        __hip_atomic_exchange(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 // A kernel of `blocks` blocks doing nothing, for the per-launch cost.
 __global__ void probe_nothing(int) {}
 
@@ -626,6 +681,26 @@ int rln_probe_atomic_policy(float* sums, int64_t hidden, int policy, int64_t blo
             case 18: probe_atomic_policy<18><<<grid, 512, 0, s>>>(sums, static_cast<int>(hidden)); break;
             default: return 1;
         }
+    }
+    return hipGetLastError() == hipSuccess ? 0 : 3;
+}
+
+// `repeats` launches of the in-launch fold combine over `sums` ([copies, 2,
+// hidden] floats, zero), `out` ([2, hidden] floats) and `counter` (one
+// uint32, zero) with `blocks` blocks, back to back on `stream`; sums and
+// counter are zero again after each launch, and out gains blocks per value;
+// at most 16 copies.
+int rln_probe_atomic_fold(float* sums, float* out, uint32_t* counter, int64_t hidden,
+                          int copies, int64_t blocks, int repeats, void* stream) {
+    if (sums == nullptr || out == nullptr || counter == nullptr || hidden <= 0 || hidden > 8192
+        || hidden % 32 != 0 || copies <= 0 || copies > kFoldCopies || blocks <= 0
+        || blocks > 65536 || repeats <= 0) {
+        return 1;
+    }
+    for (int i = 0; i < repeats; ++i) {
+        probe_atomic_fold<<<dim3(static_cast<unsigned>(blocks)), dim3(512), 0,
+                            static_cast<hipStream_t>(stream)>>>(
+            sums, out, counter, static_cast<int>(hidden), copies);
     }
     return hipGetLastError() == hipSuccess ? 0 : 3;
 }
