@@ -388,7 +388,10 @@ inline bool backward_runs_wide(int64_t hidden, int64_t rows) {
 // against 424-436 us, [18724, 7168] 425-427 against 437-441 us, [8192, 8192]
 // 209 against 212-214 us, alternated in one run), and 1-4.5 % slower at
 // 2^24-2^25; equal at 6656 columns.
-constexpr int64_t kSixteenWaveBackwardElements = 1ll << 26;
+#ifndef RLN_BWD_SIXTEEN_WAVE_ELEMENTS
+#define RLN_BWD_SIXTEEN_WAVE_ELEMENTS (1ll << 26)
+#endif
+constexpr int64_t kSixteenWaveBackwardElements = RLN_BWD_SIXTEEN_WAVE_ELEMENTS;
 constexpr int64_t kSixteenWaveBackwardMinHidden = 6657;
 
 // The shape of a supported hidden size in one pass over `rows`.
