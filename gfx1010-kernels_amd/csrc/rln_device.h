@@ -194,6 +194,13 @@
 #ifndef RLN_BWD_WRITE_THROUGH_ELEMENTS
 #define RLN_BWD_WRITE_THROUGH_ELEMENTS RLN_WRITE_THROUGH_ELEMENTS
 #endif
+// 1: the backward of rows of four waves of one slot (769-1024 columns) writes
+// through at every size. Measured on MI355X (bench.py --ab, five alternated
+// rounds): step -0.7 % at [262144, 1024], +2 % at C3 [65536, 1024], +1 % at
+// [262144, 1024] p = 0.1; so 0.
+#ifndef RLN_BWD_WIDE14_WRITE_THROUGH
+#define RLN_BWD_WIDE14_WRITE_THROUGH 0
+#endif
 
 namespace rln {
 
@@ -2074,7 +2081,11 @@ int launch_backward(const BackwardArgs& a, S shape) {
         a.flags,
         a.scale,
         backward_paced(a.rows, shape.hidden()),
-        a.rows * shape.hidden() < kBackwardWriteThroughElements ? 1 : 0);
+        a.rows * shape.hidden() < kBackwardWriteThroughElements
+                || (RLN_BWD_WIDE14_WRITE_THROUGH && S::kHidden == 0 && S::kParts == 4
+                    && S::kV == 1)
+            ? 1
+            : 0);
     return check_launch("rln_backward_kernel");
 }
 
