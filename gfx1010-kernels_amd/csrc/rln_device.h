@@ -254,8 +254,14 @@ constexpr int64_t kHiddenMultiple = 64;
 // Lanes per row of a specialized hidden size in the backward, and in the
 // shape the C ABI dispatches on: a whole wave when H/4 is a multiple of 64,
 // else half a wave.
+// Lanes per row of the 128-column backward: 32 (default) or 16. Measured on
+// MI355X (bench.py --ab, four alternated rounds): [262144, 128] step 180.5
+// us at 32 lanes against 180.9 us at 16 (184.6 us with two rows ahead).
+#ifndef RLN_FIXED_LANES_128
+#define RLN_FIXED_LANES_128 32
+#endif
 constexpr int fixed_lanes(int64_t hidden) {
-    return ((hidden / 4) % kWaveSize == 0) ? 64 : 32;
+    return hidden == 128 ? RLN_FIXED_LANES_128 : ((hidden / 4) % kWaveSize == 0) ? 64 : 32;
 }
 
 // Lanes per row in the forward, whose normalized output has type N: fewer
