@@ -240,6 +240,9 @@ def parse_args():
                              "size, forward and train, fused vs torch) at B=1, T=1024/2048/4096")
     parser.add_argument("--ceiling", action="store_true",
                         help="add op-vs-streaming-ceiling lines per configuration")
+    parser.add_argument("--alternation", action="store_true",
+                        help="only time C1's forward and backward alternating with each other "
+                             "and with the streaming probe's passes (one JSON line)")
     parser.add_argument("--quick", action="store_true",
                         help="C1 line only (with --sweep or --config: those lines), kernels "
                              "launched only as the step launches them (no input-grads-only "
@@ -1601,6 +1604,11 @@ def main() -> int:
         chosen = [workload for workload in sweep_workloads() if workload.name in args.config]
         return run_ab(torch, _cabi, stream, args, chosen or [C1])
 
+    if args.alternation:
+        with torch.cuda.stream(stream):
+            print(json.dumps(alternation_study(torch, library, _cabi, stream)), flush=True)
+        return 0
+
     if args.config:
         chosen = [workload for workload in sweep_workloads() if workload.name in args.config]
         if args.ceiling:
@@ -1690,6 +1698,79 @@ def main() -> int:
     if args.ceiling:
         run_ceilings(torch, library, _cabi, stream, args, sweep_workloads())
     return 0
+
+
+# The probe variants and grids the alternation study pairs with the op: the
+# fastest C1 forward and backward of the probe tables measured so far.
+ALTERNATION_PROBES = (("fwd t512 u1 ld2 st17 ahead0 wide0", 256),
+                      ("bwd t256 u4 ld2 st17 ahead1 wide0", 1024))
+
+
+def alternation_study(torch, library, cabi, stream, launches: int = 400) -> dict:
+    """How a C1 pass's time depends on the kernel before it: the op's forward
+    and backward and the streaming probe's C1-shaped forward and backward
+    (ALTERNATION_PROBES), alone and in alternating pairs, and the op's forward
+    after the op's backward with a 64-row launch of the same forward between
+    them (the forward's code then warm). Each sequence runs 12 untimed
+    iterations, then `launches` timed ones between two events on the launch
+    stream; microseconds per iteration, and for each pair the excess over its
+    two members timed alone."""
+    import dataclasses
+
+    runner = Runner(torch, library, cabi, C1, 4, stream)
+    if not parity_self_check(torch, runner)["pass"]:
+        raise SystemExit("bench.py: the timed path misses the parity bars")
+    tiny = Runner(torch, library, cabi, dataclasses.replace(C1, name="C1 64 rows", rows=64), 4,
+                  stream)
+    probe = probe_library()
+    names = {probe.rln_probe_variant_name(i).decode(): i
+             for i in range(probe.rln_probe_variant_count())}
+    arrays = []
+    for t in runner.sets:
+        tensors = (t["x"], t["branch"], t["updated"], t["normalized"], t["mask"], t["mean"],
+                   t["rstd"], t["grad_updated"], t["grad_normalized"], t["updated"], t["mask"],
+                   t["mean"], t["rstd"], t["grad_x"], t["grad_branch"])
+        arrays.append((ctypes.c_void_p * len(tensors))(*[x.data_ptr() for x in tensors]))
+    handle = ctypes.c_void_p(runner.handle)
+    rows, hidden = ctypes.c_int64(C1.rows), ctypes.c_int64(C1.hidden)
+
+    def probe_pass(name, blocks):
+        index, count = names[name], ctypes.c_int64(blocks)
+
+        def launch(step):
+            if probe.rln_probe_launch(index, arrays[step % len(arrays)], rows, hidden, count,
+                                      handle):
+                raise RuntimeError(f"rln_probe_launch({name}) failed")
+        return launch
+
+    passes = {"op_fwd": runner.forward, "op_bwd": runner.backward,
+              "probe_fwd": probe_pass(*ALTERNATION_PROBES[0]),
+              "probe_bwd": probe_pass(*ALTERNATION_PROBES[1]), "op_fwd_64_rows": tiny.forward}
+    sequences = [("op_fwd",), ("op_bwd",), ("probe_fwd",), ("probe_bwd",), ("op_fwd_64_rows",),
+                 ("op_fwd", "op_bwd"), ("op_fwd", "probe_bwd"), ("probe_fwd", "op_bwd"),
+                 ("probe_fwd", "probe_bwd"), ("op_bwd", "op_fwd_64_rows"),
+                 ("op_bwd", "op_fwd_64_rows", "op_fwd")]
+    timed = {}
+    for sequence in sequences:
+        def body(step, sequence=sequence):
+            for name in sequence:
+                passes[name](step)
+        for step in range(12):
+            body(step)
+        timed[" + ".join(sequence)] = round(runner.timed(body, launches) * 1e3, 3)
+    excess = {}
+    for key, us in timed.items():
+        parts = key.split(" + ")
+        if len(parts) == 2 and all(part in timed for part in parts):
+            excess[key] = round(us - sum(timed[part] for part in parts), 3)
+    after_warm = round(timed["op_bwd + op_fwd_64_rows + op_fwd"]
+                       - timed["op_bwd + op_fwd_64_rows"], 3)
+    return {"kind": "alternation", "workload": C1.describe(), "us_per_iteration": timed,
+            "pair_excess_us": excess,
+            "op_fwd_after_op_bwd_and_a_64_row_forward_us": after_warm,
+            "probe_passes": {"fwd": list(ALTERNATION_PROBES[0]),
+                             "bwd": list(ALTERNATION_PROBES[1])},
+            "launches": launches}
 
 
 def run_ceilings(torch, library, cabi, stream, args, workloads) -> None:

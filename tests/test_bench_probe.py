@@ -99,3 +99,17 @@ def test_launch_refuses_missing_buffers_without_launching():
                                     ctypes.c_int64(64), ctypes.c_int64(100), blocks, None) == 1
     assert library.rln_probe_launch(-1, (ctypes.c_void_p * 15)(*([fake] * 15)), rows, hidden,
                                     blocks, None) == 1
+
+
+def test_alternation_study_names_existing_probe_passes():
+    """bench.py --alternation pairs the op with two probe variants by name;
+    both must be variants of the headline stream configuration."""
+    bench = _bench()
+    library = _library(bench)
+    by_name = {library.rln_probe_variant_name(i).decode(): i
+               for i in range(library.rln_probe_variant_count())}
+    for (name, blocks), kind in zip(bench.ALTERNATION_PROBES, (0, 1)):
+        assert name in by_name, name
+        assert library.rln_probe_variant_kind(by_name[name]) == kind
+        assert library.rln_probe_variant_config(by_name[name]) == 0
+        assert blocks > 0
