@@ -1018,14 +1018,15 @@ def mangled_kernel_name(name: str) -> str:
     __bf16 arguments mangled, so counter csv rows are matched on this too."""
     import re
 
-    match = re.fullmatch(r"rln::(\w+)<rln::(\w+)<(\d+), (\d+)>, ([\w ]+), ([\w ]+), "
+    match = re.fullmatch(r"rln::(\w+)<rln::(\w+)<(\d+)(?:, (\d+))?>, ([\w ]+), ([\w ]+), "
                          r"(true|false)(?:, (true|false))?>", name)
     if match is None:
         raise ValueError(f"not a kernel_name() instance: {name}")
     kernel, shape, first, second, branch, normalized, aligned, ring = match.groups()
     types = {"float": "f", "_Float16": "DF16_", "__bf16": "DF16b"}
     flags = f"Lb{int(aligned == 'true')}E" + (f"Lb{int(ring == 'true')}E" if ring else "")
-    return (f"_ZN3rln{len(kernel)}{kernel}INS_{len(shape)}{shape}ILi{first}ELi{second}EEE"
+    shape_args = f"ILi{first}E" + (f"Li{second}E" if second is not None else "")
+    return (f"_ZN3rln{len(kernel)}{kernel}INS_{len(shape)}{shape}{shape_args}EE"
             f"{types[branch]}{types[normalized]}{flags}EE")
 
 
@@ -1458,7 +1459,9 @@ def kernel_name(kernel: str, workload: Workload) -> str:
     forward = kernel == "rln_forward_kernel"
     hidden = workload.hidden
     runs_wide = hidden == 1024 or (hidden == 768 and workload.rows >= 65536)
-    if hidden in SPECIALIZED_HIDDEN and (forward or not runs_wide):
+    if not forward and backward_twelve_waves(hidden, workload.rows):
+        shape = f"rln::TwelveWaveShape<{hidden}>"
+    elif hidden in SPECIALIZED_HIDDEN and (forward or not runs_wide):
         lanes = 64 if (hidden // 4) % 64 == 0 else 32
         if forward:
             lanes = {128: 16, 768: 64, 1024: 64}.get(hidden, 32)
@@ -1471,6 +1474,17 @@ def kernel_name(kernel: str, workload: Workload) -> str:
     ring = ", true" if forward_ring(workload.rows, hidden) else ", false"
     return (f"rln::{kernel}<{shape}, {types[workload.branch]}, "
             f"{types[workload.normalized]}, true{ring if forward else ''}>")
+
+
+def backward_twelve_waves(hidden: int, rows: int) -> bool:
+    """Whether the backward runs twelve-wave blocks (rln_device.h
+    backward_twelve_waves): 768 columns over 2048-9216 rows whose last row
+    step keeps at least half of the 256 x 12 waves busy, or all of them."""
+    teams = 256 * 12
+    if hidden != 768 or rows < 2048 or rows > 3 * teams:
+        return False
+    last = rows % teams
+    return last == 0 or 2 * last >= teams
 
 
 def forward_ring(rows: int, hidden: int) -> bool:

@@ -290,6 +290,7 @@ struct FixedShape {
     static constexpr int kParts = 1;
     static constexpr int kRowsPerWave = kWaveSize / kLanes;
     static constexpr bool kRagged = false;
+    static constexpr bool kCopyWalk = false;  // look-ahead backward: ring (false) or copy walk
     static constexpr int kForwardThreads = 256;
     static constexpr int kBackwardBlockThreads = kBackwardThreads;
     static_assert(H % 64 == 0 && (H / 4) % kLanes == 0 && kLanes >= 16,
@@ -308,6 +309,7 @@ struct WideShape {
     static constexpr int kParts = P;
     static constexpr int kRowsPerWave = 1;
     static constexpr bool kRagged = true;
+    static constexpr bool kCopyWalk = false;
     // Three-wave rows (the backward of large 768-column launches) run in
     // 12-wave blocks and sixteen-wave rows (the backward of large launches of
     // 6657-8192 columns) in 16-wave blocks, so that a block still holds whole
@@ -320,6 +322,16 @@ struct WideShape {
     float inv_hidden_;  // 1.0f / hidden, rounded once on the host
     __host__ __device__ int64_t hidden() const { return hidden_; }
     __host__ __device__ float inv_hidden() const { return inv_hidden_; }
+};
+
+// The backward of a specialized size in twelve-wave blocks (one row per
+// wave, one block per CU) walking its rows with the copy walk: the ring walk
+// needs ~200 VGPRs at 768 columns and spills at the 168 a twelve-wave block
+// allows. Used for the launches backward_twelve_waves selects.
+template <int H>
+struct TwelveWaveShape : FixedShape<H> {
+    static constexpr int kBackwardBlockThreads = 12 * kWaveSize;
+    static constexpr bool kCopyWalk = true;
 };
 
 inline bool specialized_hidden(int64_t hidden) {
@@ -395,6 +407,33 @@ inline bool backward_runs_wide(int64_t hidden, int64_t rows) {
     return hidden == 1024 || (hidden == 768 && rows >= kWide768BackwardRows);
 }
 
+// The backward of 768 columns over 2048-9216 rows runs twelve-wave blocks
+// (TwelveWaveShape) when the last of its at most three row steps per wave
+// keeps at least half of the 256 x 12 waves busy, or all of them: then the
+// blocks whose waves have a step fewer finish earlier and add their
+// weight/bias sums while the others still stream, and the others' twelve
+// waves per CU keep the HBM busy meanwhile, so the adds at the end of the
+// kernel contend less (at C1 the time the sums add to the backward falls
+// from 3.5 to 1.6 us). With fewer rows busy in the last step, the few CUs
+// left streaming cannot keep the HBM busy. Measured on MI355X (fwd+bwd step,
+// us, eight-wave ring against twelve-wave copy walk, five alternated rounds):
+// 2048 rows 19.6 -> 17.9, 2560 23.2 -> 22.5, 5120 29.5 -> 29.1, 6144 32.8 ->
+// 32.6, 8192 40.0 -> 39.2 (C1; bf16 output 38.2 -> 36.8); and slower at 4096
+// (26.0 -> 26.7) and 7168 (34.3 -> 35.8), where a third of the waves is busy
+// in the last step, equal at 10240 and 12288, 1-3 % slower from 16384 rows.
+// RLN_BWD_TWELVE_WAVE_768=0 keeps the eight-wave ring everywhere.
+#ifndef RLN_BWD_TWELVE_WAVE_768
+#define RLN_BWD_TWELVE_WAVE_768 1
+#endif
+inline bool backward_twelve_waves(int64_t hidden, int64_t rows) {
+    constexpr int64_t kTeams = RLN_BWD_MAX_BLOCKS * 12;
+    if (!RLN_BWD_TWELVE_WAVE_768 || hidden != 768 || rows < 2048 || rows > 3 * kTeams) {
+        return false;
+    }
+    const int64_t last = rows % kTeams;
+    return last == 0 || 2 * last >= kTeams;
+}
+
 // Backward launches of at least this many elements run rows of 6657-8192
 // columns on sixteen waves of two slots (1024-thread blocks) instead of eight
 // of four: measured 2-4.5 % faster from 2^26 elements ([16384, 8192] 416
@@ -413,7 +452,8 @@ inline ShapeInfo shape_info(int64_t hidden, Pass pass, int64_t rows) {
         && !(pass == Pass::kBackward && backward_runs_wide(hidden, rows))) {
         const int lanes = fixed_lanes(hidden);
         return {kWaveSize / lanes, 1, static_cast<int>(hidden / 4 / lanes), 256,
-                kBackwardThreads};
+                pass == Pass::kBackward && backward_twelve_waves(hidden, rows) ? 12 * kWaveSize
+                                                                              : kBackwardThreads};
     }
     int parts = wide_parts(hidden, pass);
     if (pass == Pass::kBackward && parts == 8 && hidden >= kSixteenWaveBackwardMinHidden
@@ -1835,7 +1875,7 @@ void rln_backward_kernel(
                 load_row(ra, row_of(i + 1), true);
             }
             finish(ra, rb, i);
-        } else if constexpr (!RLN_BWD_RING || P > 1) {
+        } else if constexpr (!RLN_BWD_RING || P > 1 || S::kCopyWalk) {
             int64_t i = 0;
             for (; i + 1 < count; ++i) {
                 BackwardRow<V, GY> next;
@@ -2168,6 +2208,11 @@ int with_shape(int64_t hidden, int64_t rows, Launch&& launch) {
         case 384: return launch(FixedShape<384>{});
         case 512: return launch(FixedShape<512>{});
         case 768:
+            if constexpr (kPass == Pass::kBackward) {
+                if (backward_twelve_waves(hidden, rows)) {
+                    return launch(TwelveWaveShape<768>{});
+                }
+            }
             if (kPass == Pass::kForward || !backward_runs_wide(hidden, rows)) {
                 return launch(FixedShape<768>{});
             }
@@ -2205,6 +2250,9 @@ int with_shape(int64_t hidden, int64_t rows, Launch&& launch) {
         const ForwardArgs&, FixedShape<H>, int, int, bool);                               \
     extern template int launch_backward_shape<FixedShape<H>>(                            \
         const BackwardArgs&, FixedShape<H>, int, int, bool);
+#define RLN_DECLARE_TWELVE_WAVE_BACKWARD()                                                \
+    extern template int launch_backward_shape<TwelveWaveShape<768>>(                     \
+        const BackwardArgs&, TwelveWaveShape<768>, int, int, bool);
 #define RLN_DECLARE_WIDE_FORWARD(V, P)                                                    \
     extern template int launch_forward_shape<WideShape<V, P>>(                           \
         const ForwardArgs&, WideShape<V, P>, int, int, bool);

@@ -24,6 +24,10 @@ template int launch_forward_shape<RLN_SHAPE>(const ForwardArgs&, RLN_SHAPE, int,
 #endif
 #if RLN_PASSES & 2
 template int launch_backward_shape<RLN_SHAPE>(const BackwardArgs&, RLN_SHAPE, int, int, bool);
+#if defined(RLN_HIDDEN) && RLN_HIDDEN == 768
+template int launch_backward_shape<TwelveWaveShape<768>>(const BackwardArgs&,
+                                                         TwelveWaveShape<768>, int, int, bool);
+#endif
 #endif
 
 }  // namespace rln

@@ -88,7 +88,7 @@ def test_mask_decoding_matches_the_oracle_layout():
 
 
 # The two C1 kernels as rocprofv3's counter csv names them (mangled).
-MANGLED_BACKWARD = ("_ZN3rln19rln_backward_kernelINS_10FixedShapeILi768ELi64EEEDF16_fLb1EEEvPKfPKT1_"
+MANGLED_BACKWARD = ("_ZN3rln19rln_backward_kernelINS_15TwelveWaveShapeILi768EEEDF16_fLb1EEEvPKfPKT1_"
                     "S4_S4_S4_S4_PKjPfPT0_SA_SA_SA_lT_ifii")
 MANGLED_FORWARD = ("_ZN3rln18rln_forward_kernelINS_10FixedShapeILi768ELi64EEEDF16_fLb1ELb1EEEvPKfPKT0_"
                    "S4_S4_PfPT1_S8_S8_PjS8_S8_lT_fifjNS_10PhiloxArgsEii")

@@ -254,3 +254,48 @@ def test_sixteen_wave_backward_deterministic_and_half_gradient():
     check_full_tensor(inputs, grads, outputs, runs[0], 0.15, EPS, seed, offset,
                       what=f"{rows} x {hidden} deterministic")
     check_parameter_gradients(outputs[0], grads[1], runs[0])
+
+
+# Row counts of 768 columns around backward_twelve_waves (rln_device.h): the
+# backward runs twelve-wave blocks on the copy walk for 2048-9216 rows whose
+# last row step keeps at least half of the 256 x 12 waves busy (or all of
+# them), and the eight-wave ring otherwise.
+TWELVE_WAVE_CASES = [(2047, False), (2048, True), (4096, False), (5120, True), (7168, False),
+                     (8192, True), (9216, True), (9217, False)]
+
+
+@pytest.mark.parametrize("rows,twelve_waves", TWELVE_WAVE_CASES,
+                         ids=[f"{rows}-{'twelve' if twelve else 'eight'}"
+                              for rows, twelve in TWELVE_WAVE_CASES])
+def test_backward_twelve_wave_switch(rows, twelve_waves):
+    """Both sides of the switch between eight- and twelve-wave backward blocks
+    at 768 columns, whole tensors against the oracle; deterministic mode
+    replays bitwise, and its input gradients equal the atomic mode's."""
+    from test_gpu_backward import deterministic_algorithms
+
+    hidden = 768
+    teams = 256 * 12
+    last = rows % teams
+    assert (2048 <= rows <= 3 * teams and (last == 0 or 2 * last >= teams)) == twelve_waves
+    print(f"[launch shapes] backward rows={rows} H={hidden} twelve={twelve_waves}", flush=True)
+    inputs, grads = device_inputs(rows, hidden, torch.float16, seed=13 * hidden + rows)
+    torch.cuda.manual_seed(13 * hidden + rows)
+    seed, offset = generator_state()
+    outputs = _C.residual_layer_norm_forward(*inputs, 0.1, EPS, True, 128)
+
+    def backward():
+        return _C.residual_layer_norm_backward(
+            grads[0], grads[1], outputs[0], inputs[2], outputs[2], outputs[3], outputs[4], 0.1,
+            True, True, 128, 64, 64, 1, True, torch.float16)
+
+    with deterministic_algorithms(False):
+        atomic = backward()
+    check_full_tensor(inputs, grads, outputs, atomic, 0.1, EPS, seed, offset,
+                      what=f"{rows} x {hidden}")
+    check_parameter_gradients(outputs[0], grads[1], atomic)
+    with deterministic_algorithms(True):
+        first, second = backward(), backward()
+    for a, b in zip(first, second):
+        assert torch.equal(a, b)
+    assert torch.equal(first[0], atomic[0]) and torch.equal(first[1], atomic[1])
+    check_parameter_gradients(outputs[0], grads[1], first)
