@@ -84,7 +84,7 @@ import platform
 import statistics
 import sys
 import time
-from dataclasses import dataclass
+from dataclasses import dataclass, replace
 from pathlib import Path
 
 REPO = Path(__file__).resolve().parent
@@ -177,6 +177,21 @@ class Workload:
 C1 = Workload("C1", 8 * 1024, 768, "f16", 0.5, 0.1, seed=1001)
 
 
+def ab_row_workloads(args) -> list[Workload]:
+    """C1-shaped workloads at the --ab-rows row counts: the row sweeps that
+    decided row-count-dependent launch rules (the twelve-wave backward of 768
+    columns) are re-measured through them."""
+    rows = [int(value) for value in args.ab_rows.split(",") if value.strip()]
+    if any(value <= 0 for value in rows) or args.ab_hidden <= 0:
+        raise SystemExit("bench.py: --ab-rows and --ab-hidden take positive integers")
+    workloads = [replace(C1, name=f"[{value},{args.ab_hidden}]", rows=value,
+                         hidden=args.ab_hidden) for value in rows]
+    if args.ab_bf16:
+        workloads += [replace(workload, name=workload.name + " bf16-out", branch="bf16",
+                              normalized="bf16") for workload in workloads]
+    return workloads
+
+
 def sweep_workloads() -> list[Workload]:
     """The other BASELINE.json configurations."""
     workloads = [Workload("C0", 4 * 1024, 768, "f32", 1.0, 0.0, training=False,
@@ -261,6 +276,12 @@ def parse_args():
                         help="rounds of an A/B run (each times every build once)")
     parser.add_argument("--ab-build", action="store_true",
                         help="rebuild the --ab variants even where a build exists")
+    parser.add_argument("--ab-rows", default="", metavar="ROWS[,ROWS...]",
+                        help="A/B run on C1-shaped workloads (fp16 branch, p = 0.1) of these "
+                             "row counts instead of C1, at --ab-hidden columns; with "
+                             "--ab-bf16 also with a bf16 branch and output")
+    parser.add_argument("--ab-hidden", type=int, default=768)
+    parser.add_argument("--ab-bf16", action="store_true")
     parser.add_argument("--config", action="append", default=[], metavar="NAME",
                         help="run only this sweep configuration (repeatable; e.g. 'C2 H=1024'), "
                              "without the C1 line: one kernel's launches per run, for counters")
@@ -1616,7 +1637,8 @@ def main() -> int:
 
     if args.ab:
         chosen = [workload for workload in sweep_workloads() if workload.name in args.config]
-        return run_ab(torch, _cabi, stream, args, chosen or [C1])
+        return run_ab(torch, _cabi, stream, args, chosen + ab_row_workloads(args)
+                      or [C1])
 
     if args.alternation:
         with torch.cuda.stream(stream):
@@ -1729,13 +1751,10 @@ def alternation_study(torch, library, cabi, stream, launches: int = 400) -> dict
     iterations, then `launches` timed ones between two events on the launch
     stream; microseconds per iteration, and for each pair the excess over its
     two members timed alone."""
-    import dataclasses
-
     runner = Runner(torch, library, cabi, C1, 4, stream)
     if not parity_self_check(torch, runner)["pass"]:
         raise SystemExit("bench.py: the timed path misses the parity bars")
-    tiny = Runner(torch, library, cabi, dataclasses.replace(C1, name="C1 64 rows", rows=64), 4,
-                  stream)
+    tiny = Runner(torch, library, cabi, replace(C1, name="C1 64 rows", rows=64), 4, stream)
     probe = probe_library()
     names = {probe.rln_probe_variant_name(i).decode(): i
              for i in range(probe.rln_probe_variant_count())}

@@ -8,6 +8,8 @@ import subprocess
 import sys
 from pathlib import Path
 
+import pytest
+
 
 BENCH = Path(__file__).resolve().parents[1] / "bench.py"
 
@@ -152,3 +154,25 @@ def test_mangled_kernel_names_are_the_library_symbols():
         for kernel in kernels:
             prefix = bench.mangled_kernel_name(bench.kernel_name(kernel, workload))
             assert prefix in symbols, (workload.describe(), kernel, prefix)
+
+
+def test_ab_row_workloads_are_c1_shaped():
+    """bench.py --ab-rows re-measures row-count-dependent launch rules on
+    C1-shaped workloads: C1's branch, dropout and seed at other row counts."""
+    import argparse
+
+    bench = _bench_module()
+    args = argparse.Namespace(ab_rows="2048, 8192", ab_hidden=768, ab_bf16=True)
+    workloads = bench.ab_row_workloads(args)
+    assert [w.name for w in workloads] == ["[2048,768]", "[8192,768]", "[2048,768] bf16-out",
+                                           "[8192,768] bf16-out"]
+    assert [w.rows for w in workloads] == [2048, 8192, 2048, 8192]
+    for workload in workloads[:2]:
+        assert (workload.branch, workload.normalized) == (bench.C1.branch, bench.C1.normalized)
+        assert (workload.dropout_p, workload.seed, workload.hidden) == (0.1, bench.C1.seed, 768)
+    for workload in workloads[2:]:
+        assert (workload.branch, workload.normalized) == ("bf16", "bf16")
+    assert bench.ab_row_workloads(argparse.Namespace(ab_rows="", ab_hidden=768,
+                                                     ab_bf16=False)) == []
+    with pytest.raises(SystemExit):
+        bench.ab_row_workloads(argparse.Namespace(ab_rows="0", ab_hidden=768, ab_bf16=False))
