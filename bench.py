@@ -258,6 +258,9 @@ def parse_args():
     parser.add_argument("--alternation", action="store_true",
                         help="only time C1's forward and backward alternating with each other "
                              "and with the streaming probe's passes (one JSON line)")
+    parser.add_argument("--dwdb-placement", action="store_true",
+                        help="only time C1's backward with grad_weight and grad_bias placed "
+                             "at a range of distances from each other (one JSON line)")
     parser.add_argument("--quick", action="store_true",
                         help="C1 line only (with --sweep or --config: those lines), kernels "
                              "launched only as the step launches them (no input-grads-only "
@@ -1640,6 +1643,12 @@ def main() -> int:
         return run_ab(torch, _cabi, stream, args, chosen + ab_row_workloads(args)
                       or [C1])
 
+    if args.dwdb_placement:
+        with torch.cuda.stream(stream):
+            print(json.dumps(dwdb_placement_study(torch, library, cabi=_cabi, stream=stream)),
+                  flush=True)
+        return 0
+
     if args.alternation:
         with torch.cuda.stream(stream):
             print(json.dumps(alternation_study(torch, library, _cabi, stream)), flush=True)
@@ -1740,6 +1749,42 @@ def main() -> int:
 # fastest C1 forward and backward of the probe tables measured so far.
 ALTERNATION_PROBES = (("fwd t512 u1 ld2 st17 ahead0 wide0", 256),
                       ("bwd t256 u4 ld2 st17 ahead1 wide0", 1024))
+
+
+# Byte distances from grad_weight to grad_bias for --dwdb-placement: every
+# KiB from 3 to 128, then multiples of 128 KiB to 4 MiB.
+DWDB_OFFSETS = tuple(k * 1024 for k in range(3, 129)) + tuple(k << 17 for k in range(2, 33))
+
+
+def dwdb_placement_study(torch, library, cabi, stream, launches: int = 200) -> dict:
+    """C1's backward (atomic dW/db) with grad_weight at the start of a
+    buffer and grad_bias DWDB_OFFSETS bytes after it, against the same
+    backward without the sums: what the 256 blocks' weight/bias atomics add
+    to the kernel for each relative placement of the two sums (the C ABI
+    takes them as two independent pointers)."""
+    runner = Runner(torch, library, cabi, C1, 4, stream)
+    if not parity_self_check(torch, runner)["pass"]:
+        raise SystemExit("bench.py: the timed path misses the parity bars")
+    hidden = C1.hidden
+    pool = torch.zeros((DWDB_OFFSETS[-1] + 4 * hidden) // 4 + 1024, device="cuda",
+                       dtype=torch.float32)
+    points = []
+    for offset in DWDB_OFFSETS:
+        for tensors in runner.sets:
+            tensors["grad_weight"] = pool[:hidden]
+            tensors["grad_bias"] = pool[offset // 4: offset // 4 + hidden]
+        runner._launch_arguments()
+        for index in range(20):
+            runner.step(index)
+        backward = runner.timed(lambda i: runner.backward(i), launches) * 1e3
+        input_grads = runner.timed(lambda i: runner.backward_input_grads(i), launches) * 1e3
+        points.append({"offset_bytes": offset, "backward_us": round(backward, 3),
+                       "input_grads_us": round(input_grads, 3),
+                       "sums_us": round(backward - input_grads, 3)})
+    sums = sorted(point["sums_us"] for point in points)
+    return {"kind": "dwdb_placement", "workload": C1.describe(), "launches": launches,
+            "weight_address_mod_64k": pool.data_ptr() % 65536,
+            "sums_us_median": sums[len(sums) // 2], "points": points}
 
 
 def alternation_study(torch, library, cabi, stream, launches: int = 400) -> dict:

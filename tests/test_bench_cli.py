@@ -27,7 +27,8 @@ def test_help_lists_the_measurement_modes():
                             text=True, timeout=120)
     assert result.returncode == 0
     for flag in ("--steps", "--warmup", "--sweep", "--prenorm", "--reference-table", "--config",
-                 "--ceiling", "--quick", "--traffic-summary", "--char-gpt"):
+                 "--ceiling", "--quick", "--traffic-summary", "--char-gpt", "--alternation",
+                 "--dwdb-placement", "--ab-rows"):
         assert flag in result.stdout
 
 
@@ -176,3 +177,14 @@ def test_ab_row_workloads_are_c1_shaped():
                                                      ab_bf16=False)) == []
     with pytest.raises(SystemExit):
         bench.ab_row_workloads(argparse.Namespace(ab_rows="0", ab_hidden=768, ab_bf16=False))
+
+
+def test_dwdb_placement_distances_cover_the_32k_period():
+    """--dwdb-placement walks grad_bias over every KiB of four 32 KiB periods
+    (from 3 KiB, past C1's 3 KiB arrays) and then coarser distances."""
+    bench = _bench_module()
+    offsets = bench.DWDB_OFFSETS
+    assert list(offsets) == sorted(set(offsets))
+    assert offsets[0] == 3 * 1024 and 4 * 768 <= offsets[0]
+    assert all(k * 1024 in offsets for k in range(3, 129))
+    assert offsets[-1] == 4 << 20
