@@ -179,8 +179,8 @@ C1 = Workload("C1", 8 * 1024, 768, "f16", 0.5, 0.1, seed=1001)
 
 def ab_row_workloads(args) -> list[Workload]:
     """C1-shaped workloads at the --ab-rows row counts: the row sweeps that
-    decided row-count-dependent launch rules (the twelve-wave backward of 768
-    columns) are re-measured through them."""
+    decided row-count-dependent launch rules (the twelve- and nine-wave
+    backwards of 768 and 384 columns) are re-measured through them."""
     rows = [int(value) for value in args.ab_rows.split(",") if value.strip()]
     if any(value <= 0 for value in rows) or args.ab_hidden <= 0:
         raise SystemExit("bench.py: --ab-rows and --ab-hidden take positive integers")
@@ -1485,6 +1485,8 @@ def kernel_name(kernel: str, workload: Workload) -> str:
     runs_wide = hidden == 1024 or (hidden == 768 and workload.rows >= 65536)
     if not forward and backward_twelve_waves(hidden, workload.rows):
         shape = f"rln::TwelveWaveShape<{hidden}>"
+    elif not forward and backward_nine_waves(hidden, workload.rows):
+        shape = f"rln::NineWaveShape<{hidden}>"
     elif hidden in SPECIALIZED_HIDDEN and (forward or not runs_wide):
         lanes = 64 if (hidden // 4) % 64 == 0 else 32
         if forward:
@@ -1509,6 +1511,14 @@ def backward_twelve_waves(hidden: int, rows: int) -> bool:
         return False
     last = rows % teams
     return last == 0 or 2 * last >= teams
+
+
+def backward_nine_waves(hidden: int, rows: int) -> bool:
+    """Whether the backward runs nine-wave blocks (rln_device.h
+    backward_nine_waves): 384 columns over 11520-13056 rows, a third row step
+    of the 256 x 9 two-row teams one-half to five-sixths full."""
+    slots = 256 * 9 * 2
+    return hidden == 384 and 2 * rows >= 5 * slots and 6 * rows <= 17 * slots
 
 
 def forward_ring(rows: int, hidden: int) -> bool:

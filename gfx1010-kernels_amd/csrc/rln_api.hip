@@ -13,7 +13,7 @@
 namespace rln {
 
 RLN_FOR_EACH_FIXED(RLN_DECLARE_FIXED)
-RLN_DECLARE_TWELVE_WAVE_BACKWARD()
+RLN_DECLARE_STAGGERED_BACKWARD()
 RLN_FOR_EACH_WIDE_FORWARD(RLN_DECLARE_WIDE_FORWARD)
 RLN_FOR_EACH_WIDE_BACKWARD(RLN_DECLARE_WIDE_BACKWARD)
 

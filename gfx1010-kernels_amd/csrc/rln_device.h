@@ -334,6 +334,14 @@ struct TwelveWaveShape : FixedShape<H> {
     static constexpr bool kCopyWalk = true;
 };
 
+// The same for rows of two per wave (384 columns): nine-wave blocks, 165
+// VGPRs on the copy walk. Used for the launches backward_nine_waves selects.
+template <int H>
+struct NineWaveShape : FixedShape<H> {
+    static constexpr int kBackwardBlockThreads = 9 * kWaveSize;
+    static constexpr bool kCopyWalk = true;
+};
+
 inline bool specialized_hidden(int64_t hidden) {
     for (const int64_t value : kSpecializedHidden) {
         if (value == hidden) {
@@ -434,6 +442,26 @@ inline bool backward_twelve_waves(int64_t hidden, int64_t rows) {
     return last == 0 || 2 * last >= kTeams;
 }
 
+// The backward of 384 columns (two rows per wave) over 11520-13056 rows runs
+// nine-wave blocks: 2304 teams of two rows, two full row steps and a third
+// one-half to five-sixths full, so that, as with the twelve-wave blocks of
+// 768 columns, some of the blocks end a step early and add their weight/bias
+// sums while the others stream. Measured alternated (bench.py --ab
+// eight=RLN_BWD_NINE_WAVE_384=0, backward with the sums, against eight-wave
+// blocks): the C4 tail [12291, 384] fp32 branch 20.05 -> 19.47 us at p = 0,
+// 20.80 -> 20.00 at p = 0.1; fp16 branch 11520 rows 18.93 -> 18.63, 12291
+// 20.28 -> 19.13, 13000 21.79 -> 20.11. With the third step (nearly) full
+// the blocks end together and the copy walk only costs: 13823 rows 20.68 ->
+// 21.46, 13824 20.70 -> 21.43; with two steps, 7168 rows 13.58 -> 14.11.
+#ifndef RLN_BWD_NINE_WAVE_384
+#define RLN_BWD_NINE_WAVE_384 1
+#endif
+inline bool backward_nine_waves(int64_t hidden, int64_t rows) {
+    constexpr int64_t kRowSlots = RLN_BWD_MAX_BLOCKS * 9 * 2;
+    return RLN_BWD_NINE_WAVE_384 && hidden == 384 && 2 * rows >= 5 * kRowSlots
+        && 6 * rows <= 17 * kRowSlots;
+}
+
 // Backward launches of at least this many elements run rows of 6657-8192
 // columns on sixteen waves of two slots (1024-thread blocks) instead of eight
 // of four: measured 2-4.5 % faster from 2^26 elements ([16384, 8192] 416
@@ -452,8 +480,10 @@ inline ShapeInfo shape_info(int64_t hidden, Pass pass, int64_t rows) {
         && !(pass == Pass::kBackward && backward_runs_wide(hidden, rows))) {
         const int lanes = fixed_lanes(hidden);
         return {kWaveSize / lanes, 1, static_cast<int>(hidden / 4 / lanes), 256,
-                pass == Pass::kBackward && backward_twelve_waves(hidden, rows) ? 12 * kWaveSize
-                                                                              : kBackwardThreads};
+                pass != Pass::kBackward                 ? kBackwardThreads
+                : backward_twelve_waves(hidden, rows) ? 12 * kWaveSize
+                : backward_nine_waves(hidden, rows)   ? 9 * kWaveSize
+                                                      : kBackwardThreads};
     }
     int parts = wide_parts(hidden, pass);
     if (pass == Pass::kBackward && parts == 8 && hidden >= kSixteenWaveBackwardMinHidden
@@ -2205,7 +2235,13 @@ int with_shape(int64_t hidden, int64_t rows, Launch&& launch) {
     switch (hidden) {
         case 128: return launch(FixedShape<128>{});
         case 256: return launch(FixedShape<256>{});
-        case 384: return launch(FixedShape<384>{});
+        case 384:
+            if constexpr (kPass == Pass::kBackward) {
+                if (backward_nine_waves(hidden, rows)) {
+                    return launch(NineWaveShape<384>{});
+                }
+            }
+            return launch(FixedShape<384>{});
         case 512: return launch(FixedShape<512>{});
         case 768:
             if constexpr (kPass == Pass::kBackward) {
@@ -2250,9 +2286,11 @@ int with_shape(int64_t hidden, int64_t rows, Launch&& launch) {
         const ForwardArgs&, FixedShape<H>, int, int, bool);                               \
     extern template int launch_backward_shape<FixedShape<H>>(                            \
         const BackwardArgs&, FixedShape<H>, int, int, bool);
-#define RLN_DECLARE_TWELVE_WAVE_BACKWARD()                                                \
+#define RLN_DECLARE_STAGGERED_BACKWARD()                                                  \
     extern template int launch_backward_shape<TwelveWaveShape<768>>(                     \
-        const BackwardArgs&, TwelveWaveShape<768>, int, int, bool);
+        const BackwardArgs&, TwelveWaveShape<768>, int, int, bool);                        \
+    extern template int launch_backward_shape<NineWaveShape<384>>(                       \
+        const BackwardArgs&, NineWaveShape<384>, int, int, bool);
 #define RLN_DECLARE_WIDE_FORWARD(V, P)                                                    \
     extern template int launch_forward_shape<WideShape<V, P>>(                           \
         const ForwardArgs&, WideShape<V, P>, int, int, bool);

@@ -28,6 +28,10 @@ template int launch_backward_shape<RLN_SHAPE>(const BackwardArgs&, RLN_SHAPE, in
 template int launch_backward_shape<TwelveWaveShape<768>>(const BackwardArgs&,
                                                          TwelveWaveShape<768>, int, int, bool);
 #endif
+#if defined(RLN_HIDDEN) && RLN_HIDDEN == 384
+template int launch_backward_shape<NineWaveShape<384>>(const BackwardArgs&,
+                                                       NineWaveShape<384>, int, int, bool);
+#endif
 #endif
 
 }  // namespace rln

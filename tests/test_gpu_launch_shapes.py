@@ -263,22 +263,18 @@ def test_sixteen_wave_backward_deterministic_and_half_gradient():
 TWELVE_WAVE_CASES = [(2047, False), (2048, True), (4096, False), (5120, True), (7168, False),
                      (8192, True), (9216, True), (9217, False)]
 
+# Row counts of 384 columns around backward_nine_waves: nine-wave blocks of
+# two-row teams for 11520-13056 rows, eight-wave blocks otherwise; 12291 is
+# the C4 tail.
+NINE_WAVE_CASES = [(11519, False), (11520, True), (12291, True), (13056, True), (13057, False)]
 
-@pytest.mark.parametrize("rows,twelve_waves", TWELVE_WAVE_CASES,
-                         ids=[f"{rows}-{'twelve' if twelve else 'eight'}"
-                              for rows, twelve in TWELVE_WAVE_CASES])
-def test_backward_twelve_wave_switch(rows, twelve_waves):
-    """Both sides of the switch between eight- and twelve-wave backward blocks
-    at 768 columns, whole tensors against the oracle; deterministic mode
+
+def _check_staggered_backward(rows, hidden, branch_dtype):
+    """Whole tensors of the backward against the oracle; deterministic mode
     replays bitwise, and its input gradients equal the atomic mode's."""
     from test_gpu_backward import deterministic_algorithms
 
-    hidden = 768
-    teams = 256 * 12
-    last = rows % teams
-    assert (2048 <= rows <= 3 * teams and (last == 0 or 2 * last >= teams)) == twelve_waves
-    print(f"[launch shapes] backward rows={rows} H={hidden} twelve={twelve_waves}", flush=True)
-    inputs, grads = device_inputs(rows, hidden, torch.float16, seed=13 * hidden + rows)
+    inputs, grads = device_inputs(rows, hidden, branch_dtype, seed=13 * hidden + rows)
     torch.cuda.manual_seed(13 * hidden + rows)
     seed, offset = generator_state()
     outputs = _C.residual_layer_norm_forward(*inputs, 0.1, EPS, True, 128)
@@ -286,7 +282,7 @@ def test_backward_twelve_wave_switch(rows, twelve_waves):
     def backward():
         return _C.residual_layer_norm_backward(
             grads[0], grads[1], outputs[0], inputs[2], outputs[2], outputs[3], outputs[4], 0.1,
-            True, True, 128, 64, 64, 1, True, torch.float16)
+            True, True, 128, 64, 64, 1, True, branch_dtype)
 
     with deterministic_algorithms(False):
         atomic = backward()
@@ -299,3 +295,30 @@ def test_backward_twelve_wave_switch(rows, twelve_waves):
         assert torch.equal(a, b)
     assert torch.equal(first[0], atomic[0]) and torch.equal(first[1], atomic[1])
     check_parameter_gradients(outputs[0], grads[1], first)
+
+
+@pytest.mark.parametrize("rows,twelve_waves", TWELVE_WAVE_CASES,
+                         ids=[f"{rows}-{'twelve' if twelve else 'eight'}"
+                              for rows, twelve in TWELVE_WAVE_CASES])
+def test_backward_twelve_wave_switch(rows, twelve_waves):
+    """Both sides of the switch between eight- and twelve-wave backward blocks
+    at 768 columns."""
+    hidden = 768
+    teams = 256 * 12
+    last = rows % teams
+    assert (2048 <= rows <= 3 * teams and (last == 0 or 2 * last >= teams)) == twelve_waves
+    print(f"[launch shapes] backward rows={rows} H={hidden} twelve={twelve_waves}", flush=True)
+    _check_staggered_backward(rows, hidden, torch.float16)
+
+
+@pytest.mark.parametrize("rows,nine_waves", NINE_WAVE_CASES,
+                         ids=[f"{rows}-{'nine' if nine else 'eight'}"
+                              for rows, nine in NINE_WAVE_CASES])
+def test_backward_nine_wave_switch(rows, nine_waves):
+    """Both sides of the switch between eight- and nine-wave backward blocks
+    at 384 columns, with the C4 tail's fp32 branch."""
+    hidden = 384
+    slots = 256 * 9 * 2
+    assert (2 * rows >= 5 * slots and 6 * rows <= 17 * slots) == nine_waves
+    print(f"[launch shapes] backward rows={rows} H={hidden} nine={nine_waves}", flush=True)
+    _check_staggered_backward(rows, hidden, torch.float32)
