@@ -1478,8 +1478,9 @@ def kernel_name(kernel: str, workload: Workload) -> str:
     aligned access path. Mirrors the dispatch of rln_device.h: the specialized
     sizes' lanes per row (the forward's forward_lanes), and the run-time-length
     shapes each pass runs, 1024's backward and that of 768 columns from 65536
-    rows among them (backward_runs_wide), and the sixteen-wave backward of
-    large launches of 6657-8192 columns."""
+    rows among them (backward_runs_wide), the sixteen-wave backward of large
+    launches of 6657-8192 columns, and the twelve-, nine- and twelve-wave
+    (four waves per row, at most 8192 rows) backwards of small launches."""
     forward = kernel == "rln_forward_kernel"
     hidden = workload.hidden
     runs_wide = hidden == 1024 or (hidden == 768 and workload.rows >= 65536)
@@ -1495,7 +1496,10 @@ def kernel_name(kernel: str, workload: Workload) -> str:
     else:
         parts = wide_parts(hidden, kernel, workload.rows)
         vectors = -(-hidden // (256 * parts))
-        shape = f"rln::WideShape<{vectors}, {parts}>"
+        if not forward and parts == 4 and vectors <= 2 and workload.rows <= 8192:
+            shape = f"rln::StaggeredWideShape<{vectors}>"
+        else:
+            shape = f"rln::WideShape<{vectors}, {parts}>"
     types = {"f32": "float", "f16": "_Float16", "bf16": "__bf16"}
     ring = ", true" if forward_ring(workload.rows, hidden) else ", false"
     return (f"rln::{kernel}<{shape}, {types[workload.branch]}, "

@@ -324,6 +324,14 @@ struct WideShape {
     __host__ __device__ float inv_hidden() const { return inv_hidden_; }
 };
 
+// The backward of rows of four waves and one or two slots per lane (769-1024
+// and 1217-2048 columns) in twelve-wave blocks, three rows per block step:
+// the launches of at most kStaggeredWideMaxRows rows (shape_info).
+template <int V>
+struct StaggeredWideShape : WideShape<V, 4> {
+    static constexpr int kBackwardBlockThreads = 12 * kWaveSize;
+};
+
 // The backward of a specialized size in twelve-wave blocks (one row per
 // wave, one block per CU) walking its rows with the copy walk: the ring walk
 // needs ~200 VGPRs at 768 columns and spills at the 168 a twelve-wave block
@@ -462,6 +470,26 @@ inline bool backward_nine_waves(int64_t hidden, int64_t rows) {
         && 6 * rows <= 17 * kRowSlots;
 }
 
+// Backward launches of at most 8192 rows of four waves and one or two slots
+// (769-1024 and 1217-2048 columns) run twelve-wave blocks instead of eight:
+// their waves already walk with the copy walk (multi-wave rows), in the 162-
+// 166 VGPRs that three waves per SIMD allow, so the larger blocks cost the
+// input gradients little and give the grid a last row step a third or two
+// thirds full where eight-wave blocks end together. Measured alternated
+// (bench.py --ab eight=RLN_BWD_STAGGERED_WIDE=0 --ab-rows ... --ab-hidden H,
+// backward with the sums): 1600 columns 1024 rows 14.61 -> 12.70 us, 2048
+// 17.08 -> 15.16, 4096 24.85 -> 23.45, 6144 36.82 -> 33.81, 8192 45.23 ->
+// 42.02; 1024 columns 2048 rows 13.68 -> 12.37, 4096 19.38 -> 18.01, 6144
+// 24.47 -> 23.36, 8192 30.10 -> 29.33; 832 columns 4096 rows 18.48 -> 16.47,
+// 8192 27.74 -> 24.56; 2048 columns 4096 rows 30.20 -> 29.58, 8192 52.07 ->
+// 52.65. Larger launches lose (1024 columns: 12288 rows +0.7 %, 16384
+// +1.6 %; [262144, 1600] +5.7 %), and so do rows of three slots (2432
+// columns, 4096 rows 35.4 -> 41.9 us).
+#ifndef RLN_BWD_STAGGERED_WIDE
+#define RLN_BWD_STAGGERED_WIDE 1
+#endif
+constexpr int64_t kStaggeredWideMaxRows = 8192;
+
 // Backward launches of at least this many elements run rows of 6657-8192
 // columns on sixteen waves of two slots (1024-thread blocks) instead of eight
 // of four: measured 2-4.5 % faster from 2^26 elements ([16384, 8192] 416
@@ -492,9 +520,14 @@ inline ShapeInfo shape_info(int64_t hidden, Pass pass, int64_t rows) {
     }
     const int64_t per_slot = 4 * kWaveSize * parts;
     const int vectors = static_cast<int>((hidden + per_slot - 1) / per_slot);
+    const bool staggered = pass == Pass::kBackward && RLN_BWD_STAGGERED_WIDE && parts == 4
+        && vectors <= 2 && rows <= kStaggeredWideMaxRows;
     return {1, parts, vectors, parts == 3 ? 6 * kWaveSize : parts > 4 ? parts * kWaveSize : 256,
-            parts == 3 ? 12 * kWaveSize : parts == 16 ? 16 * kWaveSize : kBackwardThreads};
+            parts == 3 || staggered ? 12 * kWaveSize
+            : parts == 16           ? 16 * kWaveSize
+                                    : kBackwardThreads};
 }
+
 
 // Blocks for a launch over `rows`: each block works on
 // (threads / 64) * rows_per_wave / parts rows at a time, and gets enough
@@ -2272,6 +2305,14 @@ int with_shape(int64_t hidden, int64_t rows, Launch&& launch) {
             default: break;
         }
     } else {
+        if (info.parts == 4 && info.backward_threads == 12 * kWaveSize) {
+            if (info.vectors == 1) {
+                return launch(StaggeredWideShape<1>{{hidden, inv_hidden}});
+            }
+            if (info.vectors == 2) {
+                return launch(StaggeredWideShape<2>{{hidden, inv_hidden}});
+            }
+        }
         switch (info.parts * 16 + info.vectors) {
             RLN_FOR_EACH_WIDE_BACKWARD(RLN_WIDE_CASE)
             default: break;
@@ -2290,7 +2331,11 @@ int with_shape(int64_t hidden, int64_t rows, Launch&& launch) {
     extern template int launch_backward_shape<TwelveWaveShape<768>>(                     \
         const BackwardArgs&, TwelveWaveShape<768>, int, int, bool);                        \
     extern template int launch_backward_shape<NineWaveShape<384>>(                       \
-        const BackwardArgs&, NineWaveShape<384>, int, int, bool);
+        const BackwardArgs&, NineWaveShape<384>, int, int, bool);                          \
+    extern template int launch_backward_shape<StaggeredWideShape<1>>(                    \
+        const BackwardArgs&, StaggeredWideShape<1>, int, int, bool);                       \
+    extern template int launch_backward_shape<StaggeredWideShape<2>>(                    \
+        const BackwardArgs&, StaggeredWideShape<2>, int, int, bool);
 #define RLN_DECLARE_WIDE_FORWARD(V, P)                                                    \
     extern template int launch_forward_shape<WideShape<V, P>>(                           \
         const ForwardArgs&, WideShape<V, P>, int, int, bool);

@@ -32,6 +32,10 @@ template int launch_backward_shape<TwelveWaveShape<768>>(const BackwardArgs&,
 template int launch_backward_shape<NineWaveShape<384>>(const BackwardArgs&,
                                                        NineWaveShape<384>, int, int, bool);
 #endif
+#if defined(RLN_WIDE_P) && RLN_WIDE_P == 4 && RLN_WIDE_V <= 2
+template int launch_backward_shape<StaggeredWideShape<RLN_WIDE_V>>(
+    const BackwardArgs&, StaggeredWideShape<RLN_WIDE_V>, int, int, bool);
+#endif
 #endif
 
 }  // namespace rln

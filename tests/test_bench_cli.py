@@ -45,7 +45,9 @@ def test_unknown_config_is_refused_with_the_list_of_names():
 def test_kernel_names_follow_the_library_backward_shapes():
     """bench.py labels the dominant kernel with the shape the library runs;
     the backward's waves per row are visible through the C ABI's workspace
-    size (one partial per block; 8-wave blocks hold 8 / parts rows)."""
+    size (one partial per block; 8-wave blocks hold 8 / parts rows, the
+    12-wave blocks of four-wave rows of one or two slots at small launches
+    12 / 4)."""
     import importlib.util
 
     from gfx1010_kernels import _cabi
@@ -54,13 +56,18 @@ def test_kernel_names_follow_the_library_backward_shapes():
     bench = importlib.util.module_from_spec(spec)
     sys.modules["bench_under_test"] = bench
     spec.loader.exec_module(bench)
-    rows = 41
-    for hidden in range(128, 8193, 64):
-        if hidden in bench.SPECIALIZED_HIDDEN and hidden != 1024:
-            continue
-        blocks = _cabi.backward_workspace_bytes(rows, hidden, True) // (2 * hidden * 4)
-        parts = bench.wide_parts(hidden, "rln_backward_kernel")
-        assert blocks == -(-rows // (8 // parts)), hidden
+    from dataclasses import replace
+
+    for rows in (41, 8192, 8193):
+        for hidden in range(128, 8193, 64):
+            if hidden in bench.SPECIALIZED_HIDDEN and hidden != 1024:
+                continue
+            blocks = _cabi.backward_workspace_bytes(rows, hidden, True) // (2 * hidden * 4)
+            parts = bench.wide_parts(hidden, "rln_backward_kernel", rows)
+            name = bench.kernel_name("rln_backward_kernel",
+                                     replace(bench.C1, hidden=hidden, rows=rows))
+            waves = 12 if "StaggeredWideShape" in name or parts == 3 else 16 if parts == 16 else 8
+            assert blocks == min(-(-rows // (waves // parts)), 256), (rows, hidden, name)
 
 
 def _bench_module():

@@ -75,16 +75,20 @@ def test_size_queries():
     assert _cabi.backward_workspace_bytes(37, 128, True) == 3 * 2 * 128 * 4
     assert _cabi.backward_workspace_bytes(41, 768, True) == 6 * 2 * 768 * 4
     assert _cabi.backward_workspace_bytes(1 << 20, 1024, True) == 256 * 2 * 1024 * 4
-    # The backward of 1024 columns runs 4 waves per row (2 rows per block).
-    assert _cabi.backward_workspace_bytes(41, 1024, True) == 21 * 2 * 1024 * 4
+    # The backward of 1024 columns runs 4 waves per row: 2 rows per 8-wave
+    # block, and 3 per 12-wave block up to 8192 rows.
+    assert _cabi.backward_workspace_bytes(41, 1024, True) == 14 * 2 * 1024 * 4
+    assert _cabi.backward_workspace_bytes(8193, 1024, True) == 256 * 2 * 1024 * 4
+    assert _cabi.backward_workspace_bytes(600, 1024, True) == 200 * 2 * 1024 * 4
     # Run-time row lengths in the backward: one wave per row up to 768, 4 up to
     # 1024, 2 up to 1216, 4 up to 2432, else 8 waves per row (8, 4, 2 or 1 rows
-    # per 8-wave block).
+    # per 8-wave block); four-wave rows of one or two slots (769-1024 and
+    # 1217-2048 columns) in 12-wave blocks up to 8192 rows.
     assert _cabi.backward_workspace_bytes(41, 640, True) == 6 * 2 * 640 * 4
-    assert _cabi.backward_workspace_bytes(41, 896, True) == 21 * 2 * 896 * 4
+    assert _cabi.backward_workspace_bytes(41, 896, True) == 14 * 2 * 896 * 4
     assert _cabi.backward_workspace_bytes(41, 1216, True) == 11 * 2 * 1216 * 4
-    assert _cabi.backward_workspace_bytes(41, 1280, True) == 21 * 2 * 1280 * 4
-    assert _cabi.backward_workspace_bytes(41, 2048, True) == 21 * 2 * 2048 * 4
+    assert _cabi.backward_workspace_bytes(41, 1280, True) == 14 * 2 * 1280 * 4
+    assert _cabi.backward_workspace_bytes(41, 2048, True) == 14 * 2 * 2048 * 4
     assert _cabi.backward_workspace_bytes(41, 2432, True) == 21 * 2 * 2432 * 4
     assert _cabi.backward_workspace_bytes(41, 2496, True) == 41 * 2 * 2496 * 4
     assert _cabi.backward_workspace_bytes(41, 4096, True) == 41 * 2 * 4096 * 4

@@ -17,7 +17,7 @@ against a float64 reduction.
 import pytest
 import torch
 
-from gfx1010_kernels import _C
+from gfx1010_kernels import _C, _cabi
 from parity import check_full_tensor, generator_state
 from test_gpu_configs import check_parameter_gradients, device_inputs
 
@@ -269,9 +269,11 @@ TWELVE_WAVE_CASES = [(2047, False), (2048, True), (4096, False), (5120, True), (
 NINE_WAVE_CASES = [(11519, False), (11520, True), (12291, True), (13056, True), (13057, False)]
 
 
-def _check_staggered_backward(rows, hidden, branch_dtype):
+def _check_staggered_backward(rows, hidden, branch_dtype, mask_threads=128):
     """Whole tensors of the backward against the oracle; deterministic mode
-    replays bitwise, and its input gradients equal the atomic mode's."""
+    replays bitwise, and its input gradients equal the atomic mode's.
+    `mask_threads`: the dropout layout the forward draws (0 at the hidden
+    sizes that only have the library's own)."""
     from test_gpu_backward import deterministic_algorithms
 
     inputs, grads = device_inputs(rows, hidden, branch_dtype, seed=13 * hidden + rows)
@@ -287,7 +289,7 @@ def _check_staggered_backward(rows, hidden, branch_dtype):
     with deterministic_algorithms(False):
         atomic = backward()
     check_full_tensor(inputs, grads, outputs, atomic, 0.1, EPS, seed, offset,
-                      what=f"{rows} x {hidden}")
+                      threads=mask_threads, what=f"{rows} x {hidden}")
     check_parameter_gradients(outputs[0], grads[1], atomic)
     with deterministic_algorithms(True):
         first, second = backward(), backward()
@@ -322,3 +324,30 @@ def test_backward_nine_wave_switch(rows, nine_waves):
     assert (2 * rows >= 5 * slots and 6 * rows <= 17 * slots) == nine_waves
     print(f"[launch shapes] backward rows={rows} H={hidden} nine={nine_waves}", flush=True)
     _check_staggered_backward(rows, hidden, torch.float32)
+
+
+# Four-wave rows of one or two slots per lane (769-1024 and 1217-2048
+# columns) run their backward in twelve-wave blocks (StaggeredWideShape) up
+# to 8192 rows; rows of three slots (2049-2432 columns) and of two waves
+# (1025-1216) keep eight-wave blocks.
+STAGGERED_WIDE_CASES = [(1600, 100, True), (1600, 8192, True), (1600, 8193, False),
+                        (1024, 8192, True), (1024, 8193, False), (832, 4096, True),
+                        (2432, 4096, False), (1216, 4096, False)]
+
+
+@pytest.mark.parametrize("hidden,rows,staggered", STAGGERED_WIDE_CASES,
+                         ids=[f"{hidden}x{rows}-{'twelve' if staggered else 'eight'}"
+                              for hidden, rows, staggered in STAGGERED_WIDE_CASES])
+def test_backward_staggered_wide_switch(hidden, rows, staggered):
+    """Both sides of the switch between eight- and twelve-wave blocks for the
+    backward of four-wave rows: the workspace query counts three rows per
+    twelve-wave block, and whole tensors match the oracle either way."""
+    per_slot = 4 * 64 * 4
+    vectors = -(-hidden // per_slot)
+    parts = 4 if (768 < hidden <= 1024 or 1216 < hidden <= 2432) else 2
+    assert (parts == 4 and vectors <= 2 and rows <= 8192) == staggered
+    rows_per_block = 3 if staggered else 8 // parts
+    blocks = min(-(-rows // rows_per_block), 256)
+    assert _cabi.backward_workspace_bytes(rows, hidden, True) == blocks * 2 * hidden * 4
+    print(f"[launch shapes] backward rows={rows} H={hidden} staggered={staggered}", flush=True)
+    _check_staggered_backward(rows, hidden, torch.float16, mask_threads=128 if hidden == 1024 else 0)
