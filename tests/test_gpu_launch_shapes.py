@@ -351,3 +351,38 @@ def test_backward_staggered_wide_switch(hidden, rows, staggered):
     assert _cabi.backward_workspace_bytes(rows, hidden, True) == blocks * 2 * hidden * 4
     print(f"[launch shapes] backward rows={rows} H={hidden} staggered={staggered}", flush=True)
     _check_staggered_backward(rows, hidden, torch.float16, mask_threads=128 if hidden == 1024 else 0)
+
+
+# One launch of each staggered backward shape (TwelveWaveShape<768>,
+# NineWaveShape<384>, StaggeredWideShape<2> and <1>), with the branch type
+# each serves in the sweep.
+STAGGERED_SHAPES = [(768, 8192, torch.float16), (384, 12291, torch.float32),
+                    (1600, 4096, torch.float16), (1024, 4096, torch.float16)]
+
+
+@pytest.mark.parametrize("hidden,rows,branch_dtype", STAGGERED_SHAPES,
+                         ids=[f"{hidden}x{rows}" for hidden, rows, _ in STAGGERED_SHAPES])
+def test_staggered_backward_element_access_matches_vector_access(hidden, rows, branch_dtype):
+    """The element-access instance of each staggered backward shape (taken
+    when a tensor is not 16-byte aligned) gives the vector instance's bits,
+    deterministic mode."""
+    from parity import assert_bitwise, host, make_grads, make_inputs
+    from test_gpu_backward import deterministic_algorithms, raw_backward
+
+    print(f"[launch shapes] misaligned backward rows={rows} H={hidden}", flush=True)
+    inputs = make_inputs((rows, hidden), branch_dtype, seed=hidden + rows)
+    torch.cuda.manual_seed(hidden)
+    outputs = _C.residual_layer_norm_forward(*inputs, 0.1, EPS, True, 128)
+    grad_updated, grad_normalized = make_grads((rows, hidden), seed=hidden + rows + 1)
+    storage = torch.empty(rows * hidden + 1, device="cuda")
+    misaligned = storage[1:].view(rows, hidden)
+    misaligned.copy_(grad_updated)
+    assert misaligned.data_ptr() % 16 != 0
+    with deterministic_algorithms(True):
+        aligned = raw_backward(grad_updated, grad_normalized, outputs, inputs[2], 0.1,
+                               branch_dtype)
+        element = raw_backward(misaligned, grad_normalized, outputs, inputs[2], 0.1,
+                               branch_dtype)
+    for a, b, name in zip(aligned, element, ("grad_x", "grad_branch", "grad_weight",
+                                             "grad_bias")):
+        assert_bitwise(host(b), host(a), f"{rows} x {hidden} {name}")
